@@ -1,0 +1,143 @@
+// Internal types of the HIP backend: context, buffers, pooled device memory.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <vector>
+
+#include "../../include/minifield_hip.h"
+
+namespace mfh {
+
+// Packed stream formats (crates/kernels-simd/src/lib.rs:87-108).
+enum class Format : int { Ternary = 0, Nf4 = 1, Int8 = 2 };
+
+__host__ __device__ constexpr int weights_per_byte(Format f)
+{
+    return f == Format::Ternary ? 4 : f == Format::Nf4 ? 2 : 1;
+}
+
+// Error carrier: the status plus a static message, like ExecutorError's
+// `&'static str` payloads.
+struct Error {
+    mfh_status status;
+    const char *message;
+};
+
+// Size-bucketed caching allocator over hipMalloc.  All device work of a
+// context runs on one stream, so a block released by the host can be handed
+// to the next allocation immediately: any later use is stream-ordered after
+// every use already queued.
+class Pool {
+public:
+    explicit Pool(int device) : device_(device) {}
+    ~Pool();
+    void *acquire(size_t bytes, size_t *capacity);
+    void release(void *ptr, size_t capacity);
+    size_t reserved() const { return reserved_; }
+
+private:
+    int device_;
+    size_t reserved_ = 0;
+    std::multimap<size_t, void *> free_;
+    std::vector<void *> all_;
+};
+
+size_t pool_bucket(size_t bytes);
+
+}  // namespace mfh
+
+struct mfh_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    mfh_backend_identity identity{};
+    mfh_limits limits{};
+    uint64_t live_by_class[4] = {0, 0, 0, 0};
+    uint64_t live_bytes = 0;
+    uint64_t peak_bytes = 0;
+    uint64_t pending_result_bytes = 0;
+    uint32_t pending_operations = 0;
+    bool cancel_requested = false;
+    const char *last_error = "no error";
+    int kernel_path = 0;
+    int cu_count = 256;
+    std::unique_ptr<mfh::Pool> pool;
+    // Small device scratch for staged host token ids and per-call partials;
+    // reused in stream order.
+    void *ids_scratch = nullptr;
+    size_t ids_scratch_capacity = 0;
+    void *work_scratch = nullptr;
+    size_t work_scratch_capacity = 0;
+};
+
+struct mfh_buf {
+    mfh_ctx *ctx = nullptr;
+    uint64_t generation = 0;
+    mfh_dtype dtype = MFH_DTYPE_F32;
+    uint32_t rank = 0;
+    uint64_t dims[4] = {0, 0, 0, 0};
+    uint64_t elements = 0;
+    uint64_t bytes = 0;
+    mfh_alloc_class cls = MFH_CLASS_SCRATCH;
+    void *dev = nullptr;
+    size_t capacity = 0;
+    // U8 streams: whether any byte equals 0x80 (the reserved INT8 code),
+    // scanned once at upload (backend-cpu/src/packed.rs:205 scans per call).
+    bool has_int8_reserved = false;
+    // F32 uploads whose every value is exactly representable in binary16 keep
+    // a binary16 copy; packed kernels read scales from it.  Any write to the
+    // buffer by an operation drops it.
+    void *f16_shadow = nullptr;
+    size_t f16_capacity = 0;
+    // Backend-private repacked copy of a U8 code stream, built on the first
+    // packed operation that fixes its format.
+    void *repacked = nullptr;
+    size_t repacked_capacity = 0;
+    int repacked_format = -1;
+};
+
+struct mfh_fence {
+    mfh_ctx *ctx = nullptr;
+    hipEvent_t event = nullptr;
+    bool cancelled = false;
+    bool consumed = false;
+};
+
+struct mfh_readback {
+    mfh_ctx *ctx = nullptr;
+    hipEvent_t event = nullptr;
+    float *host = nullptr;
+    size_t count = 0;
+    bool consumed = false;
+    bool cancelled = false;
+};
+
+namespace mfh {
+
+// Record an error on the context and return its status.
+mfh_status fail(mfh_ctx *ctx, mfh_status status, const char *message);
+inline mfh_status fail(mfh_ctx *ctx, const Error &e) { return fail(ctx, e.status, e.message); }
+
+// Buffer admission (backend-cpu/src/storage.rs:295-375, minus the per-call
+// finite scan, which deferred device backends do not perform).
+mfh_status check_buffer(mfh_ctx *ctx, const mfh_buf *buf);
+mfh_status check_f32(mfh_ctx *ctx, const mfh_buf *buf);
+mfh_status check_u8(mfh_ctx *ctx, const mfh_buf *buf);
+mfh_status check_output(mfh_ctx *ctx, const mfh_buf *buf, const uint64_t *dims, uint32_t rank);
+mfh_status check_operation(mfh_ctx *ctx, mfh_operation op);
+
+// Drop derived copies of a buffer whose contents an operation overwrites.
+void mark_written(mfh_buf *buf);
+
+// Device scratch owned by the context, grown on demand (stream ordered).
+void *ids_scratch(mfh_ctx *ctx, size_t bytes);
+void *work_scratch(mfh_ctx *ctx, size_t bytes);
+
+// Fill `count` floats with `value` on the context stream (a kernel, so the
+// call is capturable; no hipMemsetAsync).
+void launch_fill_f32(hipStream_t stream, float *dst, size_t count, float value);
+
+}  // namespace mfh

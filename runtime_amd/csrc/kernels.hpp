@@ -1,0 +1,62 @@
+// Launch interface between the host admission code and the HIP kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "internal.hpp"
+
+namespace mfh {
+
+// One packed weight stream as the kernels see it.
+struct PackedStream {
+    const uint8_t *codes = nullptr;     // canonical [n, k / wpb] row-major codes
+    const float *scales = nullptr;      // f32 [n, k / 128]
+    const uint16_t *scales16 = nullptr; // binary16 copy of `scales`, or null
+    const uint8_t *tiles = nullptr;     // backend-private repacked codes, or null
+};
+
+enum class Epilogue : int {
+    Single = 0,     // out_a = x . a
+    Pair = 1,       // out_a = x . a, out_b = x . b
+    SwigluPair = 2, // out_a = silu(x . a) * (x . b)
+};
+
+struct PackedCall {
+    Format format = Format::Ternary;
+    Epilogue epilogue = Epilogue::Single;
+    uint32_t m = 0;  // activation rows
+    uint32_t n = 0;  // weight rows (outputs per activation row)
+    uint32_t k = 0;  // inner width, multiple of 128
+    const float *x = nullptr;  // [m, k]
+    PackedStream a, b;
+    float *out_a = nullptr;  // [m, n]
+    float *out_b = nullptr;  // [m, n] (Pair only)
+};
+
+// Decode GEMV for m <= 8 on FP32 FMA units.
+void launch_gemv_fma(hipStream_t stream, const PackedCall &call);
+// Matrix-core decode GEMV for m <= 8 (needs `tiles` on both streams).
+void launch_gemv_mfma(hipStream_t stream, const PackedCall &call, void *scratch);
+size_t gemv_mfma_scratch_bytes(const PackedCall &call);
+// Repack a canonical code stream into the private tile layout.
+size_t repacked_bytes(Format format, uint32_t n, uint32_t k);
+void launch_repack(hipStream_t stream, Format format, const uint8_t *codes, uint8_t *tiles,
+                   uint32_t n, uint32_t k);
+
+// Prefill GEMM for larger m: LDS-staged dequantized tiles with FP32 FMA.
+void launch_gemm_fma(hipStream_t stream, const PackedCall &call);
+
+// out[i] = silu(gate[i]) * up[i], the reference's SwiGLU staging
+// (backend-cpu/src/packed.rs:431-441).
+void launch_swiglu(hipStream_t stream, float *out, const float *gate, const float *up,
+                   size_t count);
+
+// Dequantize selected rows.  `ids` are f32 row selectors (device ids or
+// staged host ids); invalid or out-of-range ids produce a NaN row.
+void launch_packed_gather(hipStream_t stream, Format format, float *out, const uint8_t *codes,
+                          const float *scales, const float *ids, uint32_t count, uint32_t rows,
+                          uint32_t k);
+
+}  // namespace mfh

@@ -1,0 +1,374 @@
+// Packed-weight operations: admission and kernel selection.
+//
+// Admission restates CpuBackend's checks in the reference's order and with
+// its messages (crates/backend-cpu/src/packed.rs:11-466): every operand is
+// validated before anything is enqueued, so a rejected call writes nothing.
+#include <vector>
+
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace mfh {
+namespace {
+
+struct DeviceGuard {
+    int previous = 0;
+    explicit DeviceGuard(int device)
+    {
+        (void)hipGetDevice(&previous);
+        if (previous != device)
+            (void)hipSetDevice(device);
+    }
+    ~DeviceGuard() { hipSetDevice(previous); }
+};
+
+struct Packed {
+    uint32_t rows = 0;
+    uint32_t inner = 0;
+    Format format = Format::Ternary;
+};
+
+bool same_shape(const mfh_buf *a, const mfh_buf *b)
+{
+    if (!a || !b || a->rank != b->rank)
+        return false;
+    for (uint32_t i = 0; i < a->rank; ++i)
+        if (a->dims[i] != b->dims[i])
+            return false;
+    return true;
+}
+
+// check_packed_operands, backend-cpu/src/packed.rs:177-220.
+mfh_status check_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales, Packed *out)
+{
+    mfh_status s = check_u8(ctx, codes);
+    if (!s)
+        s = check_f32(ctx, scales);
+    if (s)
+        return s;
+    if (codes->rank != 2 || scales->rank != 2)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed weight streams must be rank two");
+    uint64_t code_width = codes->dims[1];
+    uint64_t groups = scales->dims[1];
+    if (groups > UINT64_MAX / 128)
+        return fail(ctx, MFH_OVERFLOW, "packed inner width overflows usize");
+    uint64_t inner = groups * 128;
+    if (code_width == inner / 4) {
+        out->format = Format::Ternary;
+    } else if (code_width == inner / 2) {
+        out->format = Format::Nf4;
+    } else if (code_width == inner) {
+        if (codes->has_int8_reserved)
+            return fail(ctx, MFH_INVALID_ARGUMENT, "INT8 -128 code is reserved");
+        out->format = Format::Int8;
+    } else {
+        return fail(ctx, MFH_INVALID_SHAPE,
+                    "packed code width must be inner/4 (ternary), inner/2 (nf4), or inner (int8)");
+    }
+    if (scales->dims[0] != codes->dims[0])
+        return fail(ctx, MFH_INVALID_SHAPE, "packed codes and scales disagree on row count");
+    if (codes->dims[0] > UINT32_MAX || inner > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "packed stream exceeds the 32-bit kernel index range");
+    out->rows = uint32_t(codes->dims[0]);
+    out->inner = uint32_t(inner);
+    return MFH_OK;
+}
+
+bool aliases(const mfh_buf *out, std::initializer_list<const mfh_buf *> inputs)
+{
+    for (const mfh_buf *in : inputs)
+        if (in && out->dev && in->dev == out->dev)
+            return true;
+    return false;
+}
+
+PackedStream stream_of(const mfh_buf *codes, const mfh_buf *scales)
+{
+    PackedStream s;
+    s.codes = static_cast<const uint8_t *>(codes->dev);
+    s.scales = static_cast<const float *>(scales->dev);
+    s.scales16 = static_cast<const uint16_t *>(scales->f16_shadow);
+    return s;
+}
+
+// Enqueue the kernels of one admitted packed product.
+mfh_status run_packed(mfh_ctx *ctx, PackedCall call)
+{
+    hipStream_t stream = ctx->stream;
+    if (call.m == 0 || call.n == 0)
+        return MFH_OK;
+    if (call.k == 0) {
+        // An empty contraction: every row dot is 0, silu(0) * 0 is 0.
+        launch_fill_f32(stream, call.out_a, size_t(call.m) * call.n, 0.0f);
+        if (call.epilogue == Epilogue::Pair)
+            launch_fill_f32(stream, call.out_b, size_t(call.m) * call.n, 0.0f);
+        return MFH_OK;
+    }
+    if (call.m <= 8)
+        launch_gemv_fma(stream, call);
+    else
+        launch_gemm_fma(stream, call);
+    if (hipGetLastError() != hipSuccess)
+        return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
+    return MFH_OK;
+}
+
+}  // namespace
+}  // namespace mfh
+
+using namespace mfh;
+
+extern "C" {
+
+mfh_status mfh_packed_gather_rows(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *codes,
+                                  const mfh_buf *scales, const uint32_t *host_ids,
+                                  size_t host_count, const mfh_buf *device_ids)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    mfh_status s = check_operation(ctx, MFH_OP_PACKED_GATHER_ROWS);
+    if (s)
+        return s;
+    Packed p;
+    if ((s = check_packed(ctx, codes, scales, &p)))
+        return s;
+    if ((s = check_f32(ctx, output)))
+        return s;
+    if (device_ids && host_ids)
+        return fail(ctx, MFH_INVALID_ARGUMENT, "token ids must be either host or device ids");
+    uint64_t count = 0;
+    if (device_ids) {
+        if ((s = check_f32(ctx, device_ids)))
+            return s;
+        if (device_ids->rank != 1)
+            return fail(ctx, MFH_INVALID_SHAPE, "device token-id buffer must be rank one");
+        count = device_ids->dims[0];
+    } else {
+        if (host_count && !host_ids)
+            return fail(ctx, MFH_INVALID_ARGUMENT, "host id pointer is null");
+        for (size_t i = 0; i < host_count; ++i)
+            if (host_ids[i] >= p.rows || host_ids[i] >= (1u << 24))
+                return fail(ctx, MFH_OUT_OF_BOUNDS, "gather identifier exceeds row count");
+        count = host_count;
+    }
+    uint64_t dims[2] = {count, p.inner};
+    if (output->rank != 2 || output->dims[0] != dims[0] || output->dims[1] != dims[1])
+        return fail(ctx, MFH_INVALID_SHAPE, "packed gather output layout differs from required shape");
+    if (aliases(output, {codes, scales, device_ids}))
+        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
+    if (count > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "gather id count exceeds the kernel index range");
+    DeviceGuard guard(ctx->device);
+    mark_written(output);
+    if (count == 0 || p.inner == 0)
+        return MFH_OK;
+    const float *ids = nullptr;
+    if (device_ids) {
+        ids = static_cast<const float *>(device_ids->dev);
+    } else {
+        // Host ids travel as exact f32 row selectors (< 2^24 by admission).
+        std::vector<float> staged(host_count);
+        for (size_t i = 0; i < host_count; ++i)
+            staged[i] = float(host_ids[i]);
+        void *dst = ids_scratch(ctx, host_count * sizeof(float));
+        if (!dst)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        if (hipMemcpyAsync(dst, staged.data(), host_count * sizeof(float), hipMemcpyHostToDevice,
+                           ctx->stream) != hipSuccess) {
+            (void)hipGetLastError();
+            return fail(ctx, MFH_BACKEND_FAILURE, "host to device copy failed");
+        }
+        ids = static_cast<const float *>(dst);
+    }
+    launch_packed_gather(ctx->stream, p.format, static_cast<float *>(output->dev),
+                         static_cast<const uint8_t *>(codes->dev),
+                         static_cast<const float *>(scales->dev), ids, uint32_t(count), p.rows,
+                         p.inner);
+    if (hipGetLastError() != hipSuccess)
+        return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
+    return MFH_OK;
+}
+
+mfh_status mfh_packed_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                             const mfh_buf *codes, const mfh_buf *scales)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    mfh_status s = check_operation(ctx, MFH_OP_PACKED_LINEAR);
+    if (!s)
+        s = check_f32(ctx, input);
+    if (s)
+        return s;
+    Packed p;
+    if ((s = check_packed(ctx, codes, scales, &p)))
+        return s;
+    if (input->rank != 2)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input must be rank two");
+    if (input->dims[1] != p.inner)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
+    uint64_t dims[2] = {input->dims[0], p.rows};
+    if ((s = check_output(ctx, output, dims, 2)))
+        return s;
+    if (aliases(output, {input, codes, scales}))
+        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
+    if (input->dims[0] > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "packed linear row count exceeds the kernel index range");
+    DeviceGuard guard(ctx->device);
+    mark_written(output);
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = Epilogue::Single;
+    call.m = uint32_t(input->dims[0]);
+    call.n = p.rows;
+    call.k = p.inner;
+    call.x = static_cast<const float *>(input->dev);
+    call.a = stream_of(codes, scales);
+    call.out_a = static_cast<float *>(output->dev);
+    return run_packed(ctx, call);
+}
+
+mfh_status mfh_packed_linear_pair(mfh_ctx *ctx, mfh_buf *out_a, mfh_buf *out_b,
+                                  const mfh_buf *input, const mfh_buf *codes_a,
+                                  const mfh_buf *scales_a, const mfh_buf *codes_b,
+                                  const mfh_buf *scales_b)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    mfh_status s = check_operation(ctx, MFH_OP_PACKED_LINEAR_PAIR);
+    if (s)
+        return s;
+    if (!same_shape(codes_a, codes_b) || !same_shape(scales_a, scales_b) ||
+        !same_shape(out_a, out_b))
+        return fail(ctx, MFH_INVALID_SHAPE,
+                    "packed linear pair requires equal weight and output shapes");
+    // Both projections pass admission before either output is written.
+    if ((s = check_f32(ctx, input)))
+        return s;
+    Packed p, q;
+    if ((s = check_packed(ctx, codes_a, scales_a, &p)) || (s = check_packed(ctx, codes_b, scales_b, &q)))
+        return s;
+    if (input->rank != 2)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input must be rank two");
+    if (input->dims[1] != p.inner)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
+    uint64_t dims[2] = {input->dims[0], p.rows};
+    if ((s = check_output(ctx, out_a, dims, 2)) || (s = check_output(ctx, out_b, dims, 2)))
+        return s;
+    if (out_a->dev && out_a->dev == out_b->dev)
+        return fail(ctx, MFH_INVALID_ARGUMENT, "pair outputs alias each other");
+    if (aliases(out_a, {input, codes_a, scales_a, codes_b, scales_b}) ||
+        aliases(out_b, {input, codes_a, scales_a, codes_b, scales_b}))
+        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
+    if (input->dims[0] > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "packed linear row count exceeds the kernel index range");
+    DeviceGuard guard(ctx->device);
+    mark_written(out_a);
+    mark_written(out_b);
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = Epilogue::Pair;
+    call.m = uint32_t(input->dims[0]);
+    call.n = p.rows;
+    call.k = p.inner;
+    call.x = static_cast<const float *>(input->dev);
+    call.a = stream_of(codes_a, scales_a);
+    call.b = stream_of(codes_b, scales_b);
+    call.out_a = static_cast<float *>(out_a->dev);
+    call.out_b = static_cast<float *>(out_b->dev);
+    return run_packed(ctx, call);
+}
+
+mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *gate,
+                                    const mfh_buf *up, const mfh_buf *codes,
+                                    const mfh_buf *scales)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    mfh_status s = check_operation(ctx, MFH_OP_PACKED_SWIGLU_LINEAR);
+    if (!s)
+        s = check_f32(ctx, gate);
+    if (!s)
+        s = check_f32(ctx, up);
+    if (s)
+        return s;
+    Packed p;
+    if ((s = check_packed(ctx, codes, scales, &p)))
+        return s;
+    if (gate->rank != 2 || !same_shape(gate, up))
+        return fail(ctx, MFH_INVALID_SHAPE,
+                    "packed SwiGLU gate and up layouts must match and be rank two");
+    if (gate->dims[1] != p.inner)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed SwiGLU input width differs from weight width");
+    uint64_t dims[2] = {gate->dims[0], p.rows};
+    if ((s = check_output(ctx, output, dims, 2)))
+        return s;
+    if (aliases(output, {gate, up, codes, scales}))
+        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
+    if (gate->dims[0] > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "packed SwiGLU row count exceeds the kernel index range");
+    DeviceGuard guard(ctx->device);
+    mark_written(output);
+    const size_t count = size_t(gate->dims[0]) * p.inner;
+    // Stage silu(gate) * up once, then run the plain packed product on it
+    // (backend-cpu/src/packed.rs:425-455).
+    float *activated = static_cast<float *>(work_scratch(ctx, count * sizeof(float)));
+    if (count && !activated)
+        return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+    launch_swiglu(ctx->stream, activated, static_cast<const float *>(gate->dev),
+                  static_cast<const float *>(up->dev), count);
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = Epilogue::Single;
+    call.m = uint32_t(gate->dims[0]);
+    call.n = p.rows;
+    call.k = p.inner;
+    call.x = activated;
+    call.a = stream_of(codes, scales);
+    call.out_a = static_cast<float *>(output->dev);
+    return run_packed(ctx, call);
+}
+
+mfh_status mfh_packed_swiglu_pair(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                                  const mfh_buf *codes_a, const mfh_buf *scales_a,
+                                  const mfh_buf *codes_b, const mfh_buf *scales_b)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    mfh_status s = check_operation(ctx, MFH_OP_PACKED_SWIGLU_PAIR);
+    if (!s)
+        s = check_f32(ctx, input);
+    if (s)
+        return s;
+    if (!same_shape(codes_a, codes_b) || !same_shape(scales_a, scales_b))
+        return fail(ctx, MFH_INVALID_SHAPE, "packed SwiGLU pair requires equal weight shapes");
+    Packed p, q;
+    if ((s = check_packed(ctx, codes_a, scales_a, &p)) || (s = check_packed(ctx, codes_b, scales_b, &q)))
+        return s;
+    if (input->rank != 2)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed SwiGLU pair input must be rank two");
+    if (input->dims[1] != p.inner)
+        return fail(ctx, MFH_INVALID_SHAPE,
+                    "packed SwiGLU pair input width differs from weight width");
+    uint64_t dims[2] = {input->dims[0], p.rows};
+    if ((s = check_output(ctx, output, dims, 2)))
+        return s;
+    if (aliases(output, {input, codes_a, scales_a, codes_b, scales_b}))
+        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
+    if (input->dims[0] > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "packed SwiGLU row count exceeds the kernel index range");
+    DeviceGuard guard(ctx->device);
+    mark_written(output);
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = Epilogue::SwigluPair;
+    call.m = uint32_t(input->dims[0]);
+    call.n = p.rows;
+    call.k = p.inner;
+    call.x = static_cast<const float *>(input->dev);
+    call.a = stream_of(codes_a, scales_a);
+    call.b = stream_of(codes_b, scales_b);
+    call.out_a = static_cast<float *>(output->dev);
+    return run_packed(ctx, call);
+}
+
+}  // extern "C"

@@ -1,0 +1,290 @@
+"""GPU parity of the packed-weight operations against the CPU oracle.
+
+Mirrors the reference's hardware-gated suites
+(crates/backend-wgpu/tests/parity.rs, int8.rs, packed_pair_validation.rs):
+gathers are bitwise, matmuls meet the reference rule
+|d| <= 1e-4 + 1e-4*|cpu| (parity.rs:76-87) and max|d|/max|cpu| <= 1e-3,
+and every admission reject leaves its outputs untouched.  All calls go
+through the C ABI (runtime_amd.backend -> libminifield_hip.so).
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+from runtime_amd import convert
+from runtime_amd.backend import WEIGHT, ExecutorError, HipBackend
+from tests.conftest import assert_close, max_rel_err
+
+pytestmark = pytest.mark.gpu
+SCHEMES = ["ternary", "nf4", "int8"]
+PATHS = {"auto": 0}
+
+
+def say(*parts):
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def make_weights(n, k, scheme, seed):
+    codes, scales16 = convert.packed_weights(n, k, scheme, seed)
+    return codes, convert.f16_to_f32(scales16)
+
+
+def upload_weights(backend, codes, scales):
+    c = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
+    s = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
+    return c, s
+
+
+def run_linear(backend, x, codes, scales):
+    cb, sb = upload_weights(backend, codes, scales)
+    xb = backend.upload_f32(x.shape, x)
+    out = backend.allocate_f32((x.shape[0], codes.shape[0]))
+    backend.packed_linear(out, xb, cb, sb)
+    return backend.read(out)
+
+
+@pytest.fixture(params=list(PATHS))
+def path(request, backend):
+    previous = backend.set_kernel_path(PATHS[request.param])
+    yield request.param
+    backend.set_kernel_path(previous)
+
+
+# --- packed_linear ---------------------------------------------------------------
+
+REFERENCE_SHAPES = [(1, 37, 256), (5, 37, 384), (1, 70000, 128)]  # parity.rs:693-734
+NF4_ROWS = [1, 5, 12, 32, 65, 95, 96, 97, 346]                       # parity.rs:1351-1420
+INT8_ROWS = [1, 7, 95, 96, 97]                                       # int8.rs:164
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m,n,k", REFERENCE_SHAPES)
+def test_packed_linear_reference_shapes(backend, path, scheme, m, n, k):
+    say("packed_linear", scheme, path, m, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0100 + n + k)
+    x = convert.normal((m, k), 0xAC70100 + m)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear(x, codes, scales)
+    assert_close(got, want, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("m", NF4_ROWS)
+def test_nf4_row_counts(backend, path, m):
+    say("nf4 rows", path, m)
+    codes, scales = make_weights(96, 1024, "nf4", 0x5EED0200)
+    x = convert.normal((m, 1024), 0xAC70200 + m)
+    got = run_linear(backend, x, codes, scales)
+    assert_close(got, oracle.packed_linear(x, codes, scales), 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("m", INT8_ROWS)
+def test_int8_rows_match_independent_dense_math(backend, path, m):
+    """int8.rs:131-191: signed bytes against dense f64 math, |d| < 0.002."""
+    say("int8 rows", path, m)
+    rng = np.random.default_rng(m)
+    n, k = 64, 384
+    codes = rng.integers(-127, 128, size=(n, k), dtype=np.int64).astype(np.int8).view(np.uint8)
+    scales = rng.uniform(0.001, 0.01, (n, k // 128)).astype(np.float32)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.dense_f64(x, oracle.dequantize_f32(codes, scales, "int8"))
+    assert np.max(np.abs(got - want)) < 0.002
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+@pytest.mark.parametrize("n,k", [(1024, 1024), (4608, 1024), (2048, 2048), (8192, 2048),
+                                 (2048, 8192)])
+def test_decode_gemv_sweep_shapes(backend, path, scheme, m, n, k):
+    """Decode GEMV over the benchmark sweep shapes (the 65536-row head is
+    covered in its own test)."""
+    say("gemv sweep", scheme, path, m, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0001 + n + k)
+    x = convert.normal((m, k), 0xAC70001 + m)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear_threaded(x, codes, scales)
+    assert max_rel_err(got, want) <= 1e-3
+    assert_close(got, want, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_lm_head_shape(backend, scheme):
+    say("lm head", scheme)
+    n, k, m = 65536, 2048, 2
+    codes, scales = make_weights(n, k, scheme, 0x5EED0006)
+    x = convert.normal((m, k), 0xAC70002)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear_threaded(x, codes, scales)
+    assert max_rel_err(got, want) <= 1e-3
+    assert_close(got, want, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m", [96, 512])
+def test_prefill_gemm(backend, path, scheme, m):
+    say("prefill gemm", scheme, path, m)
+    n, k = 512, 2048
+    codes, scales = make_weights(n, k, scheme, 0x5EED0300)
+    x = convert.normal((m, k), 0xAC70300 + m)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear_threaded(x, codes, scales)
+    assert max_rel_err(got, want) <= 1e-3
+    assert_close(got, want, 1e-4, 1e-4)
+
+
+# --- pair / SwiGLU variants -----------------------------------------------------------
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m", [1, 3, 8, 100])
+def test_pair_and_swiglu_variants(backend, path, scheme, m):
+    say("pair/swiglu", scheme, path, m)
+    n, k = 320, 768
+    ca, sa = make_weights(n, k, scheme, 0x5EED0400)
+    cb, sb = make_weights(n, k, scheme, 0x5EED0401)
+    x = convert.normal((m, k), 0xAC70400 + m)
+    gate = convert.normal((m, k), 0xAC70401 + m)
+    up = convert.normal((m, k), 0xAC70402 + m)
+    ga, gsa = upload_weights(backend, ca, sa)
+    gb, gsb = upload_weights(backend, cb, sb)
+    xb = backend.upload_f32(x.shape, x)
+    out_a = backend.allocate_f32((m, n))
+    out_b = backend.allocate_f32((m, n))
+    backend.packed_linear_pair(out_a, out_b, xb, ga, gsa, gb, gsb)
+    want_a, want_b = oracle.packed_linear_pair(x, ca, sa, cb, sb)
+    assert_close(backend.read(out_a), want_a)
+    assert_close(backend.read(out_b), want_b)
+
+    fused = backend.allocate_f32((m, n))
+    backend.packed_swiglu_pair(fused, xb, ga, gsa, gb, gsb)
+    assert_close(backend.read(fused), oracle.packed_swiglu_pair(x, ca, sa, cb, sb))
+
+    # swiglu_linear contracts over the intermediate width: weights [n2, k].
+    n2 = 192
+    c2, s2 = make_weights(n2, k, scheme, 0x5EED0402)
+    g2, gs2 = upload_weights(backend, c2, s2)
+    gb_ = backend.upload_f32(gate.shape, gate)
+    ub_ = backend.upload_f32(up.shape, up)
+    out = backend.allocate_f32((m, n2))
+    backend.packed_swiglu_linear(out, gb_, ub_, g2, gs2)
+    assert_close(backend.read(out), oracle.packed_swiglu_linear(gate, up, c2, s2))
+
+
+# --- gather -----------------------------------------------------------------------
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_packed_gather_rows_bitwise(backend, scheme):
+    say("gather", scheme)
+    rows, k = 64, 384
+    codes, scales = make_weights(rows, k, scheme, 0x5EED0500)
+    cb, sb = upload_weights(backend, codes, scales)
+    ids = [5, 0, 63, 5, 17]
+    out = backend.allocate_f32((len(ids), k))
+    backend.packed_gather_rows(out, cb, sb, ids)
+    want = oracle.packed_gather_rows(codes, scales, np.array(ids))
+    assert backend.read(out).tobytes() == want.tobytes()
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_device_ids_poison_invalid_rows(backend, scheme):
+    say("gather device ids", scheme)
+    rows, k = 3, 384
+    codes, scales = make_weights(rows, k, scheme, 0x5EED0501)
+    cb, sb = upload_weights(backend, codes, scales)
+    id_values = np.array([2.0, np.nan, 1.5, -1.0, 3.0, 16777216.0, 0.0], np.float32)
+    ids = backend.upload_f32(id_values.shape, id_values)
+    out = backend.allocate_f32((id_values.size, k))
+    backend.packed_gather_rows(out, cb, sb, ids)
+    got = backend.read(out)
+    resolved = oracle.resolve_device_ids(id_values)
+    resolved[resolved >= rows] = -1  # deferred backends poison out-of-range ids
+    want = oracle.packed_gather_rows(codes, scales, resolved)
+    for r in range(id_values.size):
+        if resolved[r] < 0:
+            assert np.all(np.isnan(got[r])), r
+        else:
+            assert got[r].tobytes() == want[r].tobytes(), r
+
+
+def test_gather_host_id_out_of_range_and_empty(backend):
+    codes, scales = make_weights(4, 128, "ternary", 0x5EED0502)
+    cb, sb = upload_weights(backend, codes, scales)
+    sentinel = np.full((2, 128), 7.0, np.float32)
+    out = backend.upload_f32(sentinel.shape, sentinel)
+    with pytest.raises(ExecutorError) as e:
+        backend.packed_gather_rows(out, cb, sb, [1, 4])
+    assert e.value.variant == "OutOfBounds"
+    assert np.array_equal(backend.read(out), sentinel)
+    empty = backend.allocate_f32((0, 128))
+    backend.packed_gather_rows(empty, cb, sb, [])
+
+
+# --- admission --------------------------------------------------------------------
+
+def test_rejects_leave_outputs_untouched(backend):
+    """packed_pair_validation.rs:57-92: nothing is written on reject."""
+    n, k, m = 16, 256, 2
+    codes, scales = make_weights(n, k, "ternary", 0x5EED0600)
+    cb, sb = upload_weights(backend, codes, scales)
+    bad_codes = backend.upload_u8_classified((n, 40), np.zeros((n, 40), np.uint8))
+    x = backend.upload_f32((m, k), convert.normal((m, k), 1))
+    sentinel = np.full((m, n), -3.0, np.float32)
+    out_a = backend.upload_f32(sentinel.shape, sentinel)
+    out_b = backend.upload_f32(sentinel.shape, sentinel)
+    with pytest.raises(ExecutorError) as e:
+        backend.packed_linear_pair(out_a, out_b, x, cb, sb, bad_codes, sb)
+    assert e.value.variant == "InvalidShape"
+    assert np.array_equal(backend.read(out_a), sentinel)
+    assert np.array_equal(backend.read(out_b), sentinel)
+    wrong_out = backend.upload_f32((m, n + 1), np.zeros((m, n + 1), np.float32))
+    with pytest.raises(ExecutorError) as e:
+        backend.packed_linear(wrong_out, x, cb, sb)
+    assert e.value.variant == "InvalidShape"
+    reserved = np.zeros((n, k), np.uint8)
+    reserved[3, 9] = 0x80
+    rb = backend.upload_u8_classified(reserved.shape, reserved)
+    with pytest.raises(ExecutorError) as e:
+        backend.packed_linear(out_a, x, rb, sb)
+    assert e.value.variant == "InvalidArgument"
+    assert np.array_equal(backend.read(out_a), sentinel)
+
+
+def test_ownership_and_generation():
+    a = HipBackend(0, owner=11)
+    b = HipBackend(0, owner=12)
+    codes, scales = make_weights(8, 128, "ternary", 0x5EED0700)
+    ca, sa = upload_weights(a, codes, scales)
+    x = a.upload_f32((1, 128), np.ones((1, 128), np.float32))
+    out_b = b.allocate_f32((1, 8))
+    with pytest.raises(ExecutorError) as e:
+        b.packed_linear(out_b, x, ca, sa)
+    assert e.value.variant == "WrongBackend"
+    out_a = a.allocate_f32((1, 8))
+    a.advance_generation()
+    with pytest.raises(ExecutorError) as e:
+        a.packed_linear(out_a, x, ca, sa)
+    assert e.value.variant == "StaleBuffer"
+    a.request_cancel()
+    with pytest.raises(ExecutorError) as e:
+        a.allocate_f32((4,))
+    assert e.value.variant == "Cancelled"
+    a.close()
+    b.close()
+
+
+def test_fence_and_readback_completion(backend):
+    vals = np.arange(513, dtype=np.float32)
+    buf = backend.upload_f32((513,), vals)
+    fence = backend.fence()
+    while not fence.poll_step():
+        pass
+    with pytest.raises(ExecutorError) as e:
+        fence.poll_step()
+    assert e.value.variant == "CompletionConsumed"
+    assert np.array_equal(backend.read(buf), vals)
+    zeroed = backend.allocate_f32((64,))
+    assert np.all(backend.read(zeroed) == 0)
