@@ -1,0 +1,233 @@
+"""Decode-GEMV sweep benchmark on one MI355X.
+
+Workload (one step): packed decode GEMV over every format x shape x batch of
+the sweep -- {ternary, nf4, int8} x {1024x1024, 4608x1024, 2048x2048,
+8192x2048, 2048x8192, 65536x2048} x B in {1, 2, 4, 8} -- 72 launches of
+`packed_linear` through the C ABI.  Weights are seeded N(0, 0.02) dense
+matrices quantized by the backend's converter (group-128, FP16-exact scales);
+activations are seeded N(0, 1).  Everything is resident in HBM before timing.
+
+Each step is captured once as a HIP graph per weight-copy set and replayed;
+consecutive uses of one matrix rotate over copies so that every launch streams
+its weights from HBM rather than the 256 MB Infinity Cache.
+
+`value` = algorithmic bytes of all launches / wall time of the K timed steps,
+where a launch's bytes are N*K*b/8 + (N*K/128)*2 + B*K*4 + B*N*4 (codes at
+b = 2/4/8 bits, scales at their stored FP16 width, activations, outputs).
+The roofline object is for the dominant kernel (the 65536x2048 INT8 head at
+B=1): its bytes over its average launch time from HIP events recorded
+around it inside the timed graphs, against the 8 TB/s HBM peak.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+FORMATS = ["ternary", "nf4", "int8"]
+BITS = {"ternary": 2, "nf4": 4, "int8": 8}
+SHAPES = [(1024, 1024), (4608, 1024), (2048, 2048), (8192, 2048), (2048, 8192), (65536, 2048)]
+BATCHES = [1, 2, 4, 8]
+HBM_PEAK_GBS = 8000.0
+DOMINANT = ("int8", (65536, 2048), 1)
+
+
+def algorithmic_bytes(n: int, k: int, b: int, fmt: str) -> int:
+    return n * k * BITS[fmt] // 8 + (n * k // 128) * 2 + b * k * 4 + b * n * 4
+
+
+def log(*parts):
+    print("[bench]", *parts, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(weights, xs) -> dict:
+    """The oracle (a C restatement of the reference's single-threaded
+    backend-cpu path, admission scans included) over every launch of one
+    sweep step, on one host core."""
+    import oracle
+
+    total_bytes = 0
+    start = time.perf_counter()
+    for fmt in FORMATS:
+        for (n, k) in SHAPES:
+            codes, scales = weights[(fmt, n, k)]
+            for b in BATCHES:
+                oracle.packed_linear(xs[(b, k)], codes, scales)
+                total_bytes += algorithmic_bytes(n, k, b, fmt)
+    seconds = time.perf_counter() - start
+    return {"value": round(total_bytes / seconds / 1e9, 3), "unit": "GB/s", "cores": 1,
+            "kind": "port",
+            "sample": "oracle packed_linear over one full sweep step (72 launches, "
+                      f"{total_bytes / 1e6:.0f} MB algorithmic, {seconds:.1f} s)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: the packed GEMV path is single-device "
+              "(sharding is described in DESIGN.md); run it with --gpus 1", file=sys.stderr)
+        return 2
+
+    from runtime_amd import convert, hiptime
+    from runtime_amd.backend import WEIGHT, HipBackend
+
+    backend = HipBackend(0)
+    stream = backend.stream()
+
+    log("generating and quantizing weights")
+    weights = {}
+    for si, (n, k) in enumerate(SHAPES):
+        dense = convert.normal((n, k), 0x5EED0001 + si, sigma=0.02)
+        for fmt in FORMATS:
+            codes, scales16 = convert.quantize(dense, fmt)
+            weights[(fmt, n, k)] = (codes, convert.f16_to_f32(scales16))
+        del dense
+    xs = {(b, k): convert.normal((b, k), 0xAC70001 + b)
+          for b in BATCHES for k in sorted({k for _, k in SHAPES})}
+
+    log(f"uploading {args.copies} weight copies")
+    dev_w = {}
+    for key, (codes, scales) in weights.items():
+        dev_w[key] = [(backend.upload_u8_classified(codes.shape, codes, WEIGHT),
+                       backend.upload_f32_classified(scales.shape, scales, WEIGHT))
+                      for _ in range(args.copies)]
+    dev_x = {key: backend.upload_f32(x.shape, x) for key, x in xs.items()}
+    dev_out = {(b, n): backend.allocate_f32((b, n)) for b in BATCHES for n, _ in SHAPES}
+
+    launches = [(fmt, (n, k), b) for b in BATCHES for fmt in FORMATS for (n, k) in SHAPES]
+    step_bytes = sum(algorithmic_bytes(n, k, b, fmt) for fmt, (n, k), b in launches)
+
+    def launch(i: int, copy_set: int) -> None:
+        fmt, (n, k), b = launches[i]
+        # Successive launches of one matrix (one per batch size) take
+        # successive copies.
+        c, s = dev_w[(fmt, n, k)][(copy_set + BATCHES.index(b)) % args.copies]
+        backend.packed_linear(dev_out[(b, n)], dev_x[(b, k)], c, s)
+
+    def enqueue(first: int, last: int, copy_set: int) -> None:
+        for i in range(first, last):
+            launch(i, copy_set)
+
+    # Eager pass: builds any per-buffer derived layouts before capture.
+    for cs in range(args.copies):
+        enqueue(0, len(launches), cs)
+    backend.synchronize()
+
+    # Each step is three graphs -- the launches before the dominant kernel,
+    # the dominant kernel, the launches after it -- so HIP events recorded
+    # between graph launches bracket the dominant kernel exactly while the
+    # queue stays busy.
+    log("capturing graphs")
+    di = launches.index(DOMINANT)
+    graphs = []
+    for cs in range(args.copies):
+        graphs.append((hiptime.Graph(stream, lambda cs=cs: enqueue(0, di, cs)),
+                       hiptime.Graph(stream, lambda cs=cs: enqueue(di, di + 1, cs)),
+                       hiptime.Graph(stream, lambda cs=cs: enqueue(di + 1, len(launches), cs))))
+
+    for w in range(args.warmup):
+        for g in graphs[w % len(graphs)]:
+            g.launch(stream)
+    backend.synchronize()
+
+    log(f"timing {args.steps} steps")
+    dom_events = [(hiptime.Event(), hiptime.Event()) for _ in range(args.steps)]
+    start, stop = hiptime.Event(), hiptime.Event()
+    start.record(stream)
+    t0 = time.perf_counter()
+    for step in range(args.steps):
+        pre, dom, post = graphs[step % len(graphs)]
+        pre.launch(stream)
+        dom_events[step][0].record(stream)
+        dom.launch(stream)
+        dom_events[step][1].record(stream)
+        post.launch(stream)
+    stop.record(stream)
+    stop.synchronize()
+    wall_s = time.perf_counter() - t0
+    total_ms = stop.elapsed_ms(start)
+    dom_ms = float(np.mean([e1.elapsed_ms(e0) for e0, e1 in dom_events]))
+
+    ms_per_step = total_ms / args.steps
+    value_gbs = step_bytes * args.steps / (total_ms / 1e3) / 1e9
+    fmt, (n, k), b = DOMINANT
+    dom_bytes = algorithmic_bytes(n, k, b, fmt)
+    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+
+    # Per-launch table (outside the timed region): each launch runs right
+    # after a spacer launch of the 65536x2048 INT8 head on another copy, which
+    # keeps the queue busy while the host records the bracketing events and
+    # streams 137 MB through the Infinity Cache.
+    log("per-launch table")
+    repeats = 5
+    table = np.zeros((repeats, len(launches)))
+    pairs = [[(hiptime.Event(), hiptime.Event()) for _ in launches] for _ in range(repeats)]
+    for r in range(repeats):
+        for i in range(len(launches)):
+            launch(di, r + 1)
+            pairs[r][i][0].record(stream)
+            launch(i, r)
+            pairs[r][i][1].record(stream)
+    backend.synchronize()
+    for r in range(repeats):
+        table[r] = [e1.elapsed_ms(e0) for e0, e1 in pairs[r]]
+    detail = {}
+    for i, (fmt_i, (n_i, k_i), b_i) in enumerate(launches):
+        us = float(np.median(table[:, i])) * 1e3
+        detail[f"{fmt_i}:{n_i}x{k_i}:B{b_i}"] = {
+            "us": round(us, 2),
+            "GBs": round(algorithmic_bytes(n_i, k_i, b_i, fmt_i) / (us / 1e6) / 1e9, 1)}
+
+    result = {
+        "metric": "packed GEMV HBM GB/s (% of 8 TB/s peak); LFM2 batch-1 decode tok/s",
+        "value": round(value_gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u8 codes, f32 activations/accumulation",
+        "data": "synthetic: seeded N(0,0.02) weights quantized group-128, N(0,1) activations",
+        "config": {
+            "workload": "decode GEMV sweep {ternary,nf4,int8} x {1024x1024,4608x1024,"
+                        "2048x2048,8192x2048,2048x8192,65536x2048} x B{1,2,4,8}, "
+                        "72 launches per step",
+            "weight_copies": args.copies,
+            "bytes_per_step": step_bytes,
+            "host_wall_s": round(wall_s, 4),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": f"packed GEMV {fmt} {n}x{k} B={b}",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(dom_ms * 1e3, 3),
+        },
+        "detail": detail,
+    }
+    if not args.no_cpu:
+        log("timing the CPU baseline")
+        result["cpu_baseline"] = cpu_baseline(weights, xs)
+    print(json.dumps(result))
+    backend.close()
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

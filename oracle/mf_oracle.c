@@ -110,11 +110,6 @@ static row_dot_fn row_dot_for(int format)
     }
 }
 
-static size_t weights_per_byte(int format)
-{
-    return format == MFO_TERNARY ? 4 : format == MFO_NF4 ? 2 : 1;
-}
-
 /* check_packed_operands, backend-cpu/src/packed.rs:177-220: K is the scales
  * width times 128 and the codes width picks the format.  INT8 streams are
  * scanned for the reserved 0x80 byte on every call, as the reference does. */

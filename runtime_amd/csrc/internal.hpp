@@ -6,6 +6,7 @@
 #include <cstdint>
 #include <map>
 #include <memory>
+#include <unordered_set>
 #include <vector>
 
 #include "../../include/minifield_hip.h"
@@ -71,6 +72,13 @@ struct mfh_ctx {
     size_t ids_scratch_capacity = 0;
     void *work_scratch = nullptr;
     size_t work_scratch_capacity = 0;
+    void *digits_scratch = nullptr;
+    size_t digits_scratch_capacity = 0;
+    // Live handles, orphaned (their ctx pointer cleared) when the context is
+    // destroyed first, so a late release or free stays safe.
+    std::unordered_set<mfh_buf *> live_buffers;
+    std::unordered_set<mfh_fence *> live_fences;
+    std::unordered_set<mfh_readback *> live_readbacks;
 };
 
 struct mfh_buf {
@@ -97,6 +105,12 @@ struct mfh_buf {
     void *repacked = nullptr;
     size_t repacked_capacity = 0;
     int repacked_format = -1;
+    // F32 scale streams: the scales in tile order for one format's padding,
+    // built on first matrix-core use; dropped when the buffer is written.
+    void *tiled_scales = nullptr;
+    size_t tiled_capacity = 0;
+    int tiled_format = -1;
+    bool tiled_half = false;
 };
 
 struct mfh_fence {
@@ -135,6 +149,7 @@ void mark_written(mfh_buf *buf);
 // Device scratch owned by the context, grown on demand (stream ordered).
 void *ids_scratch(mfh_ctx *ctx, size_t bytes);
 void *work_scratch(mfh_ctx *ctx, size_t bytes);
+void *digits_scratch(mfh_ctx *ctx, size_t bytes);
 
 // Fill `count` floats with `value` on the context stream (a kernel, so the
 // call is capturable; no hipMemsetAsync).

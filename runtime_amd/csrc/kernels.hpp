@@ -11,10 +11,12 @@ namespace mfh {
 
 // One packed weight stream as the kernels see it.
 struct PackedStream {
-    const uint8_t *codes = nullptr;     // canonical [n, k / wpb] row-major codes
-    const float *scales = nullptr;      // f32 [n, k / 128]
-    const uint16_t *scales16 = nullptr; // binary16 copy of `scales`, or null
-    const uint8_t *tiles = nullptr;     // backend-private repacked codes, or null
+    const uint8_t *codes = nullptr;      // canonical [n, k / wpb] row-major codes
+    const float *scales = nullptr;       // f32 [n, k / 128]
+    const uint16_t *scales16 = nullptr;  // binary16 copy of `scales`, or null
+    const uint8_t *tiles = nullptr;      // backend-private repacked codes, or null
+    const void *tiled_scales = nullptr;  // scales in tile order, or null
+    bool tiled_half = false;             // tiled_scales holds binary16 values
 };
 
 enum class Epilogue : int {
@@ -37,13 +39,19 @@ struct PackedCall {
 
 // Decode GEMV for m <= 8 on FP32 FMA units.
 void launch_gemv_fma(hipStream_t stream, const PackedCall &call);
-// Matrix-core decode GEMV for m <= 8 (needs `tiles` on both streams).
+// Matrix-core decode GEMV for m <= 8 (needs `tiles` and `tiled_scales` on
+// every stream).  `scratch` holds gemv_mfma_scratch_bytes(call) bytes.
+bool gemv_mfma_supported(Format format);
 void launch_gemv_mfma(hipStream_t stream, const PackedCall &call, void *scratch);
 size_t gemv_mfma_scratch_bytes(const PackedCall &call);
-// Repack a canonical code stream into the private tile layout.
+// Repack a canonical code stream into the private tile layout, and a scale
+// stream into tile order (binary16 when `half`).
 size_t repacked_bytes(Format format, uint32_t n, uint32_t k);
 void launch_repack(hipStream_t stream, Format format, const uint8_t *codes, uint8_t *tiles,
                    uint32_t n, uint32_t k);
+size_t tiled_scales_bytes(Format format, uint32_t n, uint32_t k, bool half);
+void launch_tile_scales(hipStream_t stream, Format format, const float *scales, void *out,
+                        uint32_t n, uint32_t k, bool half);
 
 // Prefill GEMM for larger m: LDS-staged dequantized tiles with FP32 FMA.
 void launch_gemm_fma(hipStream_t stream, const PackedCall &call);

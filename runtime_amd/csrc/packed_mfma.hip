@@ -1,0 +1,939 @@
+// Matrix-core decode GEMV (m <= 8) for ternary, NF4 and INT8 streams.
+//
+// Ternary and INT8 (integer MFMA).  Activation row b is split into 128-wide
+// groups; group g is scaled by a power of two so its largest magnitude is
+// below 2^30 and rounded to v = rint(x * 2^(30 - e_bg)), a 31-bit integer
+// written as four signed digits v = d0*2^24 + d1*2^16 + d2*2^8 + d3.
+// Weight codes are exact small integers (ternary code c in {0,1,2}, INT8 in
+// [-127, 127]), so v_mfma_i32_16x16x64_i8 forms every per-group digit dot
+// sum_k code_k * d_k exactly in int32.  Per group the four digit sums are
+// combined, multiplied by the group's weight scale and 2^(e_bg - 30), and
+// accumulated in f32 -- the reference's group-then-scale order
+// (kernels-simd/src/lib.rs:54,205).  Ternary codes enter through nested bit
+// masks and a per-group integer correction (see the operand-field note at
+// digits_kernel).  x is represented to within 2^-25 of its group's largest
+// magnitude.
+//
+// NF4 (f16 MFMA).  NF4 levels are not integers, so each level is split into
+// two binary16 values L = L_hi + L_lo (22 significant bits) and each
+// activation group, scaled by 2^-e_bg, into x = x_hi + x_lo.  A rows are
+// (batch, hi/lo), B is the hi plane then the lo plane of the decoded levels,
+// both v_mfma_f32_16x16x32_f16 products accumulate in f32 (f16 x f16 products
+// are exact in f32), and a per-group epilogue applies scale * 2^e_bg.  Code
+// bytes decode through a 256-entry LDS table giving both nibbles' hi and lo
+// halves, already packed as MFMA operand dwords.
+//
+// MFMA operand layout (probed on gfx950 for i8, bf16 and f16): lane
+// l = 16*q + i supplies row/column i of k-slot block q; D[i][j] =
+// sum_q sum_b A_lane(16q+i)[b] * B_lane(16q+j)[b]; result register r of lane
+// l holds D[4*(l/16) + r][l % 16].
+//
+// Private weight layout ("tiles"): 16 rows x K per tile, ordered so one
+// 16-byte load per lane reads 1 KB of contiguous memory per wave:
+//   INT8:    [tile][kstep s][lane][16 B]: lane (q,j) row j, k = 64s + 16q + b.
+//   ternary: [tile][s/4][lane][4 x 4 B]: dword s%4 holds canonical code bytes
+//            [16s + 4q, +4) of row j with bit 7 of every byte flipped (field 3
+//            stored as (c + 2) mod 4); byte e, field f is k = 64s + 16q + 4e + f.
+//   NF4:     [tile][s/4][lane][4 x 4 B] (s = 32-wide kstep): dword s%4 holds
+//            canonical code bytes [16s + 4q, +4) of row j = k 32s + 8q + 0..7.
+// Scales: [tile][group][16] as binary16 when every scale is exact in it,
+// otherwise f32.
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+
+#include "kernels.hpp"
+
+namespace mfh {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+__constant__ float kNf4Levels[16] = {
+    -1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f,
+    -0.28444138f, -0.18477343f, -0.091050036f, 0.0f,
+    0.0795803f,   0.1609302f,   0.2461123f,   0.33791524f,
+    0.44070983f,  0.562617f,    0.72295684f,  1.0f,
+};
+
+// Per-format geometry.
+//   kstep: k covered by one MFMA;  kpl: ksteps per 16-byte lane load;
+//   spg: ksteps per 128-weight group;  lb: ksteps per loop block;
+//   align: K padding of the tile layout.
+template <Format F> struct Geo;
+template <> struct Geo<Format::Ternary> {
+    static constexpr int kstep = 64, kpl = 4, spg = 2, lb = 4, align = 256;
+};
+template <> struct Geo<Format::Int8> {
+    static constexpr int kstep = 64, kpl = 1, spg = 2, lb = 2, align = 128;
+};
+template <> struct Geo<Format::Nf4> {
+    static constexpr int kstep = 32, kpl = 4, spg = 4, lb = 4, align = 128;
+};
+
+__host__ __device__ inline uint32_t pad_to(uint32_t v, uint32_t a) { return (v + a - 1) / a * a; }
+
+uint32_t align_of(Format f)
+{
+    return f == Format::Ternary ? 256 : 128;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float silu_mul(float gate, float up)
+{
+    float sigmoid = 1.0f / (1.0f + expf(-gate));
+    return (gate * sigmoid) * up;
+}
+
+// ---------------------------------------------------------------------------
+// Activation prologues: one wave per (128-wide group, batch slot).  Slots at
+// or beyond m are written as zeros so every fragment byte is defined.
+// ---------------------------------------------------------------------------
+struct GroupX {
+    float x[2];
+    int e;
+    bool bad;
+};
+
+__device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_t g, uint32_t m,
+                                             uint32_t k)
+{
+    const uint32_t lane = threadIdx.x;
+    GroupX r;
+    r.bad = false;
+    float mx = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t kk = g * 128 + h * 64 + lane;
+        float v = (b < m && kk < k) ? x[size_t(b) * k + kk] : 0.0f;
+        if (!isfinite(v)) {
+            r.bad = true;
+            v = 0.0f;
+        }
+        r.x[h] = v;
+        mx = fmaxf(mx, fabsf(v));
+    }
+    r.bad = __any(r.bad);
+    mx = wave_max(mx);
+    r.e = 0;
+    if (mx > 0.0f)
+        frexpf(mx, &r.e);  // mx = f * 2^e with f in [0.5, 1), so |x| < 2^e
+    return r;
+}
+
+// Ternary operand fields.  Within a 64-wide kstep, k = 16q + 4e + f puts
+// weight k in bits [2f, 2f+2) of code byte e of lane block q (f = k % 4).
+// The tile layout stores field 3 as (c + 2) mod 4, and the B operand's four
+// dwords are w, w & 0xFCFCFCFC, w & 0xF0F0F0F0, w & 0xC0C0C0C0: as signed
+// bytes, dword d holds sum_{f >= d} 4^f c'_f with c'_f = c_f for f < 3 and
+// c_3 - 2 for field 3.  The matching A dword d holds
+// y_d = u_d - u_{d-1}, where u_f = round(v_f / 4^f), so the MFMA sum
+// telescopes to sum_f 4^f c'_f u_f.  The prologue's per-group correction
+// corr = sum_{f<3} 4^f u_f - 64 sum_{f=3} u_f turns that into
+// sum_k (c_k - 1) * 4^f u_k, i.e. sum_k (c_k - 1) v_k to within 2^5 units of
+// the 2^30-scaled group maximum per weight.
+template <Format F>
+__global__ __launch_bounds__(64) void digits_kernel(const float *x, uint32_t m, uint32_t k,
+                                                    uint32_t groups, uint32_t nfrag,
+                                                    int8_t *afrag, float *xf, int2 *corr)
+{
+    const uint32_t g = blockIdx.x, b = blockIdx.y;
+    const uint32_t lane = threadIdx.x;
+    const GroupX gx = load_group(x, b, g, m, k);
+    if (lane == 0)
+        xf[b * groups + g] = gx.bad ? __builtin_nanf("") : ldexpf(1.0f, gx.e - 30);
+    long long corr_sum = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t kk = g * 128 + h * 64 + lane;
+        int val = gx.bad ? 0 : int(rintf(ldexpf(gx.x[h], 30 - gx.e)));
+        if constexpr (F == Format::Ternary) {
+            const int f = int(lane & 3);
+            const int u = f == 0 ? val : (val + (1 << (2 * f - 1))) >> (2 * f);
+            const int u_prev = __shfl_up(u, 1, 64);
+            val = f == 0 ? u : u - u_prev;
+            corr_sum += f < 3 ? (static_cast<long long>(u) << (2 * f))
+                              : -(static_cast<long long>(u) << 6);
+        }
+        // Offset form: bytes of val + 0x808080 are the low digits plus 128.
+        const int vp = val + 0x808080;
+        int d[4];
+        d[0] = vp >> 24;
+        d[1] = int(int8_t(((vp >> 16) & 255) ^ 0x80));
+        d[2] = int(int8_t(((vp >> 8) & 255) ^ 0x80));
+        d[3] = int(int8_t((vp & 255) ^ 0x80));
+        const uint32_t s = kk / 64, r = kk % 64;
+        const uint32_t q = r / 16, c = r % 16;
+        const uint32_t byte = (F == Format::Ternary) ? (4 * (c & 3) + (c >> 2)) : c;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t row = 4 * (b % 4) + i;
+            afrag[((size_t(s) * nfrag + b / 4) * 64 + 16 * q + row) * 16 + byte] = int8_t(d[i]);
+        }
+    }
+    if constexpr (F == Format::Ternary) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1)
+            corr_sum += __shfl_xor(corr_sum, off, 64);
+        if (lane == 0) {
+            // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
+            const long long lo = ((corr_sum + 32768) & 65535) - 32768;
+            corr[size_t(b) * groups + g] = int2{int((corr_sum - lo) >> 16), int(lo)};
+        }
+    }
+}
+
+__global__ __launch_bounds__(64) void halves_kernel(const float *x, uint32_t m, uint32_t k,
+                                                    uint32_t groups, _Float16 *afrag, float *xf)
+{
+    const uint32_t g = blockIdx.x, b = blockIdx.y;
+    const uint32_t lane = threadIdx.x;
+    const GroupX gx = load_group(x, b, g, m, k);
+    if (lane == 0)
+        xf[b * groups + g] = gx.bad ? __builtin_nanf("") : ldexpf(1.0f, gx.e);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t kk = g * 128 + h * 64 + lane;
+        const float v = gx.bad ? 0.0f : ldexpf(gx.x[h], -gx.e);
+        const _Float16 hi = _Float16(v);
+        const _Float16 lo = _Float16(v - float(hi));
+        const uint32_t s = kk / 32, r = kk % 32;
+        const uint32_t q = r / 8, pos = r % 8;
+        afrag[(size_t(s) * 64 + 16 * q + 2 * b) * 8 + pos] = hi;
+        afrag[(size_t(s) * 64 + 16 * q + 2 * b + 1) * 8 + pos] = lo;
+    }
+}
+
+template <bool HALF>
+struct ScaleT;
+template <> struct ScaleT<true> { typedef __half type; };
+template <> struct ScaleT<false> { typedef float type; };
+
+template <bool HALF>
+__device__ __forceinline__ float to_f32(typename ScaleT<HALF>::type v)
+{
+    if constexpr (HALF)
+        return __half2float(v);
+    else
+        return v;
+}
+
+struct MfmaArgs {
+    const void *afrag;
+    const float *xf;
+    const int2 *corr;
+    const uint8_t *tiles[2];
+    const void *scales[2];
+    float *out[2];
+    uint32_t m, n, k_pad;
+    uint32_t ksteps_per_wave;
+};
+
+// Fixed-order sum of the wave partials through LDS, then the epilogue.
+// vals[idx] per lane; idx = (st * T + t) * NB + batch-slot-of-lane.
+template <int S, int T, int NB, Epilogue E>
+__device__ __forceinline__ void reduce_and_store(const MfmaArgs &a, float (&vals)[S][T][NB],
+                                                 const uint32_t (&batch)[NB], uint32_t tile0,
+                                                 uint32_t j)
+{
+    extern __shared__ float red[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    constexpr int V = S * T * NB;
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                red[(wave * V + (st * T + t) * NB + nb) * 64 + lane] = vals[st][t][nb];
+    __syncthreads();
+    for (int idx = wave; idx < T * NB; idx += waves) {
+        const int t = idx / NB, nb = idx % NB;
+        float v[S];
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+            float sum = 0.0f;
+            for (int w2 = 0; w2 < waves; ++w2)
+                sum += red[(w2 * V + (st * T + t) * NB + nb) * 64 + lane];
+            v[st] = sum;
+        }
+        const uint32_t b = batch[nb];
+        const uint32_t row = (tile0 + t) * 16 + j;
+        if (b < a.m && row < a.n) {
+            const size_t o = size_t(b) * a.n + row;
+            if constexpr (E == Epilogue::Single) {
+                a.out[0][o] = v[0];
+            } else if constexpr (E == Epilogue::Pair) {
+                a.out[0][o] = v[0];
+                a.out[1][o] = v[S - 1];
+            } else {
+                a.out[0][o] = silu_mul(v[0], v[S - 1]);
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Integer-MFMA GEMV (ternary, INT8).  A block owns T consecutive tiles of each
+// of S streams; its W waves split K.  Loop blocks of LB ksteps are double
+// buffered in registers: the next block's weights and activation fragments
+// are in flight while the current one is computed.
+// ---------------------------------------------------------------------------
+template <Format F, int T, int S, int NF>
+struct I8Block {
+    static constexpr int LB = Geo<F>::lb;
+    static constexpr int LOADS = LB / Geo<F>::kpl;
+    v4u w[S][T][LOADS];
+    v4i af[LB][NF];
+};
+
+template <Format F, int T, int S, int NF>
+__device__ __forceinline__ void i8_load(I8Block<F, T, S, NF> &blk, const v4u *const (&wp)[S][T],
+                                        const v4i *ap, uint32_t index)
+{
+    using B = I8Block<F, T, S, NF>;
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int l = 0; l < B::LOADS; ++l)
+                blk.w[st][t][l] = wp[st][t][(index * B::LOADS + l) * 64];
+#pragma unroll
+    for (int ks = 0; ks < B::LB; ++ks)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            blk.af[ks][f] = ap[((index * B::LB + ks) * NF + f) * 64];
+}
+
+template <Format F, int T, int S, int NF, bool HALF>
+__device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF> &blk,
+                                           float (&accf)[S][T][NF],
+                                           const typename ScaleT<HALF>::type *const (&sp)[S][T],
+                                           const float *const (&xp)[NF],
+                                           const int2 *const (&cp)[NF], uint32_t gindex)
+{
+    using B = I8Block<F, T, S, NF>;
+    constexpr int GPB = B::LB / 2;
+#pragma unroll
+    for (int gg = 0; gg < GPB; ++gg) {
+        const uint32_t g = gindex * GPB + gg;
+        // Group constants: issued first so their latency overlaps the MFMAs.
+        float sc[S][T];
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+                sc[st][t] = to_f32<HALF>(sp[st][t][g * 16]);
+        float xfv[NF];
+        int2 cv[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            xfv[f] = xp[f][g];
+            if constexpr (F == Format::Ternary)
+                cv[f] = cp[f][g];
+            else
+                cv[f] = int2{0, 0};
+        }
+        v4i acci[S][T][NF];
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    acci[st][t][f] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int ks = gg * 2 + kk;
+#pragma unroll
+            for (int st = 0; st < S; ++st)
+#pragma unroll
+                for (int t = 0; t < T; ++t) {
+                    v4i bw;
+                    if constexpr (F == Format::Ternary) {
+                        // Nested field masks (see the operand-field note above).
+                        const unsigned word = blk.w[st][t][0][ks];
+                        bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
+                                 int(word & 0xC0C0C0C0u)};
+                    } else {
+                        const v4u v = blk.w[st][t][ks];
+                        bw = v4i{int(v.x), int(v.y), int(v.z), int(v.w)};
+                    }
+#pragma unroll
+                    for (int f = 0; f < NF; ++f)
+                        acci[st][t][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            blk.af[ks][f], bw, acci[st][t][f], 0, 0, 0);
+                }
+        }
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+#pragma unroll
+            for (int t = 0; t < T; ++t)
+#pragma unroll
+                for (int f = 0; f < NF; ++f) {
+                    const v4i d = acci[st][t][f];
+                    // |d.x| < 2^21, so the pairs combine exactly in int32.
+                    const int hi = (d.x << 8) + d.y - cv[f].x;
+                    const int lo = (d.z << 8) + d.w - cv[f].y;
+                    const float gsum = float(hi) * 65536.0f + float(lo);
+                    accf[st][t][f] += gsum * (sc[st][t] * xfv[f]);
+                }
+    }
+}
+
+// At most 8 waves per block: two per SIMD leaves 256 VGPRs per wave for the
+// double-buffered loop blocks.
+template <Format F, int T, int S, int NF, bool HALF, Epilogue E>
+__global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
+{
+    using B = I8Block<F, T, S, NF>;
+    using ST = typename ScaleT<HALF>::type;
+    constexpr int KPL = Geo<F>::kpl;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t tile0 = blockIdx.x * T;
+    const uint32_t groups = a.k_pad / 128;
+    const uint32_t s_begin = wave * a.ksteps_per_wave;
+    const uint32_t nblk = a.ksteps_per_wave / B::LB;
+    const uint32_t g_begin = s_begin / 2;
+    const size_t tile_vecs = size_t(a.k_pad) / 64 / KPL * 64;
+
+    const v4u *wp[S][T];
+    const ST *sp[S][T];
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            wp[st][t] = reinterpret_cast<const v4u *>(a.tiles[st]) + (tile0 + t) * tile_vecs +
+                        (s_begin / KPL) * 64 + lane;
+            sp[st][t] = reinterpret_cast<const ST *>(a.scales[st]) +
+                        (size_t(tile0 + t) * groups + g_begin) * 16 + j;
+        }
+    const v4i *ap = reinterpret_cast<const v4i *>(a.afrag) + size_t(s_begin) * NF * 64 + lane;
+    const float *xp[NF];
+    const int2 *cp[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        xp[f] = a.xf + (4 * f + q) * groups + g_begin;
+        cp[f] = a.corr + (4 * f + q) * groups + g_begin;
+    }
+
+    float accf[S][T][NF];
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                accf[st][t][f] = 0.0f;
+
+    B buf0, buf1;
+    if (nblk > 0)
+        i8_load(buf0, wp, ap, 0);
+    for (uint32_t i = 0; i < nblk; i += 2) {
+        if (i + 1 < nblk)
+            i8_load(buf1, wp, ap, i + 1);
+        i8_compute<F, T, S, NF, HALF>(buf0, accf, sp, xp, cp, i);
+        if (i + 1 < nblk) {
+            if (i + 2 < nblk)
+                i8_load(buf0, wp, ap, i + 2);
+            i8_compute<F, T, S, NF, HALF>(buf1, accf, sp, xp, cp, i + 1);
+        }
+    }
+
+    uint32_t batch[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+        batch[f] = 4 * f + q;
+    reduce_and_store<S, T, NF, E>(a, accf, batch, tile0, j);
+}
+
+// ---------------------------------------------------------------------------
+// NF4 GEMV on f16 MFMA.  One loop block = one 16-byte lane load per tile =
+// four 32-wide ksteps = one 128-weight group.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kLutCopies = 16;
+template <int T, int S>
+struct Nf4Block {
+    v4u w[S][T];
+    v8h af[4];
+};
+
+template <int T, int S>
+__device__ __forceinline__ void nf4_load(Nf4Block<T, S> &blk, const v4u *const (&wp)[S][T],
+                                         const v8h *ap, uint32_t index)
+{
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            blk.w[st][t] = wp[st][t][index * 64];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        blk.af[ks] = ap[(index * 4 + ks) * 64];
+}
+
+template <int T, int S, bool HALF>
+__device__ __forceinline__ void nf4_compute(const Nf4Block<T, S> &blk, float (&accf)[S][T][2],
+                                            const typename ScaleT<HALF>::type *const (&sp)[S][T],
+                                            const float *const (&xp)[2], const uint2 *lut,
+                                            uint32_t g)
+{
+    float sc[S][T];
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            sc[st][t] = to_f32<HALF>(sp[st][t][g * 16]);
+    const float xf0 = xp[0][g], xf1 = xp[1][g];
+    v4f acc[S][T];
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            acc[st][t] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const unsigned word = blk.w[st][t][ks];
+                v4u hi, lo;
+#pragma unroll
+                for (int p = 0; p < 4; ++p) {
+                    const uint2 e = lut[((word >> (8 * p)) & 255u) * kLutCopies];
+                    hi[p] = e.x;
+                    lo[p] = e.y;
+                }
+                acc[st][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    blk.af[ks], __builtin_bit_cast(v8h, hi), acc[st][t], 0, 0, 0);
+                acc[st][t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                    blk.af[ks], __builtin_bit_cast(v8h, lo), acc[st][t], 0, 0, 0);
+            }
+    }
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            // Rows 4q + {0,1} are batch 2q (hi, lo), rows 4q + {2,3} batch 2q+1.
+            accf[st][t][0] += (acc[st][t].x + acc[st][t].y) * (sc[st][t] * xf0);
+            accf[st][t][1] += (acc[st][t].z + acc[st][t].w) * (sc[st][t] * xf1);
+        }
+}
+
+template <int T, int S, bool HALF, Epilogue E>
+__global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
+{
+    using ST = typename ScaleT<HALF>::type;
+    // kLutCopies interleaved copies of the 256-entry table; lane l reads copy
+    // l % kLutCopies, so the lanes of one LDS cycle spread over distinct banks.
+    __shared__ uint2 lut_all[256 * kLutCopies];
+    for (uint32_t i = threadIdx.x; i < 256 * kLutCopies; i += blockDim.x) {
+        // Entry for one code byte: x = hi halves of (low nibble, high nibble),
+        // y = lo halves, each a packed f16 pair for consecutive k.
+        const uint32_t e = i / kLutCopies;
+        const float l0 = kNf4Levels[e & 15], l1 = kNf4Levels[e >> 4];
+        const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
+        const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
+        lut_all[i] = uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
+                               (unsigned(__builtin_bit_cast(unsigned short, h1)) << 16),
+                           unsigned(__builtin_bit_cast(unsigned short, r0)) |
+                               (unsigned(__builtin_bit_cast(unsigned short, r1)) << 16)};
+    }
+    __syncthreads();
+    const uint2 *lut = lut_all + (threadIdx.x % kLutCopies);
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t tile0 = blockIdx.x * T;
+    const uint32_t groups = a.k_pad / 128;
+    const uint32_t s_begin = wave * a.ksteps_per_wave;  // 32-wide ksteps
+    const uint32_t nblk = a.ksteps_per_wave / 4;
+    const uint32_t g_begin = s_begin / 4;
+    const size_t tile_vecs = size_t(a.k_pad) / 128 * 64;
+
+    const v4u *wp[S][T];
+    const ST *sp[S][T];
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            wp[st][t] = reinterpret_cast<const v4u *>(a.tiles[st]) + (tile0 + t) * tile_vecs +
+                        g_begin * 64 + lane;
+            sp[st][t] = reinterpret_cast<const ST *>(a.scales[st]) +
+                        (size_t(tile0 + t) * groups + g_begin) * 16 + j;
+        }
+    const v8h *ap = reinterpret_cast<const v8h *>(a.afrag) + size_t(s_begin) * 64 + lane;
+    const float *xp[2] = {a.xf + (2 * q) * groups + g_begin, a.xf + (2 * q + 1) * groups + g_begin};
+
+    float accf[S][T][2];
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+            accf[st][t][0] = accf[st][t][1] = 0.0f;
+
+    Nf4Block<T, S> buf0, buf1;
+    if (nblk > 0)
+        nf4_load(buf0, wp, ap, 0);
+    for (uint32_t i = 0; i < nblk; i += 2) {
+        if (i + 1 < nblk)
+            nf4_load(buf1, wp, ap, i + 1);
+        nf4_compute<T, S, HALF>(buf0, accf, sp, xp, lut, i);
+        if (i + 1 < nblk) {
+            if (i + 2 < nblk)
+                nf4_load(buf0, wp, ap, i + 2);
+            nf4_compute<T, S, HALF>(buf1, accf, sp, xp, lut, i + 1);
+        }
+    }
+    const uint32_t batch[2] = {2 * q, 2 * q + 1};
+    reduce_and_store<S, T, 2, E>(a, accf, batch, tile0, j);
+}
+
+// ---------------------------------------------------------------------------
+// Repack canonical codes into tiles, and scales into [tile][group][16].
+// ---------------------------------------------------------------------------
+template <Format F>
+__global__ __launch_bounds__(256) void repack_kernel(const uint8_t *codes, uint8_t *tiles,
+                                                     uint32_t n, uint32_t k, uint32_t k_pad,
+                                                     uint32_t n_tiles)
+{
+    constexpr uint32_t KPL = Geo<F>::kpl, KSTEP = Geo<F>::kstep;
+    const uint32_t loads_per_tile = k_pad / KSTEP / KPL;
+    const size_t total = size_t(n_tiles) * loads_per_tile * 64;
+    const uint32_t row_bytes = k / weights_per_byte(F);
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < total;
+         i += size_t(gridDim.x) * 256) {
+        const uint32_t lane = uint32_t(i % 64);
+        const uint32_t u = uint32_t((i / 64) % loads_per_tile);
+        const uint32_t tile = uint32_t(i / 64 / loads_per_tile);
+        const uint32_t q = lane / 16, jj = lane % 16;
+        const uint32_t row = tile * 16 + jj;
+        // Padding decodes to weight 0 in every format.
+        const unsigned pad = F == Format::Ternary ? 0x55555555u : F == Format::Nf4 ? 0x77777777u : 0u;
+        unsigned out[4] = {pad, pad, pad, pad};
+        if (row < n) {
+            const uint8_t *src = codes + size_t(row) * row_bytes;
+            if constexpr (F == Format::Int8) {
+                const uint32_t byte0 = 64 * u + 16 * q;
+                if (byte0 < row_bytes) {
+                    uint4 v = *reinterpret_cast<const uint4 *>(src + byte0);
+                    out[0] = v.x;
+                    out[1] = v.y;
+                    out[2] = v.z;
+                    out[3] = v.w;
+                }
+            } else {
+                // Ternary 64-wide and NF4 32-wide ksteps both span 16 code bytes.
+                for (int kk = 0; kk < 4; ++kk) {
+                    const uint32_t byte0 = 16 * (u * 4 + kk) + 4 * q;
+                    if (byte0 < row_bytes)
+                        out[kk] = *reinterpret_cast<const unsigned *>(src + byte0) ^
+                                  (F == Format::Ternary ? 0x80808080u : 0u);  // field 3 + 2
+                }
+            }
+        }
+        reinterpret_cast<uint4 *>(tiles)[i] = uint4{out[0], out[1], out[2], out[3]};
+    }
+}
+
+template <bool HALF>
+__global__ __launch_bounds__(256) void tile_scales_kernel(const float *scales, void *out,
+                                                          uint32_t n, uint32_t groups,
+                                                          uint32_t groups_pad, uint32_t n_tiles)
+{
+    const size_t total = size_t(n_tiles) * groups_pad * 16;
+    for (size_t i = size_t(blockIdx.x) * 256 + threadIdx.x; i < total;
+         i += size_t(gridDim.x) * 256) {
+        const uint32_t jj = uint32_t(i % 16);
+        const uint32_t g = uint32_t((i / 16) % groups_pad);
+        const uint32_t tile = uint32_t(i / 16 / groups_pad);
+        const uint32_t row = tile * 16 + jj;
+        const float v = (row < n && g < groups) ? scales[size_t(row) * groups + g] : 0.0f;
+        if constexpr (HALF)
+            reinterpret_cast<__half *>(out)[i] = __float2half(v);
+        else
+            reinterpret_cast<float *>(out)[i] = v;
+    }
+}
+
+unsigned grid_for(size_t count)
+{
+    size_t blocks = (count + 255) / 256;
+    return unsigned(blocks < 65536 ? (blocks ? blocks : 1) : 65536);
+}
+
+struct Plan {
+    int tiles_per_block;
+    int waves;
+};
+
+// Tiles per block T and waves per block W (which split K).  Prefer the widest
+// T that still yields >= 2048 waves; each wave covers whole loop blocks.
+Plan plan_for(uint32_t n_tiles, uint32_t ksteps, uint32_t lb, int max_t)
+{
+    auto fits = [&](uint32_t w) { return ksteps % (w * lb) == 0; };
+    for (int t : {4, 2, 1}) {
+        if (t > max_t || n_tiles % t)
+            continue;
+        for (int w : {4, 8})
+            if (fits(w) && uint64_t(n_tiles / t) * w >= 2048)
+                return Plan{t, w};
+    }
+    for (int w : {8, 4, 2, 1})
+        if (fits(w))
+            return Plan{1, w};
+    return Plan{1, 1};
+}
+
+template <int S, int NB>
+size_t reduce_lds_bytes(int waves, int t)
+{
+    return size_t(waves) * S * t * NB * 64 * sizeof(float);
+}
+
+template <Format F, int T, int S, int NF, bool HALF>
+void launch_i8(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves)
+{
+    const size_t lds = reduce_lds_bytes<S, NF>(waves, T);
+    if constexpr (S == 1) {
+        gemv_i8_kernel<F, T, 1, NF, HALF, Epilogue::Single>
+            <<<blocks, 64 * waves, lds, stream>>>(args);
+    } else if (e == Epilogue::Pair) {
+        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::Pair><<<blocks, 64 * waves, lds, stream>>>(args);
+    } else {
+        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::SwigluPair>
+            <<<blocks, 64 * waves, lds, stream>>>(args);
+    }
+}
+
+template <Format F, int T, int S>
+void launch_i8_nf(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves,
+                  int nf, bool half)
+{
+    if (nf == 1) {
+        if (half)
+            launch_i8<F, T, S, 1, true>(stream, args, e, blocks, waves);
+        else
+            launch_i8<F, T, S, 1, false>(stream, args, e, blocks, waves);
+    } else {
+        if (half)
+            launch_i8<F, T, S, 2, true>(stream, args, e, blocks, waves);
+        else
+            launch_i8<F, T, S, 2, false>(stream, args, e, blocks, waves);
+    }
+}
+
+template <int T, int S, bool HALF>
+void launch_nf4(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves)
+{
+    const size_t lds = reduce_lds_bytes<S, 2>(waves, T);
+    if constexpr (S == 1) {
+        gemv_nf4_kernel<T, 1, HALF, Epilogue::Single><<<blocks, 64 * waves, lds, stream>>>(args);
+    } else if (e == Epilogue::Pair) {
+        gemv_nf4_kernel<T, 2, HALF, Epilogue::Pair><<<blocks, 64 * waves, lds, stream>>>(args);
+    } else {
+        gemv_nf4_kernel<T, 2, HALF, Epilogue::SwigluPair><<<blocks, 64 * waves, lds, stream>>>(args);
+    }
+}
+
+struct Scratch {
+    void *afrag;
+    float *xf;
+    int2 *corr;
+};
+
+Scratch carve(void *scratch, uint32_t k_pad)
+{
+    // afrag: k_pad * 16 bytes per 4-batch integer fragment (two fragments at
+    // most); the f16 NF4 fragment takes k_pad * 32 bytes.  Same bound.
+    char *p = static_cast<char *>(scratch);
+    Scratch s;
+    s.afrag = p;
+    p += size_t(k_pad) * 32;
+    s.xf = reinterpret_cast<float *>(p);
+    p += size_t(8) * (k_pad / 128) * sizeof(float);
+    s.corr = reinterpret_cast<int2 *>(p);
+    return s;
+}
+
+template <Format F>
+void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
+{
+    const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
+    const uint32_t groups = k_pad / 128;
+    const uint32_t n_tiles = pad_to(call.n, 64) / 16;
+    const int nf = call.m <= 4 ? 1 : 2;
+    Scratch sc = carve(scratch, k_pad);
+    digits_kernel<F><<<dim3(groups, 4 * nf), 64, 0, stream>>>(
+        call.x, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag), sc.xf, sc.corr);
+    const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
+    const uint32_t ksteps = k_pad / 64;
+    Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1);
+    if (plan.tiles_per_block == 2)
+        plan.tiles_per_block = 1;  // T in {1, 4} are instantiated
+    MfmaArgs args{};
+    args.afrag = sc.afrag;
+    args.xf = sc.xf;
+    args.corr = sc.corr;
+    args.tiles[0] = call.a.tiles;
+    args.tiles[1] = call.b.tiles;
+    args.scales[0] = call.a.tiled_scales;
+    args.scales[1] = call.b.tiled_scales;
+    args.out[0] = call.out_a;
+    args.out[1] = call.out_b;
+    args.m = call.m;
+    args.n = call.n;
+    args.k_pad = k_pad;
+    args.ksteps_per_wave = ksteps / plan.waves;
+    const unsigned blocks = n_tiles / plan.tiles_per_block;
+    const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
+    if (streams == 1) {
+        if (plan.tiles_per_block == 4)
+            launch_i8_nf<F, 4, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half);
+        else
+            launch_i8_nf<F, 1, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half);
+    } else {
+        launch_i8_nf<F, 1, 2>(stream, args, call.epilogue, blocks, plan.waves, nf, half);
+    }
+}
+
+void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
+{
+    const uint32_t k_pad = pad_to(call.k, 128);
+    const uint32_t groups = k_pad / 128;
+    const uint32_t n_tiles = pad_to(call.n, 64) / 16;
+    Scratch sc = carve(scratch, k_pad);
+    halves_kernel<<<dim3(groups, 8), 64, 0, stream>>>(call.x, call.m, call.k, groups,
+                                                      static_cast<_Float16 *>(sc.afrag), sc.xf);
+    const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
+    const uint32_t ksteps = k_pad / 32;
+    Plan plan = plan_for(n_tiles, ksteps, 4, streams == 1 ? 2 : 1);
+    MfmaArgs args{};
+    args.afrag = sc.afrag;
+    args.xf = sc.xf;
+    args.tiles[0] = call.a.tiles;
+    args.tiles[1] = call.b.tiles;
+    args.scales[0] = call.a.tiled_scales;
+    args.scales[1] = call.b.tiled_scales;
+    args.out[0] = call.out_a;
+    args.out[1] = call.out_b;
+    args.m = call.m;
+    args.n = call.n;
+    args.k_pad = k_pad;
+    args.ksteps_per_wave = ksteps / plan.waves;
+    const unsigned blocks = n_tiles / plan.tiles_per_block;
+    const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
+    if (streams == 1) {
+        if (plan.tiles_per_block == 2) {
+            if (half)
+                launch_nf4<2, 1, true>(stream, args, call.epilogue, blocks, plan.waves);
+            else
+                launch_nf4<2, 1, false>(stream, args, call.epilogue, blocks, plan.waves);
+        } else {
+            if (half)
+                launch_nf4<1, 1, true>(stream, args, call.epilogue, blocks, plan.waves);
+            else
+                launch_nf4<1, 1, false>(stream, args, call.epilogue, blocks, plan.waves);
+        }
+    } else {
+        if (half)
+            launch_nf4<1, 2, true>(stream, args, call.epilogue, blocks, plan.waves);
+        else
+            launch_nf4<1, 2, false>(stream, args, call.epilogue, blocks, plan.waves);
+    }
+}
+
+}  // namespace
+
+bool gemv_mfma_supported(Format format)
+{
+    (void)format;
+    return true;
+}
+
+size_t gemv_mfma_scratch_bytes(const PackedCall &call)
+{
+    const uint32_t k_pad = pad_to(call.k, 256);
+    return size_t(k_pad) * 32 + size_t(8) * (k_pad / 128) * sizeof(float) +
+           size_t(8) * (k_pad / 128) * 4 * sizeof(int);
+}
+
+void launch_gemv_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
+{
+    switch (call.format) {
+    case Format::Ternary: gemv_i8_format<Format::Ternary>(stream, call, scratch); break;
+    case Format::Int8: gemv_i8_format<Format::Int8>(stream, call, scratch); break;
+    case Format::Nf4: gemv_nf4(stream, call, scratch); break;
+    }
+}
+
+size_t repacked_bytes(Format format, uint32_t n, uint32_t k)
+{
+    const uint32_t n_tiles = pad_to(n, 64) / 16;
+    return size_t(n_tiles) * 16 * pad_to(k, align_of(format)) / weights_per_byte(format);
+}
+
+size_t tiled_scales_bytes(Format format, uint32_t n, uint32_t k, bool half)
+{
+    const uint32_t n_tiles = pad_to(n, 64) / 16;
+    const uint32_t k_pad = pad_to(k, align_of(format));
+    return size_t(n_tiles) * (k_pad / 128) * 16 * (half ? 2 : 4);
+}
+
+void launch_repack(hipStream_t stream, Format format, const uint8_t *codes, uint8_t *tiles,
+                   uint32_t n, uint32_t k)
+{
+    const uint32_t n_tiles = pad_to(n, 64) / 16;
+    const uint32_t k_pad = pad_to(k, align_of(format));
+    const size_t total = repacked_bytes(format, n, k) / 16;
+    switch (format) {
+    case Format::Ternary:
+        repack_kernel<Format::Ternary><<<grid_for(total), 256, 0, stream>>>(codes, tiles, n, k,
+                                                                             k_pad, n_tiles);
+        break;
+    case Format::Nf4:
+        repack_kernel<Format::Nf4><<<grid_for(total), 256, 0, stream>>>(codes, tiles, n, k, k_pad,
+                                                                         n_tiles);
+        break;
+    case Format::Int8:
+        repack_kernel<Format::Int8><<<grid_for(total), 256, 0, stream>>>(codes, tiles, n, k,
+                                                                          k_pad, n_tiles);
+        break;
+    }
+}
+
+void launch_tile_scales(hipStream_t stream, Format format, const float *scales, void *out,
+                        uint32_t n, uint32_t k, bool half)
+{
+    const uint32_t n_tiles = pad_to(n, 64) / 16;
+    const uint32_t k_pad = pad_to(k, align_of(format));
+    const size_t total = size_t(n_tiles) * (k_pad / 128) * 16;
+    if (half)
+        tile_scales_kernel<true><<<grid_for(total), 256, 0, stream>>>(scales, out, n, k / 128,
+                                                                      k_pad / 128, n_tiles);
+    else
+        tile_scales_kernel<false><<<grid_for(total), 256, 0, stream>>>(scales, out, n, k / 128,
+                                                                       k_pad / 128, n_tiles);
+}
+
+}  // namespace mfh

@@ -91,8 +91,58 @@ PackedStream stream_of(const mfh_buf *codes, const mfh_buf *scales)
     return s;
 }
 
-// Enqueue the kernels of one admitted packed product.
-mfh_status run_packed(mfh_ctx *ctx, PackedCall call)
+// Build (once) the tile-order copies the matrix-core kernels read: the
+// repacked codes live on the code buffer, the tiled scales on the scale
+// buffer.  Both are stream-ordered kernels; nothing synchronizes.
+mfh_status prepare_tiles(mfh_ctx *ctx, const mfh_buf *codes_c, const mfh_buf *scales_c,
+                         const Packed &p, PackedStream *stream)
+{
+    // Derived copies are caches on immutable inputs; the handles stay const
+    // to callers.
+    mfh_buf *codes = const_cast<mfh_buf *>(codes_c);
+    mfh_buf *scales = const_cast<mfh_buf *>(scales_c);
+    const int fmt = int(p.format);
+    if (!codes->repacked || codes->repacked_format != fmt) {
+        if (codes->repacked)
+            ctx->pool->release(codes->repacked, codes->repacked_capacity);
+        codes->repacked = ctx->pool->acquire(repacked_bytes(p.format, p.rows, p.inner),
+                                             &codes->repacked_capacity);
+        codes->repacked_format = codes->repacked ? fmt : -1;
+        if (!codes->repacked)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        launch_repack(ctx->stream, p.format, static_cast<const uint8_t *>(codes->dev),
+                      static_cast<uint8_t *>(codes->repacked), p.rows, p.inner);
+    }
+    const bool half = scales->f16_shadow != nullptr;
+    if (!scales->tiled_scales || scales->tiled_format != fmt || scales->tiled_half != half) {
+        if (scales->tiled_scales)
+            ctx->pool->release(scales->tiled_scales, scales->tiled_capacity);
+        scales->tiled_scales = ctx->pool->acquire(
+            tiled_scales_bytes(p.format, p.rows, p.inner, half), &scales->tiled_capacity);
+        scales->tiled_format = scales->tiled_scales ? fmt : -1;
+        scales->tiled_half = half;
+        if (!scales->tiled_scales)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        launch_tile_scales(ctx->stream, p.format, static_cast<const float *>(scales->dev),
+                           scales->tiled_scales, p.rows, p.inner, half);
+    }
+    stream->tiles = static_cast<const uint8_t *>(codes->repacked);
+    stream->tiled_scales = scales->tiled_scales;
+    stream->tiled_half = half;
+    return MFH_OK;
+}
+
+// Whether the matrix-core decode GEMV serves this call.
+bool use_mfma_gemv(const mfh_ctx *ctx, const PackedCall &call)
+{
+    return call.m <= 8 && ctx->kernel_path != 1 && gemv_mfma_supported(call.format);
+}
+
+// Enqueue the kernels of one admitted packed product.  `a`/`b` are the
+// weight operands (b only for two-stream calls).
+mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
+                      const mfh_buf *scales_a, const mfh_buf *codes_b = nullptr,
+                      const mfh_buf *scales_b = nullptr)
 {
     hipStream_t stream = ctx->stream;
     if (call.m == 0 || call.n == 0)
@@ -104,10 +154,22 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call)
             launch_fill_f32(stream, call.out_b, size_t(call.m) * call.n, 0.0f);
         return MFH_OK;
     }
-    if (call.m <= 8)
+    if (use_mfma_gemv(ctx, call)) {
+        Packed p{call.n, call.k, call.format};
+        mfh_status s = prepare_tiles(ctx, codes_a, scales_a, p, &call.a);
+        if (!s && codes_b)
+            s = prepare_tiles(ctx, codes_b, scales_b, p, &call.b);
+        if (s)
+            return s;
+        void *scratch = digits_scratch(ctx, gemv_mfma_scratch_bytes(call));
+        if (!scratch)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        launch_gemv_mfma(stream, call, scratch);
+    } else if (call.m <= 8) {
         launch_gemv_fma(stream, call);
-    else
+    } else {
         launch_gemm_fma(stream, call);
+    }
     if (hipGetLastError() != hipSuccess)
         return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
     return MFH_OK;
@@ -224,7 +286,7 @@ mfh_status mfh_packed_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input
     call.x = static_cast<const float *>(input->dev);
     call.a = stream_of(codes, scales);
     call.out_a = static_cast<float *>(output->dev);
-    return run_packed(ctx, call);
+    return run_packed(ctx, call, codes, scales);
 }
 
 mfh_status mfh_packed_linear_pair(mfh_ctx *ctx, mfh_buf *out_a, mfh_buf *out_b,
@@ -275,7 +337,7 @@ mfh_status mfh_packed_linear_pair(mfh_ctx *ctx, mfh_buf *out_a, mfh_buf *out_b,
     call.b = stream_of(codes_b, scales_b);
     call.out_a = static_cast<float *>(out_a->dev);
     call.out_b = static_cast<float *>(out_b->dev);
-    return run_packed(ctx, call);
+    return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
 }
 
 mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *gate,
@@ -325,7 +387,7 @@ mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf
     call.x = activated;
     call.a = stream_of(codes, scales);
     call.out_a = static_cast<float *>(output->dev);
-    return run_packed(ctx, call);
+    return run_packed(ctx, call, codes, scales);
 }
 
 mfh_status mfh_packed_swiglu_pair(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
@@ -368,7 +430,7 @@ mfh_status mfh_packed_swiglu_pair(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *
     call.a = stream_of(codes_a, scales_a);
     call.b = stream_of(codes_b, scales_b);
     call.out_a = static_cast<float *>(output->dev);
-    return run_packed(ctx, call);
+    return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
 }
 
 }  // extern "C"

@@ -145,30 +145,41 @@ void mark_written(mfh_buf *buf)
         buf->f16_shadow = nullptr;
         buf->f16_capacity = 0;
     }
+    if (buf->tiled_scales) {
+        buf->ctx->pool->release(buf->tiled_scales, buf->tiled_capacity);
+        buf->tiled_scales = nullptr;
+        buf->tiled_capacity = 0;
+        buf->tiled_format = -1;
+    }
+}
+
+// Scratch blocks only grow, and a grown block is never returned to the pool
+// while the context lives: work captured into a graph may still address it.
+static void *grow(mfh_ctx *ctx, void **slot, size_t *capacity, size_t bytes)
+{
+    if (bytes > *capacity) {
+        size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+        void *p = ctx->pool->acquire(want, capacity);
+        if (!p)
+            return nullptr;
+        *slot = p;
+    }
+    return *slot;
 }
 
 void *ids_scratch(mfh_ctx *ctx, size_t bytes)
 {
-    if (bytes > ctx->ids_scratch_capacity) {
-        if (ctx->ids_scratch)
-            ctx->pool->release(ctx->ids_scratch, ctx->ids_scratch_capacity);
-        ctx->ids_scratch = ctx->pool->acquire(bytes, &ctx->ids_scratch_capacity);
-        if (!ctx->ids_scratch)
-            ctx->ids_scratch_capacity = 0;
-    }
-    return ctx->ids_scratch;
+    return grow(ctx, &ctx->ids_scratch, &ctx->ids_scratch_capacity, bytes);
 }
 
 void *work_scratch(mfh_ctx *ctx, size_t bytes)
 {
-    if (bytes > ctx->work_scratch_capacity) {
-        if (ctx->work_scratch)
-            ctx->pool->release(ctx->work_scratch, ctx->work_scratch_capacity);
-        ctx->work_scratch = ctx->pool->acquire(bytes, &ctx->work_scratch_capacity);
-        if (!ctx->work_scratch)
-            ctx->work_scratch_capacity = 0;
-    }
-    return ctx->work_scratch;
+    return grow(ctx, &ctx->work_scratch, &ctx->work_scratch_capacity, bytes);
+}
+
+void *digits_scratch(mfh_ctx *ctx, size_t bytes)
+{
+    return grow(ctx, &ctx->digits_scratch, &ctx->digits_scratch_capacity, bytes);
 }
 
 }  // namespace mfh
@@ -267,6 +278,7 @@ mfh_status make_buffer(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, mfh_dt
             return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
         }
     }
+    ctx->live_buffers.insert(buf);
     ctx->live_bytes += bytes;
     ctx->live_by_class[cls] += bytes;
     uint64_t total = ctx->live_bytes + ctx->pending_result_bytes;
@@ -359,6 +371,25 @@ void mfh_destroy(mfh_ctx *ctx)
     {
         DeviceGuard guard(ctx->device);
         (void)hipStreamSynchronize(ctx->stream);
+        // Orphan every handle still alive: its memory goes with the pool and
+        // its later release/free only deletes the host-side record.
+        for (mfh_buf *buf : ctx->live_buffers) {
+            buf->ctx = nullptr;
+            buf->dev = buf->f16_shadow = buf->repacked = buf->tiled_scales = nullptr;
+        }
+        for (mfh_fence *fence : ctx->live_fences) {
+            (void)hipEventDestroy(fence->event);
+            fence->event = nullptr;
+            fence->ctx = nullptr;
+        }
+        for (mfh_readback *rb : ctx->live_readbacks) {
+            (void)hipEventDestroy(rb->event);
+            if (rb->host)
+                (void)hipHostFree(rb->host);
+            rb->event = nullptr;
+            rb->host = nullptr;
+            rb->ctx = nullptr;
+        }
         ctx->pool.reset();
         (void)hipStreamDestroy(ctx->stream);
     }
@@ -531,7 +562,7 @@ mfh_status mfh_upload_u8(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, cons
         return MFH_OK;
     buf->has_int8_reserved = std::memchr(bytes, 0x80, count) != nullptr;
     if (hipMemcpyAsync(buf->dev, bytes, count, hipMemcpyHostToDevice, ctx->stream) != hipSuccess ||
-        (void)hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        hipStreamSynchronize(ctx->stream) != hipSuccess) {
         (void)hipGetLastError();
         mfh_release(buf);
         *out = nullptr;
@@ -549,8 +580,10 @@ void mfh_release(mfh_buf *buf)
         ctx->pool->release(buf->dev, buf->capacity);
         ctx->pool->release(buf->f16_shadow, buf->f16_capacity);
         ctx->pool->release(buf->repacked, buf->repacked_capacity);
+        ctx->pool->release(buf->tiled_scales, buf->tiled_capacity);
         ctx->live_bytes -= buf->bytes;
         ctx->live_by_class[buf->cls] -= buf->bytes;
+        ctx->live_buffers.erase(buf);
     }
     delete buf;
 }
@@ -589,6 +622,7 @@ mfh_status mfh_fence_submit(mfh_ctx *ctx, mfh_fence **out)
         delete fence;
         return fail(ctx, MFH_BACKEND_FAILURE, "fence submission failed");
     }
+    ctx->live_fences.insert(fence);
     *out = fence;
     return MFH_OK;
 }
@@ -605,6 +639,10 @@ mfh_status mfh_fence_poll(mfh_fence *fence, int *ready)
     if (fence->consumed) {
         *ready = 1;
         return MFH_COMPLETION_CONSUMED;
+    }
+    if (!fence->ctx) {
+        *ready = 1;
+        return MFH_WRONG_BACKEND;  // its backend was destroyed
     }
     DeviceGuard guard(fence->ctx->device);
     hipError_t e = hipEventQuery(fence->event);
@@ -632,9 +670,10 @@ void mfh_fence_free(mfh_fence *fence)
 {
     if (!fence)
         return;
-    {
+    if (fence->ctx) {
         DeviceGuard guard(fence->ctx->device);
         (void)hipEventDestroy(fence->event);
+        fence->ctx->live_fences.erase(fence);
     }
     delete fence;
 }
@@ -680,6 +719,7 @@ mfh_status mfh_read_f32_async(mfh_ctx *ctx, const mfh_buf *buf, mfh_readback **o
         return fail(ctx, MFH_BACKEND_FAILURE, "readback submission failed");
     }
     ctx->pending_result_bytes += buf->bytes;
+    ctx->live_readbacks.insert(rb);
     *out = rb;
     return MFH_OK;
 }
@@ -697,6 +737,10 @@ mfh_status mfh_readback_poll(mfh_readback *rb, int *ready, float *dst, size_t ca
     if (rb->consumed) {
         *ready = 1;
         return MFH_COMPLETION_CONSUMED;
+    }
+    if (!rb->ctx) {
+        *ready = 1;
+        return MFH_WRONG_BACKEND;  // its backend was destroyed
     }
     DeviceGuard guard(rb->ctx->device);
     hipError_t e = hipEventQuery(rb->event);
@@ -729,7 +773,7 @@ void mfh_readback_free(mfh_readback *rb)
 {
     if (!rb)
         return;
-    {
+    if (rb->ctx) {
         DeviceGuard guard(rb->ctx->device);
         // The copy may still be in flight: wait for it before freeing the
         // pinned destination.
@@ -739,6 +783,7 @@ void mfh_readback_free(mfh_readback *rb)
             (void)hipHostFree(rb->host);
         if (!rb->consumed)
             rb->ctx->pending_result_bytes -= rb->count * 4;
+        rb->ctx->live_readbacks.erase(rb);
     }
     delete rb;
 }

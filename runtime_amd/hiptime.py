@@ -1,0 +1,103 @@
+"""HIP events and stream capture over ctypes, for timing and replaying work
+queued on a backend's stream (`mfh_stream`).
+
+Uses the same libamdhip64 the backend library links, so stream and event
+handles are shared with it.  Plumbing for benches and drivers; no compute.
+"""
+from __future__ import annotations
+
+import ctypes
+import ctypes.util
+
+_hip = None
+
+
+def hip() -> ctypes.CDLL:
+    global _hip
+    if _hip is None:
+        _hip = ctypes.CDLL("/opt/rocm/lib/libamdhip64.so.7")
+        P, PP = ctypes.c_void_p, ctypes.POINTER(ctypes.c_void_p)
+        sigs = {
+            "hipEventCreate": [PP],
+            "hipEventDestroy": [P],
+            "hipEventRecord": [P, P],
+            "hipEventSynchronize": [P],
+            "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), P, P],
+            "hipStreamSynchronize": [P],
+            "hipStreamBeginCapture": [P, ctypes.c_int],
+            "hipStreamEndCapture": [P, PP],
+            "hipGraphInstantiate": [PP, P, P, P, ctypes.c_size_t],
+            "hipGraphLaunch": [P, P],
+            "hipGraphExecDestroy": [P],
+            "hipGraphDestroy": [P],
+            "hipGetErrorString": [ctypes.c_int],
+        }
+        for name, args in sigs.items():
+            fn = getattr(_hip, name)
+            fn.argtypes = args
+            fn.restype = ctypes.c_char_p if name == "hipGetErrorString" else ctypes.c_int
+    return _hip
+
+
+def check(err: int, what: str) -> None:
+    if err:
+        raise RuntimeError(f"{what} failed: {hip().hipGetErrorString(err).decode()} ({err})")
+
+
+class Event:
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(hip().hipEventCreate(ctypes.byref(h)), "hipEventCreate")
+        self.handle = h.value
+
+    def record(self, stream: int) -> None:
+        check(hip().hipEventRecord(self.handle, stream), "hipEventRecord")
+
+    def synchronize(self) -> None:
+        check(hip().hipEventSynchronize(self.handle), "hipEventSynchronize")
+
+    def elapsed_ms(self, start: "Event") -> float:
+        ms = ctypes.c_float(0)
+        check(hip().hipEventElapsedTime(ctypes.byref(ms), start.handle, self.handle),
+              "hipEventElapsedTime")
+        return float(ms.value)
+
+    def __del__(self):
+        try:
+            if self.handle:
+                hip().hipEventDestroy(self.handle)
+        except Exception:
+            pass
+
+
+class Graph:
+    """Work captured from one stream, replayable with `launch`."""
+
+    def __init__(self, stream: int, record):
+        """Capture everything `record()` enqueues on `stream`."""
+        check(hip().hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed
+        try:
+            record()
+        finally:
+            g = ctypes.c_void_p()
+            err = hip().hipStreamEndCapture(stream, ctypes.byref(g))
+        check(err, "hipStreamEndCapture")
+        self.graph = g.value
+        e = ctypes.c_void_p()
+        check(hip().hipGraphInstantiate(ctypes.byref(e), self.graph, None, None, 0),
+              "hipGraphInstantiate")
+        self.exec = e.value
+
+    def launch(self, stream: int) -> None:
+        check(hip().hipGraphLaunch(self.exec, stream), "hipGraphLaunch")
+
+    def __del__(self):
+        try:
+            hip().hipGraphExecDestroy(self.exec)
+            hip().hipGraphDestroy(self.graph)
+        except Exception:
+            pass
+
+
+def stream_synchronize(stream: int) -> None:
+    check(hip().hipStreamSynchronize(stream), "hipStreamSynchronize")

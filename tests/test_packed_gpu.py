@@ -21,7 +21,9 @@ from tests.conftest import assert_close, max_rel_err
 
 pytestmark = pytest.mark.gpu
 SCHEMES = ["ternary", "nf4", "int8"]
-PATHS = {"auto": 0}
+# auto selects the matrix-core decode GEMV for ternary/INT8 at m <= 8;
+# fma forces the FP32-FMA kernels everywhere.
+PATHS = {"auto": 0, "fma": 1}
 
 
 def say(*parts):
