@@ -470,7 +470,10 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
 // NF4 GEMV on f16 MFMA.  One loop block = one 16-byte lane load per tile =
 // four 32-wide ksteps = one 128-weight group.
 // ---------------------------------------------------------------------------
-constexpr uint32_t kLutCopies = 16;
+// One table copy: replicating it per lane (to spread LDS banks) measured
+// slower -- the extra build work and LDS footprint cost more than the bank
+// conflicts it removes.
+constexpr uint32_t kLutCopies = 1;
 template <int T, int S>
 struct Nf4Block {
     v4u w[S][T];
