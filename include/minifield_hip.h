@@ -255,6 +255,82 @@ mfh_status mfh_packed_swiglu_pair(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *
  * (inference.rs:268-309). */
 int mfh_supports_ternary_lut2(const mfh_ctx *ctx);
 
+/* ---- dense LFM2 operations (the rest of a forward pass) ---------------- */
+/*
+ * Same operand order as the trait.  Spec structs of the reference
+ * (PackedHeadSpec, RotarySpec, GqaSpec, GatedShortConvSpec, RectCopy2d;
+ * engine-api/src/backend.rs:120-380) are passed as their scalar fields and
+ * validated with the same rules and messages.
+ */
+
+/* InferenceOps::copy (inference.rs:113). */
+mfh_status mfh_copy(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input);
+/* InferenceOps::copy_rect_2d (inference.rs:118-123), RectCopy2d fields. */
+mfh_status mfh_copy_rect_2d(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                            uint64_t source_row, uint64_t source_column,
+                            uint64_t destination_row, uint64_t destination_column,
+                            uint64_t rows, uint64_t columns);
+/* InferenceOps::argmax (inference.rs:131): first strict maximum per row as an
+ * exact f32 index, NaN for a row holding any non-finite value. */
+mfh_status mfh_argmax(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input);
+/* InferenceOps::argmax_masked (inference.rs:140-149): `mask` holds
+ * ceil(width / 64) u64 words, bit i % 64 of word i / 64 admits column i. */
+mfh_status mfh_argmax_masked(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                             const uint64_t *mask, size_t mask_words);
+/* InferenceOps::gather_rows (inference.rs:151-156); token ids as for
+ * mfh_packed_gather_rows. */
+mfh_status mfh_gather_rows(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *table,
+                           const uint32_t *host_ids, size_t host_count,
+                           const mfh_buf *device_ids);
+/* InferenceOps::gather_columns (inference.rs:166-171). */
+mfh_status mfh_gather_columns(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                              const uint32_t *columns, size_t count);
+/* InferenceOps::add / multiply (inference.rs:346-357). */
+mfh_status mfh_add(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *left, const mfh_buf *right);
+mfh_status mfh_multiply(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *left,
+                        const mfh_buf *right);
+/* InferenceOps::linear (inference.rs:358-363): dense f32 X[M,K] * W[N,K]^T. */
+mfh_status mfh_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                      const mfh_buf *weight);
+/* InferenceOps::row_rms_norm (inference.rs:364-370). */
+mfh_status mfh_row_rms_norm(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                            const mfh_buf *weight, float epsilon);
+/* InferenceOps::head_rms_norm (inference.rs:373-380), PackedHeadSpec fields. */
+mfh_status mfh_head_rms_norm(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                             const mfh_buf *weight, uint32_t heads, uint32_t head_dim,
+                             float epsilon);
+/* InferenceOps::split_half_rotary (inference.rs:383-389), RotarySpec fields. */
+mfh_status mfh_split_half_rotary(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                                 const uint64_t *positions, size_t position_count,
+                                 uint32_t heads, uint32_t head_dim, float theta);
+/* InferenceOps::add_row_rms_norm (inference.rs:316-324). */
+mfh_status mfh_add_row_rms_norm(mfh_ctx *ctx, mfh_buf *sum, mfh_buf *normed,
+                                const mfh_buf *left, const mfh_buf *right,
+                                const mfh_buf *weight, float epsilon);
+/* InferenceOps::qk_norm_rope (inference.rs:333-345): RotarySpec (query heads,
+ * head_dim, theta) and the key/value PackedHeadSpec. */
+mfh_status mfh_qk_norm_rope(mfh_ctx *ctx, mfh_buf *query_out, mfh_buf *key_out,
+                            const mfh_buf *query, const mfh_buf *key,
+                            const mfh_buf *query_weight, const mfh_buf *key_weight,
+                            const uint64_t *positions, size_t position_count,
+                            uint32_t query_heads, uint32_t head_dim, float theta,
+                            uint32_t key_value_heads, uint32_t key_value_head_dim,
+                            float epsilon);
+/* InferenceOps::causal_gqa (inference.rs:394-404), GqaSpec fields.  The new
+ * K/V rows are appended at [*cache_len, *cache_len + tokens) and *cache_len
+ * advances only after every check passed. */
+mfh_status mfh_causal_gqa(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *query,
+                          const mfh_buf *key, const mfh_buf *value, mfh_buf *key_cache,
+                          mfh_buf *value_cache, uint64_t *cache_len, uint32_t query_heads,
+                          uint32_t key_value_heads, uint32_t head_dim);
+/* InferenceOps::gated_short_convolution (inference.rs:409-416),
+ * GatedShortConvSpec fields. */
+mfh_status mfh_gated_short_convolution(mfh_ctx *ctx, mfh_buf *output,
+                                       const mfh_buf *projection, const mfh_buf *kernel,
+                                       mfh_buf *history, uint32_t hidden, uint32_t width);
+/* InferenceOps::swiglu (inference.rs:419-424). */
+mfh_status mfh_swiglu(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *gate, const mfh_buf *up);
+
 /* ---- diagnostics (no counterpart in the reference) --------------------- */
 
 /* The HIP stream (hipStream_t) all work of `ctx` is ordered on, so a caller

@@ -26,6 +26,7 @@ _f = ctypes.POINTER(ctypes.c_float)
 _u8 = ctypes.POINTER(ctypes.c_uint8)
 _d = ctypes.POINTER(ctypes.c_double)
 _i64 = ctypes.POINTER(ctypes.c_int64)
+_u64 = ctypes.POINTER(ctypes.c_uint64)
 _SZ = ctypes.c_size_t
 
 _SIGS = {
@@ -43,6 +44,17 @@ _SIGS = {
     "mfo_packed_gather_rows": (ctypes.c_int, [_f, _u8, _f, _SZ, _SZ, _SZ, _i64, _SZ]),
     "mfo_f16_to_f32": (ctypes.c_float, [ctypes.c_uint16]),
     "mfo_dense_f64": (None, [_d, _f, _SZ, _f, _SZ, _SZ]),
+    "mfo_row_rms_norm": (ctypes.c_int, [_f, _f, _f, _SZ, _SZ, ctypes.c_float]),
+    "mfo_head_rms_norm": (ctypes.c_int, [_f, _f, _f, _SZ, _SZ, _SZ, ctypes.c_float]),
+    "mfo_split_half_rotary": (ctypes.c_int, [_f, _f, _u64, _SZ, _SZ, _SZ, ctypes.c_float]),
+    "mfo_qk_norm_rope": (ctypes.c_int, [_f, _f, _f, _f, _f, _f, _u64, _SZ, _SZ, _SZ, _SZ,
+                                        ctypes.c_float, ctypes.c_float]),
+    "mfo_elementwise": (ctypes.c_int, [_f, _f, _f, _SZ, ctypes.c_int]),
+    "mfo_linear": (ctypes.c_int, [_f, _f, _f, _SZ, _SZ, _SZ]),
+    "mfo_argmax": (None, [_f, _f, _SZ, _SZ, _u64]),
+    "mfo_gather_rows": (ctypes.c_int, [_f, _f, _SZ, _SZ, _i64, _SZ]),
+    "mfo_causal_gqa": (ctypes.c_int, [_f, _f, _f, _f, _f, _f, _u64, _SZ, _SZ, _SZ, _SZ]),
+    "mfo_gated_short_convolution": (ctypes.c_int, [_f, _f, _f, _f, _SZ, _SZ, _SZ]),
 }
 
 _lib = None
@@ -235,3 +247,136 @@ def dequantize_f32(codes, scales, scheme: str) -> np.ndarray:
     else:
         levels = codes.view(np.int8).astype(np.float32)
     return levels * np.repeat(scales, 128, axis=1)
+
+
+# ---- dense LFM2 operations (mf_dense_oracle.c) -----------------------------
+
+def _cu64(a):
+    return np.ascontiguousarray(a, dtype=np.uint64).reshape(-1)
+
+
+def row_rms_norm(x, weight, epsilon) -> np.ndarray:
+    """CpuBackend::row_rms_norm over [rows, width]."""
+    x, weight = _c32(x), _c32(weight)
+    out = np.zeros_like(x)
+    _check(lib().mfo_row_rms_norm(_fp(out), _fp(x), _fp(weight), x.shape[0], x.shape[1],
+                                  epsilon))
+    return out
+
+
+def head_rms_norm(x, weight, heads, head_dim, epsilon) -> np.ndarray:
+    x, weight = _c32(x), _c32(weight)
+    out = np.zeros_like(x)
+    _check(lib().mfo_head_rms_norm(_fp(out), _fp(x), _fp(weight), x.shape[0], heads, head_dim,
+                                   epsilon))
+    return out
+
+
+def split_half_rotary(x, positions, heads, head_dim, theta) -> np.ndarray:
+    x, pos = _c32(x), _cu64(positions)
+    out = np.zeros_like(x)
+    _check(lib().mfo_split_half_rotary(_fp(out), _fp(x), pos.ctypes.data_as(_u64), x.shape[0],
+                                       heads, head_dim, theta))
+    return out
+
+
+def qk_norm_rope(query, key, query_weight, key_weight, positions, query_heads, key_heads,
+                 head_dim, theta, epsilon):
+    query, key = _c32(query), _c32(key)
+    qw, kw, pos = _c32(query_weight), _c32(key_weight), _cu64(positions)
+    q_out, k_out = np.zeros_like(query), np.zeros_like(key)
+    _check(lib().mfo_qk_norm_rope(_fp(q_out), _fp(k_out), _fp(query), _fp(key), _fp(qw),
+                                  _fp(kw), pos.ctypes.data_as(_u64), query.shape[0],
+                                  query_heads, key_heads, head_dim, theta, epsilon))
+    return q_out, k_out
+
+
+def add(left, right) -> np.ndarray:
+    left, right = _c32(left), _c32(right)
+    out = np.zeros_like(left)
+    _check(lib().mfo_elementwise(_fp(out), _fp(left), _fp(right), left.size, 0))
+    return out
+
+
+def multiply(left, right) -> np.ndarray:
+    left, right = _c32(left), _c32(right)
+    out = np.zeros_like(left)
+    _check(lib().mfo_elementwise(_fp(out), _fp(left), _fp(right), left.size, 1))
+    return out
+
+
+def add_row_rms_norm(left, right, weight, epsilon):
+    """CpuBackend::add_row_rms_norm: add, then row_rms_norm of the sum."""
+    total = add(left, right)
+    return total, row_rms_norm(total, weight, epsilon)
+
+
+def linear(x, weight) -> np.ndarray:
+    x, weight = _c32(x), _c32(weight)
+    m, k = x.shape
+    n = weight.shape[0]
+    out = np.zeros((m, n), dtype=np.float32)
+    _check(lib().mfo_linear(_fp(out), _fp(x), _fp(weight), m, n, k))
+    return out
+
+
+def argmax(x, mask=None) -> np.ndarray:
+    x = _c32(x)
+    out = np.zeros(x.shape[0], dtype=np.float32)
+    mask_ptr = None
+    if mask is not None:
+        mask = _cu64(mask)
+        mask_ptr = mask.ctypes.data_as(_u64)
+    lib().mfo_argmax(_fp(out), _fp(x), x.shape[0], x.shape[1], mask_ptr)
+    return out
+
+
+def gather_rows(table, ids) -> np.ndarray:
+    """ids: int64 row ids, -1 for a None (NaN) row."""
+    table = _c32(table)
+    ids = np.ascontiguousarray(ids, dtype=np.int64).reshape(-1)
+    out = np.zeros((ids.size, table.shape[1]), dtype=np.float32)
+    _check(lib().mfo_gather_rows(_fp(out), _fp(table), table.shape[0], table.shape[1],
+                                 ids.ctypes.data_as(_i64), ids.size))
+    return out
+
+
+def gather_columns(x, columns) -> np.ndarray:
+    """CpuBackend::gather_columns (dense.rs:143-149): out[r, k] = x[r, columns[k]]."""
+    x = _c32(x)
+    return np.ascontiguousarray(x[:, np.asarray(columns, dtype=np.int64)])
+
+
+def copy_rect_2d(dst, src, rect) -> np.ndarray:
+    """CpuBackend::copy_rect_2d (dense.rs:311-339) on a copy of `dst`;
+    rect = (source_row, source_column, destination_row, destination_column,
+    rows, columns)."""
+    sr, sc, dr, dc, rows, cols = rect
+    out = _c32(dst).copy()
+    out[dr:dr + rows, dc:dc + cols] = _c32(src)[sr:sr + rows, sc:sc + cols]
+    return out
+
+
+def causal_gqa(query, key, value, key_cache, value_cache, cache_len, query_heads, key_heads,
+               head_dim):
+    """Returns (output, key_cache, value_cache, new_cache_len); the caches
+    passed in are not modified."""
+    query, key, value = _c32(query), _c32(key), _c32(value)
+    kc, vc = _c32(key_cache).copy(), _c32(value_cache).copy()
+    out = np.zeros_like(query)
+    length = ctypes.c_uint64(cache_len)
+    _check(lib().mfo_causal_gqa(_fp(out), _fp(query), _fp(key), _fp(value), _fp(kc), _fp(vc),
+                                ctypes.byref(length), query.shape[0], query_heads, key_heads,
+                                head_dim))
+    return out, kc, vc, length.value
+
+
+def gated_short_convolution(projection, kernel, history, hidden, width):
+    """Returns (output, new_history); the history passed in is not modified."""
+    projection, kernel = _c32(projection), _c32(kernel)
+    hist = _c32(history).copy()
+    tokens = projection.shape[0]
+    out = np.zeros((tokens, hidden), dtype=np.float32)
+    _check(lib().mfo_gated_short_convolution(_fp(out), _fp(projection), _fp(kernel), _fp(hist),
+                                             tokens, hidden, width))
+    return out, hist

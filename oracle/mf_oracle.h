@@ -50,4 +50,26 @@ float mfo_f16_to_f32(uint16_t bits);
 void mfo_dense_f64(double *out, const float *x, size_t m, const float *weights, size_t n,
                    size_t k);
 
+/* Dense LFM2 operations (mf_dense_oracle.c). */
+int mfo_row_rms_norm(float *out, const float *in, const float *weight, size_t rows,
+                     size_t width, float epsilon);
+int mfo_head_rms_norm(float *out, const float *in, const float *weight, size_t tokens,
+                      size_t heads, size_t head_dim, float epsilon);
+int mfo_split_half_rotary(float *out, const float *in, const uint64_t *positions, size_t tokens,
+                          size_t heads, size_t head_dim, float theta);
+int mfo_qk_norm_rope(float *query_out, float *key_out, const float *query, const float *key,
+                     const float *query_weight, const float *key_weight,
+                     const uint64_t *positions, size_t tokens, size_t query_heads,
+                     size_t key_heads, size_t head_dim, float theta, float epsilon);
+int mfo_elementwise(float *out, const float *left, const float *right, size_t count, int op);
+int mfo_linear(float *out, const float *x, const float *w, size_t m, size_t n, size_t k);
+void mfo_argmax(float *out, const float *in, size_t rows, size_t width, const uint64_t *mask);
+int mfo_gather_rows(float *out, const float *table, size_t rows, size_t columns,
+                    const int64_t *ids, size_t count);
+int mfo_causal_gqa(float *out, const float *query, const float *key, const float *value,
+                   float *key_cache, float *value_cache, uint64_t *cache_len, size_t tokens,
+                   size_t query_heads, size_t key_heads, size_t head_dim);
+int mfo_gated_short_convolution(float *out, const float *projection, const float *kernel,
+                                float *history, size_t tokens, size_t hidden, size_t width);
+
 #endif

@@ -88,6 +88,27 @@ SIGNATURES = {
     "mfh_packed_swiglu_linear": (S, [P, P, P, P, P, P]),
     "mfh_packed_swiglu_pair": (S, [P, P, P, P, P, P, P]),
     "mfh_supports_ternary_lut2": (ctypes.c_int, [P]),
+    # dense ops
+    "mfh_copy": (S, [P, P, P]),
+    "mfh_copy_rect_2d": (S, [P, P, P] + [ctypes.c_uint64] * 6),
+    "mfh_argmax": (S, [P, P, P]),
+    "mfh_argmax_masked": (S, [P, P, P, c_u64_p, SZ]),
+    "mfh_gather_rows": (S, [P, P, P, c_u32_p, SZ, P]),
+    "mfh_gather_columns": (S, [P, P, P, c_u32_p, SZ]),
+    "mfh_add": (S, [P, P, P, P]),
+    "mfh_multiply": (S, [P, P, P, P]),
+    "mfh_linear": (S, [P, P, P, P]),
+    "mfh_row_rms_norm": (S, [P, P, P, P, ctypes.c_float]),
+    "mfh_head_rms_norm": (S, [P, P, P, P, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
+    "mfh_split_half_rotary": (S, [P, P, P, c_u64_p, SZ, ctypes.c_uint32, ctypes.c_uint32,
+                                  ctypes.c_float]),
+    "mfh_add_row_rms_norm": (S, [P, P, P, P, P, P, ctypes.c_float]),
+    "mfh_qk_norm_rope": (S, [P, P, P, P, P, P, P, c_u64_p, SZ, ctypes.c_uint32, ctypes.c_uint32,
+                             ctypes.c_float, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_float]),
+    "mfh_causal_gqa": (S, [P, P, P, P, P, P, P, c_u64_p, ctypes.c_uint32, ctypes.c_uint32,
+                           ctypes.c_uint32]),
+    "mfh_gated_short_convolution": (S, [P, P, P, P, P, ctypes.c_uint32, ctypes.c_uint32]),
+    "mfh_swiglu": (S, [P, P, P, P]),
     # diagnostics
     "mfh_stream": (P, [P]),
     "mfh_set_kernel_path": (ctypes.c_int, [P, ctypes.c_int]),

@@ -312,3 +312,151 @@ class HipBackend:
         self._check(_ffi.lib().mfh_packed_swiglu_pair(
             self._ctx, output.handle, input.handle, codes_a.handle, scales_a.handle,
             codes_b.handle, scales_b.handle))
+
+    # ---- dense ops (inference.rs:113-424) --------------------------------
+
+    def copy(self, output: Buffer, input: Buffer) -> None:
+        self._check(_ffi.lib().mfh_copy(self._ctx, output.handle, input.handle))
+
+    def copy_rect_2d(self, output: Buffer, input: Buffer, rect: "RectCopy2d") -> None:
+        self._check(_ffi.lib().mfh_copy_rect_2d(
+            self._ctx, output.handle, input.handle, rect.source_row, rect.source_column,
+            rect.destination_row, rect.destination_column, rect.rows, rect.columns))
+
+    def argmax(self, output: Buffer, input: Buffer) -> None:
+        self._check(_ffi.lib().mfh_argmax(self._ctx, output.handle, input.handle))
+
+    def argmax_masked(self, output: Buffer, input: Buffer, mask) -> None:
+        words = np.ascontiguousarray(mask, dtype=np.uint64).reshape(-1)
+        ptr = words.ctypes.data_as(_ffi.c_u64_p) if words.size else None
+        self._check(_ffi.lib().mfh_argmax_masked(self._ctx, output.handle, input.handle, ptr,
+                                                 words.size))
+
+    def gather_rows(self, output: Buffer, table: Buffer, ids) -> None:
+        """`ids` as for `packed_gather_rows`."""
+        lib = _ffi.lib()
+        if isinstance(ids, Buffer):
+            self._check(lib.mfh_gather_rows(self._ctx, output.handle, table.handle, None, 0,
+                                            ids.handle))
+        else:
+            host = np.ascontiguousarray(ids, dtype=np.uint32).reshape(-1)
+            ptr = host.ctypes.data_as(_ffi.c_u32_p) if host.size else None
+            self._check(lib.mfh_gather_rows(self._ctx, output.handle, table.handle, ptr,
+                                            host.size, None))
+
+    def gather_columns(self, output: Buffer, input: Buffer, columns) -> None:
+        cols = np.ascontiguousarray(columns, dtype=np.uint32).reshape(-1)
+        ptr = cols.ctypes.data_as(_ffi.c_u32_p) if cols.size else None
+        self._check(_ffi.lib().mfh_gather_columns(self._ctx, output.handle, input.handle, ptr,
+                                                  cols.size))
+
+    def add(self, output: Buffer, left: Buffer, right: Buffer) -> None:
+        self._check(_ffi.lib().mfh_add(self._ctx, output.handle, left.handle, right.handle))
+
+    def multiply(self, output: Buffer, left: Buffer, right: Buffer) -> None:
+        self._check(_ffi.lib().mfh_multiply(self._ctx, output.handle, left.handle,
+                                            right.handle))
+
+    def linear(self, output: Buffer, input: Buffer, weight: Buffer) -> None:
+        self._check(_ffi.lib().mfh_linear(self._ctx, output.handle, input.handle,
+                                          weight.handle))
+
+    def row_rms_norm(self, output: Buffer, input: Buffer, weight: Buffer, epsilon: float) -> None:
+        self._check(_ffi.lib().mfh_row_rms_norm(self._ctx, output.handle, input.handle,
+                                                weight.handle, epsilon))
+
+    def head_rms_norm(self, output: Buffer, input: Buffer, weight: Buffer,
+                      heads: "PackedHeadSpec", epsilon: float) -> None:
+        self._check(_ffi.lib().mfh_head_rms_norm(self._ctx, output.handle, input.handle,
+                                                 weight.handle, heads.heads, heads.head_dim,
+                                                 epsilon))
+
+    def split_half_rotary(self, output: Buffer, input: Buffer, positions,
+                          spec: "RotarySpec") -> None:
+        pos = np.ascontiguousarray(positions, dtype=np.uint64).reshape(-1)
+        ptr = pos.ctypes.data_as(_ffi.c_u64_p) if pos.size else None
+        self._check(_ffi.lib().mfh_split_half_rotary(
+            self._ctx, output.handle, input.handle, ptr, pos.size, spec.heads.heads,
+            spec.heads.head_dim, spec.theta))
+
+    def add_row_rms_norm(self, sum: Buffer, normed: Buffer, left: Buffer, right: Buffer,
+                         weight: Buffer, epsilon: float) -> None:
+        self._check(_ffi.lib().mfh_add_row_rms_norm(self._ctx, sum.handle, normed.handle,
+                                                    left.handle, right.handle, weight.handle,
+                                                    epsilon))
+
+    def qk_norm_rope(self, query_out: Buffer, key_out: Buffer, query: Buffer, key: Buffer,
+                     query_weight: Buffer, key_weight: Buffer, positions, rope: "RotarySpec",
+                     key_value_heads: "PackedHeadSpec", epsilon: float) -> None:
+        pos = np.ascontiguousarray(positions, dtype=np.uint64).reshape(-1)
+        ptr = pos.ctypes.data_as(_ffi.c_u64_p) if pos.size else None
+        self._check(_ffi.lib().mfh_qk_norm_rope(
+            self._ctx, query_out.handle, key_out.handle, query.handle, key.handle,
+            query_weight.handle, key_weight.handle, ptr, pos.size, rope.heads.heads,
+            rope.heads.head_dim, rope.theta, key_value_heads.heads, key_value_heads.head_dim,
+            epsilon))
+
+    def causal_gqa(self, output: Buffer, query: Buffer, key: Buffer, value: Buffer,
+                   key_cache: Buffer, value_cache: Buffer, cache_len: "CacheLength",
+                   spec: "GqaSpec") -> None:
+        """`cache_len` is a mutable `CacheLength`; it advances only on success."""
+        length = ctypes.c_uint64(cache_len.value)
+        self._check(_ffi.lib().mfh_causal_gqa(
+            self._ctx, output.handle, query.handle, key.handle, value.handle, key_cache.handle,
+            value_cache.handle, ctypes.byref(length), spec.query_heads, spec.key_value_heads,
+            spec.head_dim))
+        cache_len.value = length.value
+
+    def gated_short_convolution(self, output: Buffer, projection: Buffer, kernel: Buffer,
+                                history: Buffer, spec: "GatedShortConvSpec") -> None:
+        self._check(_ffi.lib().mfh_gated_short_convolution(
+            self._ctx, output.handle, projection.handle, kernel.handle, history.handle,
+            spec.hidden, spec.width))
+
+    def swiglu(self, output: Buffer, gate: Buffer, up: Buffer) -> None:
+        self._check(_ffi.lib().mfh_swiglu(self._ctx, output.handle, gate.handle, up.handle))
+
+
+# ---- operation descriptors (engine-api/src/backend.rs:128-383) -------------
+# Plain carriers: the library validates them with the reference's rules and
+# messages when an operation receives them.
+
+@dataclass(frozen=True)
+class RectCopy2d:
+    source_row: int
+    source_column: int
+    destination_row: int
+    destination_column: int
+    rows: int
+    columns: int
+
+
+@dataclass(frozen=True)
+class PackedHeadSpec:
+    heads: int
+    head_dim: int
+
+
+@dataclass(frozen=True)
+class RotarySpec:
+    heads: PackedHeadSpec
+    theta: float
+
+
+@dataclass(frozen=True)
+class GqaSpec:
+    query_heads: int
+    key_value_heads: int
+    head_dim: int
+
+
+@dataclass(frozen=True)
+class GatedShortConvSpec:
+    hidden: int
+    width: int
+
+
+@dataclass
+class CacheLength:
+    """The `&mut u64` cache length of `causal_gqa`."""
+    value: int = 0

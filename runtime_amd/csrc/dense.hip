@@ -1,0 +1,709 @@
+// Dense f32 kernels of the LFM2 forward pass: copies, gathers, element-wise
+// arithmetic, row selectors, RMS normalisation, split-half rotary, causal
+// grouped-query attention and the gated short convolution.
+//
+// Arithmetic follows the reference's scalar f32 code
+// (crates/backend-cpu/src/{dense,normalization_rotary,attention_convolution}.rs):
+// contraction is off, so every product and sum rounds where the reference's
+// does.  Reductions the reference runs sequentially (sums of squares, softmax
+// denominators, attention-weighted sums) run here as fixed-shape trees, so
+// results are deterministic run to run and agree with the reference within
+// f32 reassociation error.  Attention scores keep the reference's sequential
+// dot order per key and are bit-identical to it.
+//
+// Unlike the reference's CPU backend, a non-finite intermediate does not
+// raise an error: device work is deferred, so NaN/Inf propagate to the
+// outputs (argmax turns them into its NaN marker), as on the reference's
+// device backends.
+#pragma clang fp contract(off)
+
+#include "kernels.hpp"
+
+namespace mfh {
+namespace {
+
+constexpr int kBlock = 256;
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v += __shfl_xor(v, offset, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
+}
+
+// Block-wide sum of a kBlock-thread block, the same value returned to every
+// thread.  `scratch` holds kBlock / 64 floats.
+__device__ __forceinline__ float block_sum(float v, float *scratch)
+{
+    v = wave_sum(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        scratch[wave] = v;
+    __syncthreads();
+    float total = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w)
+        total += scratch[w];
+    return total;
+}
+
+__device__ __forceinline__ float block_max(float v, float *scratch)
+{
+    v = wave_max(v);
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        scratch[wave] = v;
+    __syncthreads();
+    float best = scratch[0];
+#pragma unroll
+    for (int w = 1; w < kBlock / 64; ++w)
+        best = fmaxf(best, scratch[w]);
+    return best;
+}
+
+unsigned grid_for(size_t count, size_t per_block = kBlock)
+{
+    size_t blocks = (count + per_block - 1) / per_block;
+    return unsigned(blocks < 65536 * 4 ? (blocks ? blocks : 1) : 65536 * 4);
+}
+
+// ---- copies ------------------------------------------------------------
+
+__global__ __launch_bounds__(kBlock) void copy_kernel(float *__restrict__ dst,
+                                                      const float *__restrict__ src, size_t count)
+{
+    // Buffers start on pool blocks (256-byte aligned): move float4s, then
+    // the tail.
+    const size_t quads = count / 4;
+    const size_t stride = size_t(gridDim.x) * kBlock;
+    for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < quads; i += stride)
+        reinterpret_cast<float4 *>(dst)[i] = reinterpret_cast<const float4 *>(src)[i];
+    for (size_t i = quads * 4 + size_t(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride)
+        dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(kBlock) void rect_copy_kernel(float *__restrict__ dst,
+                                                           const float *__restrict__ src,
+                                                           RectCopy rect)
+{
+    for (uint64_t row = blockIdx.x; row < rect.rows; row += gridDim.x) {
+        const float *s = src + (rect.source_row + row) * rect.source_width + rect.source_column;
+        float *d = dst + (rect.destination_row + row) * rect.destination_width +
+                   rect.destination_column;
+        for (uint64_t c = threadIdx.x; c < rect.columns; c += kBlock)
+            d[c] = s[c];
+    }
+}
+
+// ---- selectors ---------------------------------------------------------
+
+// A device row selector is valid when finite, integral and in [0, 2^24)
+// (backend-cpu/src/dense.rs:24-53) and, for a table, below its row count.
+__device__ __forceinline__ bool valid_row(float id, uint32_t rows)
+{
+    return isfinite(id) && id >= 0.0f && truncf(id) == id && id < 16777216.0f &&
+           uint32_t(id) < rows;
+}
+
+__global__ __launch_bounds__(kBlock) void gather_rows_kernel(float *__restrict__ out,
+                                                             const float *__restrict__ table,
+                                                             const float *__restrict__ ids,
+                                                             uint32_t count, uint32_t rows,
+                                                             uint64_t columns)
+{
+    for (uint32_t r = blockIdx.x; r < count; r += gridDim.x) {
+        const float id = ids[r];
+        float *dst = out + uint64_t(r) * columns;
+        if (valid_row(id, rows)) {
+            const float *src = table + uint64_t(uint32_t(id)) * columns;
+            for (uint64_t c = threadIdx.x; c < columns; c += kBlock)
+                dst[c] = src[c];
+        } else {
+            for (uint64_t c = threadIdx.x; c < columns; c += kBlock)
+                dst[c] = __builtin_nanf("");
+        }
+    }
+}
+
+__global__ __launch_bounds__(kBlock) void gather_columns_kernel(float *__restrict__ out,
+                                                                const float *__restrict__ in,
+                                                                const uint32_t *__restrict__ cols,
+                                                                uint64_t rows, uint64_t width,
+                                                                uint32_t count)
+{
+    const uint64_t total = rows * count;
+    const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+    for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const uint64_t r = i / count;
+        const uint32_t k = uint32_t(i - r * count);
+        out[i] = in[r * width + cols[k]];
+    }
+}
+
+// Row argmax: first strict maximum among admitted finite values; any
+// admitted non-finite value, or no admitted value, gives NaN
+// (backend-cpu/src/dense.rs:373-473).  One 1024-thread block per row; each
+// thread scans a strided slice in increasing order, then (value, index)
+// pairs reduce with ties going to the lower index.
+constexpr int kArgmaxBlock = 1024;
+
+// Whether candidate (ov, oi) replaces (best, index); UINT32_MAX marks none.
+__device__ __forceinline__ bool takes(float ov, uint32_t oi, float best, uint32_t index)
+{
+    return oi != UINT32_MAX && (index == UINT32_MAX || ov > best || (ov == best && oi < index));
+}
+
+__device__ void argmax_row(float *out, const float *__restrict__ row, uint32_t width,
+                           const uint64_t *__restrict__ mask)
+{
+    __shared__ float best_value[kArgmaxBlock / 64];
+    __shared__ uint32_t best_index[kArgmaxBlock / 64];
+    __shared__ int poison[kArgmaxBlock / 64];
+    float best = -__builtin_inff();
+    uint32_t index = UINT32_MAX;
+    int poisoned = 0;
+    for (uint32_t j = threadIdx.x; j < width; j += kArgmaxBlock) {
+        if (mask && !((mask[j >> 6] >> (j & 63)) & 1))
+            continue;
+        const float v = row[j];
+        if (!isfinite(v)) {
+            poisoned = 1;
+        } else if (index == UINT32_MAX || v > best) {
+            // Strictly greater only: a thread's indices increase, so equal
+            // values keep the earlier one.
+            best = v;
+            index = j;
+        }
+    }
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1) {
+        const float ov = __shfl_xor(best, offset, 64);
+        const uint32_t oi = __shfl_xor(index, offset, 64);
+        poisoned |= __shfl_xor(poisoned, offset, 64);
+        if (takes(ov, oi, best, index)) {
+            best = ov;
+            index = oi;
+        }
+    }
+    const int wave = threadIdx.x >> 6;
+    if ((threadIdx.x & 63) == 0) {
+        best_value[wave] = best;
+        best_index[wave] = index;
+        poison[wave] = poisoned;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kArgmaxBlock / 64; ++w) {
+            poisoned |= poison[w];
+            if (takes(best_value[w], best_index[w], best, index)) {
+                best = best_value[w];
+                index = best_index[w];
+            }
+        }
+        *out = (poisoned || index == UINT32_MAX) ? __builtin_nanf("") : float(index);
+    }
+    // The shared slots are rewritten by the next row.
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(kArgmaxBlock) void argmax_kernel(float *__restrict__ out,
+                                                              const float *__restrict__ in,
+                                                              uint32_t rows, uint32_t width,
+                                                              const uint64_t *__restrict__ mask)
+{
+    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x)
+        argmax_row(out + r, in + uint64_t(r) * width, width, mask);
+}
+
+// ---- element-wise ------------------------------------------------------
+
+template <int OP>
+__global__ __launch_bounds__(kBlock) void binary_kernel(float *__restrict__ out,
+                                                        const float *__restrict__ left,
+                                                        const float *__restrict__ right,
+                                                        size_t count)
+{
+    const size_t stride = size_t(gridDim.x) * kBlock;
+    for (size_t i = size_t(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride)
+        out[i] = OP == 0 ? left[i] + right[i] : left[i] * right[i];
+}
+
+// ---- dense linear ------------------------------------------------------
+
+// X[m, k] . W[n, k]^T: one wave per output element, lanes stride k.
+__global__ __launch_bounds__(kBlock) void linear_kernel(float *__restrict__ out,
+                                                        const float *__restrict__ x,
+                                                        const float *__restrict__ w, uint32_t m,
+                                                        uint32_t n, uint32_t k)
+{
+    const uint64_t total = uint64_t(m) * n;
+    const uint64_t waves = uint64_t(gridDim.x) * (kBlock / 64);
+    const int lane = threadIdx.x & 63;
+    for (uint64_t o = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6); o < total;
+         o += waves) {
+        const uint32_t row = uint32_t(o / n);
+        const uint32_t col = uint32_t(o - uint64_t(row) * n);
+        const float *xr = x + uint64_t(row) * k;
+        const float *wr = w + uint64_t(col) * k;
+        float acc = 0.0f;
+        for (uint32_t i = lane; i < k; i += 64)
+            acc += xr[i] * wr[i];
+        acc = wave_sum(acc);
+        if (lane == 0)
+            out[o] = acc;
+    }
+}
+
+// ---- RMS normalisation -------------------------------------------------
+
+// reciprocal = 1 / sqrt(sum(x * x) / width + epsilon); out = (x * r) * w
+// (backend-cpu/src/normalization_rotary.rs:55-79).  With ADD the row is
+// first formed as left + right and stored to `sum`
+// (normalization_rotary.rs:223-235).  One block per row; each thread reads
+// back only the elements it wrote.
+template <bool ADD>
+__global__ __launch_bounds__(kBlock) void row_rms_kernel(float *__restrict__ out,
+                                                         float *__restrict__ sum,
+                                                         const float *__restrict__ in,
+                                                         const float *__restrict__ right,
+                                                         const float *__restrict__ weight,
+                                                         uint64_t rows, uint32_t width,
+                                                         float epsilon)
+{
+    __shared__ float scratch[kBlock / 64];
+    const float width_f = float(width);
+    for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const uint64_t base = r * width;
+        float squares = 0.0f;
+        for (uint32_t c = threadIdx.x; c < width; c += kBlock) {
+            float v = in[base + c];
+            if (ADD) {
+                v = v + right[base + c];
+                sum[base + c] = v;
+            }
+            squares += v * v;
+        }
+        squares = block_sum(squares, scratch);
+        const float reciprocal = 1.0f / sqrtf(squares / width_f + epsilon);
+        const float *src = ADD ? sum : in;
+        for (uint32_t c = threadIdx.x; c < width; c += kBlock) {
+            const float normalized = src[base + c] * reciprocal;
+            out[base + c] = normalized * weight[c];
+        }
+    }
+}
+
+// Head-local RMS norm over packed [tokens, heads * head_dim] rows
+// (normalization_rotary.rs:124-151): one wave per (token, head).
+__global__ __launch_bounds__(kBlock) void head_rms_kernel(float *__restrict__ out,
+                                                          const float *__restrict__ in,
+                                                          const float *__restrict__ weight,
+                                                          uint64_t segments, uint32_t head_dim,
+                                                          float epsilon)
+{
+    const int lane = threadIdx.x & 63;
+    const uint64_t waves = uint64_t(gridDim.x) * (kBlock / 64);
+    const float dim_f = float(head_dim);
+    for (uint64_t s = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6); s < segments;
+         s += waves) {
+        const uint64_t base = s * head_dim;
+        float squares = 0.0f;
+        for (uint32_t c = lane; c < head_dim; c += 64) {
+            const float v = in[base + c];
+            squares += v * v;
+        }
+        squares = wave_sum(squares);
+        const float reciprocal = 1.0f / sqrtf(squares / dim_f + epsilon);
+        for (uint32_t c = lane; c < head_dim; c += 64) {
+            const float normalized = in[base + c] * reciprocal;
+            out[base + c] = normalized * weight[c];
+        }
+    }
+}
+
+// ---- split-half rotary -------------------------------------------------
+
+// The reference's rotation coefficients: frequency = f32(theta^(-2c/d)) in
+// f64, angle = position * frequency in f32, sine and cosine in f64 rounded
+// to f32 (normalization_rotary.rs:196-207).
+struct Rotation {
+    float cosine, sine;
+};
+
+__device__ __forceinline__ Rotation rotation(float position, uint32_t column, uint32_t head_dim,
+                                             float theta)
+{
+    const double exponent = -2.0 * double(column) / double(head_dim);
+    const float frequency = float(pow(double(theta), exponent));
+    const float angle = position * frequency;
+    return {float(cos(double(angle))), float(sin(double(angle)))};
+}
+
+// One thread per (token, head, column < half).
+__global__ __launch_bounds__(kBlock) void rotary_kernel(float *__restrict__ out,
+                                                        const float *__restrict__ in,
+                                                        const float *__restrict__ positions,
+                                                        uint64_t tokens, uint32_t heads,
+                                                        uint32_t head_dim, float theta)
+{
+    const uint32_t half = head_dim / 2;
+    const uint64_t total = tokens * heads * half;
+    const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+    for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const uint64_t segment = i / half;
+        const uint32_t column = uint32_t(i - segment * half);
+        const uint64_t token = segment / heads;
+        const Rotation rot = rotation(positions[token], column, head_dim, theta);
+        const uint64_t base = segment * head_dim;
+        const float first = in[base + column];
+        const float second = in[base + half + column];
+        out[base + column] = first * rot.cosine - second * rot.sine;
+        out[base + half + column] = second * rot.cosine + first * rot.sine;
+    }
+}
+
+// Per-head RMS norm then split-half rotary for query and key heads in one
+// launch (normalization_rotary.rs:246-369): one wave per (token, head),
+// query heads first.
+__global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(
+    float *__restrict__ query_out, float *__restrict__ key_out, const float *__restrict__ query,
+    const float *__restrict__ key, const float *__restrict__ query_weight,
+    const float *__restrict__ key_weight, const float *__restrict__ positions, uint64_t tokens,
+    uint32_t query_heads, uint32_t key_heads, uint32_t head_dim, float theta, float epsilon)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t heads = query_heads + key_heads;
+    const uint64_t segments = tokens * heads;
+    const uint64_t waves = uint64_t(gridDim.x) * (kBlock / 64);
+    const uint32_t half = head_dim / 2;
+    const float dim_f = float(head_dim);
+    for (uint64_t s = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6); s < segments;
+         s += waves) {
+        const uint64_t token = s / heads;
+        const uint32_t head = uint32_t(s - token * heads);
+        const bool is_query = head < query_heads;
+        const uint32_t h = is_query ? head : head - query_heads;
+        const uint64_t base =
+            (token * (is_query ? query_heads : key_heads) + h) * uint64_t(head_dim);
+        const float *in = (is_query ? query : key) + base;
+        float *out = (is_query ? query_out : key_out) + base;
+        const float *weight = is_query ? query_weight : key_weight;
+        float squares = 0.0f;
+        for (uint32_t c = lane; c < head_dim; c += 64) {
+            const float v = in[c];
+            squares += v * v;
+        }
+        squares = wave_sum(squares);
+        const float reciprocal = 1.0f / sqrtf(squares / dim_f + epsilon);
+        const float position = positions[token];
+        for (uint32_t c = lane; c < half; c += 64) {
+            const float first = (in[c] * reciprocal) * weight[c];
+            const float second = (in[half + c] * reciprocal) * weight[half + c];
+            const Rotation rot = rotation(position, c, head_dim, theta);
+            out[c] = first * rot.cosine - second * rot.sine;
+            out[half + c] = second * rot.cosine + first * rot.sine;
+        }
+    }
+}
+
+// ---- causal grouped-query attention ------------------------------------
+
+// Append the new key/value rows at row `start` of both caches.
+__global__ __launch_bounds__(kBlock) void cache_append_kernel(float *__restrict__ key_cache,
+                                                              float *__restrict__ value_cache,
+                                                              const float *__restrict__ key,
+                                                              const float *__restrict__ value,
+                                                              uint64_t offset, uint64_t count)
+{
+    const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+    for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) {
+        key_cache[offset + i] = key[i];
+        value_cache[offset + i] = value[i];
+    }
+}
+
+constexpr int kKeyChunk = 1024;
+
+// One block per (token, query head) over caches that already hold every
+// visible key (the append runs first).  Three passes over the visible keys
+// as in the reference (attention_convolution.rs:90-170): the maximum score,
+// the softmax denominator, then probability-weighted values, with scores
+// recomputed per pass.  Each score is a sequential dot in dimension order,
+// the reference's exact arithmetic.
+__global__ __launch_bounds__(kBlock) void gqa_kernel(float *__restrict__ out,
+                                                     const float *__restrict__ query,
+                                                     const float *__restrict__ key_cache,
+                                                     const float *__restrict__ value_cache,
+                                                     GqaShape g)
+{
+    extern __shared__ float lds[];
+    float *q = lds;                        // head_dim
+    float *prob = q + g.head_dim;          // kKeyChunk
+    float *part = prob + kKeyChunk;        // kBlock
+    __shared__ float scratch[kBlock / 64];
+
+    const uint32_t query_heads = g.query_heads;
+    const uint64_t token = blockIdx.x / query_heads;
+    const uint32_t head = uint32_t(blockIdx.x - token * query_heads);
+    const uint32_t kv_head = head / g.group;
+    const uint32_t d = g.head_dim;
+    const uint64_t kv_width = uint64_t(g.key_value_heads) * d;
+    const uint64_t visible = g.initial_len + token + 1;
+    const float *qrow = query + (token * query_heads + head) * uint64_t(d);
+    const float *keys = key_cache + uint64_t(kv_head) * d;
+    const float *values = value_cache + uint64_t(kv_head) * d;
+    for (uint32_t c = threadIdx.x; c < d; c += kBlock)
+        q[c] = qrow[c];
+    __syncthreads();
+
+    auto score = [&](uint64_t j) {
+        const float *krow = keys + j * kv_width;
+        float dot = 0.0f;
+        for (uint32_t c = 0; c < d; ++c)
+            dot += q[c] * krow[c];
+        return dot * g.scale;
+    };
+
+    float maximum = -__builtin_inff();
+    for (uint64_t j = threadIdx.x; j < visible; j += kBlock)
+        maximum = fmaxf(maximum, score(j));
+    maximum = block_max(maximum, scratch);
+
+    float denominator = 0.0f;
+    for (uint64_t j = threadIdx.x; j < visible; j += kBlock)
+        denominator += expf(score(j) - maximum);
+    denominator = block_sum(denominator, scratch);
+
+    // Threads split as `groups` key groups of `span` dimensions; a head wider
+    // than the block gives each thread up to kMaxDimsPerThread dimensions.
+    const uint32_t span = d < kBlock ? d : kBlock;
+    const uint32_t groups = kBlock / span;
+    const uint32_t group = threadIdx.x / span;
+    const uint32_t lane_dim = threadIdx.x - group * span;
+    float acc[kMaxDimsPerThread];
+#pragma unroll
+    for (int i = 0; i < kMaxDimsPerThread; ++i)
+        acc[i] = 0.0f;
+    for (uint64_t base = 0; base < visible; base += kKeyChunk) {
+        const uint32_t chunk = uint32_t(visible - base < kKeyChunk ? visible - base : kKeyChunk);
+        __syncthreads();
+        for (uint32_t j = threadIdx.x; j < chunk; j += kBlock)
+            prob[j] = expf(score(base + j) - maximum) / denominator;
+        __syncthreads();
+        if (group < groups) {
+#pragma unroll
+            for (int i = 0; i < kMaxDimsPerThread; ++i) {
+                const uint32_t dim = lane_dim + uint32_t(i) * kBlock;
+                if (dim >= d)
+                    break;
+                float a = acc[i];
+                for (uint32_t j = group; j < chunk; j += groups)
+                    a += prob[j] * values[(base + j) * kv_width + dim];
+                acc[i] = a;
+            }
+        }
+    }
+    float *orow = out + (token * query_heads + head) * uint64_t(d);
+    if (groups == 1) {
+        if (group != 0)
+            return;
+#pragma unroll
+        for (int i = 0; i < kMaxDimsPerThread; ++i) {
+            const uint32_t dim = lane_dim + uint32_t(i) * kBlock;
+            if (dim < d)
+                orow[dim] = acc[i];
+        }
+        return;
+    }
+    __syncthreads();
+    if (group < groups)
+        part[threadIdx.x] = acc[0];
+    __syncthreads();
+    if (threadIdx.x < d) {
+        float total = part[threadIdx.x];
+        for (uint32_t gi = 1; gi < groups; ++gi)
+            total += part[gi * span + threadIdx.x];
+        orow[threadIdx.x] = total;
+    }
+}
+
+// ---- gated short convolution -------------------------------------------
+
+// u = B * V per (token, channel); out = (sum over taps of kernel * u) * C,
+// with taps oldest to current and the first width - 1 reaching into the
+// rolling history; afterwards the history holds the last width - 1 u rows
+// (attention_convolution.rs:220-340).  One thread per channel walks the
+// tokens, so the in-place history update needs no cross-thread ordering.
+__global__ __launch_bounds__(kBlock) void short_conv_kernel(float *__restrict__ out,
+                                                            const float *__restrict__ projection,
+                                                            const float *__restrict__ kernel,
+                                                            float *__restrict__ history,
+                                                            uint64_t tokens, uint32_t hidden,
+                                                            uint32_t width)
+{
+    const uint32_t channel = blockIdx.x * kBlock + threadIdx.x;
+    if (channel >= hidden)
+        return;
+    const uint64_t pw = uint64_t(hidden) * 3;
+    const int64_t history_rows = int64_t(width) - 1;
+    auto u_at = [&](int64_t relative) {
+        if (relative < 0)
+            return history[uint64_t(relative + history_rows) * hidden + channel];
+        const float *p = projection + uint64_t(relative) * pw + channel;
+        return p[0] * p[2 * uint64_t(hidden)];
+    };
+    const float *taps = kernel + uint64_t(channel) * width;
+    for (uint64_t t = 0; t < tokens; ++t) {
+        float total = 0.0f;
+        for (uint32_t tap = 0; tap < width; ++tap)
+            total += taps[tap] * u_at(int64_t(t) + int64_t(tap) - history_rows);
+        out[t * hidden + channel] = total * projection[t * pw + hidden + channel];
+    }
+    if (history_rows <= 0)
+        return;
+    // Row r of the new history is logical position tokens - history_rows + r;
+    // rows read from the old history sit strictly above the row written, so
+    // an increasing walk reads each old value before overwriting it.
+    for (int64_t r = 0; r < history_rows; ++r)
+        history[uint64_t(r) * hidden + channel] = u_at(int64_t(tokens) - history_rows + r);
+}
+
+}  // namespace
+
+// ---- launches ----------------------------------------------------------
+
+void launch_copy(hipStream_t stream, float *dst, const float *src, size_t count)
+{
+    if (count)
+        copy_kernel<<<grid_for((count + 3) / 4), kBlock, 0, stream>>>(dst, src, count);
+}
+
+void launch_rect_copy(hipStream_t stream, float *dst, const float *src, const RectCopy &rect)
+{
+    if (rect.rows && rect.columns)
+        rect_copy_kernel<<<grid_for(rect.rows, 1), kBlock, 0, stream>>>(dst, src, rect);
+}
+
+void launch_gather_rows(hipStream_t stream, float *out, const float *table, const float *ids,
+                        uint32_t count, uint32_t rows, uint64_t columns)
+{
+    if (count && columns)
+        gather_rows_kernel<<<grid_for(count, 1), kBlock, 0, stream>>>(out, table, ids, count,
+                                                                      rows, columns);
+}
+
+void launch_gather_columns(hipStream_t stream, float *out, const float *in, const uint32_t *cols,
+                           uint64_t rows, uint64_t width, uint32_t count)
+{
+    if (rows && count)
+        gather_columns_kernel<<<grid_for(rows * count), kBlock, 0, stream>>>(out, in, cols, rows,
+                                                                             width, count);
+}
+
+void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
+                   const uint64_t *mask)
+{
+    if (rows)
+        argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, in, rows, width,
+                                                                      mask);
+}
+
+void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
+                   size_t count)
+{
+    if (!count)
+        return;
+    if (op == 0)
+        binary_kernel<0><<<grid_for(count), kBlock, 0, stream>>>(out, left, right, count);
+    else
+        binary_kernel<1><<<grid_for(count), kBlock, 0, stream>>>(out, left, right, count);
+}
+
+void launch_linear(hipStream_t stream, float *out, const float *x, const float *w, uint32_t m,
+                   uint32_t n, uint32_t k)
+{
+    if (uint64_t(m) * n)
+        linear_kernel<<<grid_for(uint64_t(m) * n, kBlock / 64), kBlock, 0, stream>>>(out, x, w,
+                                                                                   m, n, k);
+}
+
+void launch_row_rms(hipStream_t stream, float *out, float *sum, const float *left,
+                    const float *right, const float *weight, uint64_t rows, uint32_t width,
+                    float epsilon)
+{
+    if (!rows || !width)
+        return;
+    if (sum)
+        row_rms_kernel<true><<<grid_for(rows, 1), kBlock, 0, stream>>>(out, sum, left, right,
+                                                                       weight, rows, width,
+                                                                       epsilon);
+    else
+        row_rms_kernel<false><<<grid_for(rows, 1), kBlock, 0, stream>>>(out, nullptr, left,
+                                                                        nullptr, weight, rows,
+                                                                        width, epsilon);
+}
+
+void launch_head_rms(hipStream_t stream, float *out, const float *in, const float *weight,
+                     uint64_t segments, uint32_t head_dim, float epsilon)
+{
+    if (segments)
+        head_rms_kernel<<<grid_for(segments, kBlock / 64), kBlock, 0, stream>>>(
+            out, in, weight, segments, head_dim, epsilon);
+}
+
+void launch_rotary(hipStream_t stream, float *out, const float *in, const float *positions,
+                   uint64_t tokens, uint32_t heads, uint32_t head_dim, float theta)
+{
+    const uint64_t total = tokens * heads * (head_dim / 2);
+    if (total)
+        rotary_kernel<<<grid_for(total), kBlock, 0, stream>>>(out, in, positions, tokens, heads,
+                                                               head_dim, theta);
+}
+
+void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, const float *query,
+                         const float *key, const float *query_weight, const float *key_weight,
+                         const float *positions, uint64_t tokens, uint32_t query_heads,
+                         uint32_t key_heads, uint32_t head_dim, float theta, float epsilon)
+{
+    const uint64_t segments = tokens * (query_heads + key_heads);
+    if (segments)
+        qk_norm_rope_kernel<<<grid_for(segments, kBlock / 64), kBlock, 0, stream>>>(
+            query_out, key_out, query, key, query_weight, key_weight, positions, tokens,
+            query_heads, key_heads, head_dim, theta, epsilon);
+}
+
+void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
+                const float *value, float *key_cache, float *value_cache, const GqaShape &g)
+{
+    const uint64_t kv_width = uint64_t(g.key_value_heads) * g.head_dim;
+    const uint64_t appended = g.tokens * kv_width;
+    if (appended)
+        cache_append_kernel<<<grid_for(appended), kBlock, 0, stream>>>(
+            key_cache, value_cache, key, value, g.initial_len * kv_width, appended);
+    const uint64_t blocks = g.tokens * g.query_heads;
+    if (!blocks)
+        return;
+    const size_t lds = (size_t(g.head_dim) + kKeyChunk + kBlock) * sizeof(float);
+    gqa_kernel<<<unsigned(blocks), kBlock, lds, stream>>>(out, query, key_cache, value_cache, g);
+}
+
+void launch_short_conv(hipStream_t stream, float *out, const float *projection,
+                       const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
+                       uint32_t width)
+{
+    short_conv_kernel<<<(hidden + kBlock - 1) / kBlock, kBlock, 0, stream>>>(
+        out, projection, kernel, history, tokens, hidden, width);
+}
+
+}  // namespace mfh

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <initializer_list>
 #include <map>
 #include <memory>
 #include <unordered_set>
@@ -145,6 +146,37 @@ mfh_status check_operation(mfh_ctx *ctx, mfh_operation op);
 
 // Drop derived copies of a buffer whose contents an operation overwrites.
 void mark_written(mfh_buf *buf);
+
+// Make the context's device current for the scope of one call.
+struct DeviceGuard {
+    int previous = 0;
+    explicit DeviceGuard(int device)
+    {
+        (void)hipGetDevice(&previous);
+        if (previous != device)
+            (void)hipSetDevice(device);
+    }
+    ~DeviceGuard() { (void)hipSetDevice(previous); }
+};
+
+inline bool same_shape(const mfh_buf *a, const mfh_buf *b)
+{
+    if (!a || !b || a->rank != b->rank)
+        return false;
+    for (uint32_t i = 0; i < a->rank; ++i)
+        if (a->dims[i] != b->dims[i])
+            return false;
+    return true;
+}
+
+// Whether `out` shares storage with any of `inputs` (null entries skipped).
+inline bool aliases(const mfh_buf *out, std::initializer_list<const mfh_buf *> inputs)
+{
+    for (const mfh_buf *in : inputs)
+        if (in && out->dev && in->dev == out->dev)
+            return true;
+    return false;
+}
 
 // Device scratch owned by the context, grown on demand (stream ordered).
 void *ids_scratch(mfh_ctx *ctx, size_t bytes);

@@ -67,4 +67,62 @@ void launch_packed_gather(hipStream_t stream, Format format, float *out, const u
                           const float *scales, const float *ids, uint32_t count, uint32_t rows,
                           uint32_t k);
 
+// ---- dense f32 operations (dense.hip) ----------------------------------
+
+struct RectCopy {
+    uint64_t source_width, destination_width;
+    uint64_t source_row, source_column, destination_row, destination_column;
+    uint64_t rows, columns;
+};
+
+// Attention over caches of [capacity, key_value_heads * head_dim] rows; the
+// `tokens` new rows land at row `initial_len`.
+struct GqaShape {
+    uint64_t tokens = 0;
+    uint64_t initial_len = 0;
+    uint32_t query_heads = 0;
+    uint32_t key_value_heads = 0;
+    uint32_t head_dim = 0;
+    uint32_t group = 0;
+    float scale = 0.0f;
+};
+// Widest head the attention kernel serves: a 256-thread block gives each
+// thread at most this many output dimensions.
+constexpr int kMaxDimsPerThread = 4;
+constexpr uint32_t kMaxGqaHeadDim = 256 * kMaxDimsPerThread;
+
+void launch_copy(hipStream_t stream, float *dst, const float *src, size_t count);
+void launch_rect_copy(hipStream_t stream, float *dst, const float *src, const RectCopy &rect);
+// `ids` are f32 row selectors; invalid or out-of-range ids give a NaN row.
+void launch_gather_rows(hipStream_t stream, float *out, const float *table, const float *ids,
+                        uint32_t count, uint32_t rows, uint64_t columns);
+void launch_gather_columns(hipStream_t stream, float *out, const float *in, const uint32_t *cols,
+                           uint64_t rows, uint64_t width, uint32_t count);
+// `mask` is null for the unmasked selector.
+void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
+                   const uint64_t *mask);
+// op 0: left + right, op 1: left * right.
+void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
+                   size_t count);
+void launch_linear(hipStream_t stream, float *out, const float *x, const float *w, uint32_t m,
+                   uint32_t n, uint32_t k);
+// With `sum` non-null: sum = left + right, out = rms(sum); else out = rms(left).
+void launch_row_rms(hipStream_t stream, float *out, float *sum, const float *left,
+                    const float *right, const float *weight, uint64_t rows, uint32_t width,
+                    float epsilon);
+void launch_head_rms(hipStream_t stream, float *out, const float *in, const float *weight,
+                     uint64_t segments, uint32_t head_dim, float epsilon);
+// `positions` holds one f32 position per token.
+void launch_rotary(hipStream_t stream, float *out, const float *in, const float *positions,
+                   uint64_t tokens, uint32_t heads, uint32_t head_dim, float theta);
+void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, const float *query,
+                         const float *key, const float *query_weight, const float *key_weight,
+                         const float *positions, uint64_t tokens, uint32_t query_heads,
+                         uint32_t key_heads, uint32_t head_dim, float theta, float epsilon);
+void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
+                const float *value, float *key_cache, float *value_cache, const GqaShape &g);
+void launch_short_conv(hipStream_t stream, float *out, const float *projection,
+                       const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
+                       uint32_t width);
+
 }  // namespace mfh

@@ -11,32 +11,11 @@
 namespace mfh {
 namespace {
 
-struct DeviceGuard {
-    int previous = 0;
-    explicit DeviceGuard(int device)
-    {
-        (void)hipGetDevice(&previous);
-        if (previous != device)
-            (void)hipSetDevice(device);
-    }
-    ~DeviceGuard() { hipSetDevice(previous); }
-};
-
 struct Packed {
     uint32_t rows = 0;
     uint32_t inner = 0;
     Format format = Format::Ternary;
 };
-
-bool same_shape(const mfh_buf *a, const mfh_buf *b)
-{
-    if (!a || !b || a->rank != b->rank)
-        return false;
-    for (uint32_t i = 0; i < a->rank; ++i)
-        if (a->dims[i] != b->dims[i])
-            return false;
-    return true;
-}
 
 // check_packed_operands, backend-cpu/src/packed.rs:177-220.
 mfh_status check_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales, Packed *out)
@@ -72,14 +51,6 @@ mfh_status check_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scale
     out->rows = uint32_t(codes->dims[0]);
     out->inner = uint32_t(inner);
     return MFH_OK;
-}
-
-bool aliases(const mfh_buf *out, std::initializer_list<const mfh_buf *> inputs)
-{
-    for (const mfh_buf *in : inputs)
-        if (in && out->dev && in->dev == out->dev)
-            return true;
-    return false;
 }
 
 PackedStream stream_of(const mfh_buf *codes, const mfh_buf *scales)

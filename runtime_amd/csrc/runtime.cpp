@@ -201,17 +201,6 @@ const uint64_t kOperations = (1ull << MFH_OP_COPY) | (1ull << MFH_OP_RECT_COPY_2
                              (1ull << MFH_OP_PACKED_SWIGLU_PAIR) | (1ull << MFH_OP_QK_NORM_ROPE) |
                              (1ull << MFH_OP_ARGMAX) | (1ull << MFH_OP_GATHER_COLUMNS);
 
-struct DeviceGuard {
-    int previous = 0;
-    explicit DeviceGuard(int device)
-    {
-        (void)hipGetDevice(&previous);
-        if (previous != device)
-            (void)hipSetDevice(device);
-    }
-    ~DeviceGuard() { hipSetDevice(previous); }
-};
-
 // Shape admission shared by the allocation entry points: rank <= 4, element
 // count and byte size without overflow, capability and limit checks
 // (storage.rs:381-420, backend.rs:397-431, resources.rs:27-43).
