@@ -7,16 +7,18 @@ the sweep -- {ternary, nf4, int8} x {1024x1024, 4608x1024, 2048x2048,
 matrices quantized by the backend's converter (group-128, FP16-exact scales);
 activations are seeded N(0, 1).  Everything is resident in HBM before timing.
 
-Each step is captured once as a HIP graph per weight-copy set and replayed;
-consecutive uses of one matrix rotate over copies so that every launch streams
-its weights from HBM rather than the 256 MB Infinity Cache.
+Launches are eager (the host enqueues ahead of the device); consecutive uses
+of one matrix rotate over weight copies so that the large matrices stream
+from HBM rather than the 256 MB Infinity Cache.
 
-`value` = algorithmic bytes of all launches / wall time of the K timed steps,
-where a launch's bytes are N*K*b/8 + (N*K/128)*2 + B*K*4 + B*N*4 (codes at
-b = 2/4/8 bits, scales at their stored FP16 width, activations, outputs).
-The roofline object is for the dominant kernel (the 65536x2048 INT8 head at
-B=1): its bytes over its average launch time from HIP events recorded
-around it inside the timed graphs, against the 8 TB/s HBM peak.
+`value` = algorithmic bytes of all launches / device time of the K timed
+steps (HIP events on the backend's stream), where a launch's bytes are
+N*K*b/8 + (N*K/128)*2 + B*K*4 + B*N*4 (codes at b = 2/4/8 bits, scales at
+their stored FP16 width, activations, outputs).  The roofline object is for
+the dominant operation (the 65536x2048 INT8 head at B=1, an activation
+prologue kernel plus the GEMV kernel): its bytes over its average duration
+across back-to-back launches on rotating copies, against the 8 TB/s HBM
+peak.
 """
 from __future__ import annotations
 
@@ -34,6 +36,10 @@ SHAPES = [(1024, 1024), (4608, 1024), (2048, 2048), (8192, 2048), (2048, 8192), 
 BATCHES = [1, 2, 4, 8]
 HBM_PEAK_GBS = 8000.0
 DOMINANT = ("int8", (65536, 2048), 1)
+# HBM bytes per dominant launch (prologue + GEMV) from rocprofv3 FETCH_SIZE
+# and WRITE_SIZE runs of `--profile dominant`, scaled by the same counters
+# over `--profile copy` (profiles/int8_gemv_65536x2048_b1.md).
+DOMINANT_TRAFFIC_BYTES = 137_163_747
 
 
 def algorithmic_bytes(n: int, k: int, b: int, fmt: str) -> int:
@@ -51,18 +57,60 @@ def cpu_baseline(weights, xs) -> dict:
     import oracle
 
     total_bytes = 0
+    sweeps = 0
     start = time.perf_counter()
-    for fmt in FORMATS:
-        for (n, k) in SHAPES:
-            codes, scales = weights[(fmt, n, k)]
-            for b in BATCHES:
-                oracle.packed_linear(xs[(b, k)], codes, scales)
-                total_bytes += algorithmic_bytes(n, k, b, fmt)
+    while sweeps == 0 or time.perf_counter() - start < 10.0:
+        for fmt in FORMATS:
+            for (n, k) in SHAPES:
+                codes, scales = weights[(fmt, n, k)]
+                for b in BATCHES:
+                    oracle.packed_linear(xs[(b, k)], codes, scales)
+                    total_bytes += algorithmic_bytes(n, k, b, fmt)
+        sweeps += 1
     seconds = time.perf_counter() - start
     return {"value": round(total_bytes / seconds / 1e9, 3), "unit": "GB/s", "cores": 1,
             "kind": "port",
-            "sample": "oracle packed_linear over one full sweep step (72 launches, "
+            "sample": f"oracle packed_linear over {sweeps} full sweep steps (72 launches each, "
                       f"{total_bytes / 1e6:.0f} MB algorithmic, {seconds:.1f} s)"}
+
+
+def profile_only(backend, args) -> int:
+    """Launch sequences for rocprofv3: `dominant` builds the 65536x2048 INT8
+    head (same seed as the sweep) on `copies` buffers and launches it
+    8 * copies times after one untimed pass; `copy` moves 256 MiB with
+    mfh_copy four times, the known-size reference for FETCH_SIZE and
+    WRITE_SIZE."""
+    from runtime_amd import convert
+    from runtime_amd.backend import WEIGHT
+
+    if args.profile == "copy":
+        count = 64 << 20
+        src = backend.allocate_f32((count,))
+        dst = backend.allocate_f32((count,))
+        for _ in range(4):
+            backend.copy(dst, src)
+        backend.synchronize()
+        log(f"copied {count * 4} bytes x 4")
+        return 0
+    fmt, (n, k), b = DOMINANT
+    dense = convert.normal((n, k), 0x5EED0001 + SHAPES.index((n, k)), sigma=0.02)
+    codes, scales16 = convert.quantize(dense, fmt)
+    scales = convert.f16_to_f32(scales16)
+    del dense
+    copies = [(backend.upload_u8_classified(codes.shape, codes, WEIGHT),
+               backend.upload_f32_classified(scales.shape, scales, WEIGHT))
+              for _ in range(args.copies)]
+    x = backend.upload_f32((b, k), convert.normal((b, k), 0xAC70001 + b))
+    out = backend.allocate_f32((b, n))
+    for c, s in copies:
+        backend.packed_linear(out, x, c, s)
+    backend.synchronize()
+    for r in range(8 * args.copies):
+        c, s = copies[r % args.copies]
+        backend.packed_linear(out, x, c, s)
+    backend.synchronize()
+    log(f"{fmt} {n}x{k} B={b}: {8 * args.copies} launches after one pass per copy")
+    return 0
 
 
 def main() -> int:
@@ -72,6 +120,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile", choices=["dominant", "copy"],
+                    help="run only the dominant operation (or a 256 MiB device copy, the "
+                         "counter calibration) for rocprofv3, and print no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the packed GEMV path is single-device "
@@ -83,6 +134,8 @@ def main() -> int:
 
     backend = HipBackend(0)
     stream = backend.stream()
+    if args.profile:
+        return profile_only(backend, args)
 
     log("generating and quantizing weights")
     weights = {}
@@ -118,45 +171,45 @@ def main() -> int:
         for i in range(first, last):
             launch(i, copy_set)
 
-    # Eager pass: builds any per-buffer derived layouts before capture.
+    # Eager pass: builds every per-buffer derived layout (repacked tiles,
+    # tiled scales) before anything is timed.
     for cs in range(args.copies):
         enqueue(0, len(launches), cs)
     backend.synchronize()
 
-    # Each step is three graphs -- the launches before the dominant kernel,
-    # the dominant kernel, the launches after it -- so HIP events recorded
-    # between graph launches bracket the dominant kernel exactly while the
-    # queue stays busy.
-    log("capturing graphs")
-    di = launches.index(DOMINANT)
-    graphs = []
-    for cs in range(args.copies):
-        graphs.append((hiptime.Graph(stream, lambda cs=cs: enqueue(0, di, cs)),
-                       hiptime.Graph(stream, lambda cs=cs: enqueue(di, di + 1, cs)),
-                       hiptime.Graph(stream, lambda cs=cs: enqueue(di + 1, len(launches), cs))))
-
+    # Launches are eager: the host enqueues ahead of the device, so the
+    # stream stays busy and the timed region is device time.
     for w in range(args.warmup):
-        for g in graphs[w % len(graphs)]:
-            g.launch(stream)
+        enqueue(0, len(launches), w % args.copies)
     backend.synchronize()
 
     log(f"timing {args.steps} steps")
-    dom_events = [(hiptime.Event(), hiptime.Event()) for _ in range(args.steps)]
     start, stop = hiptime.Event(), hiptime.Event()
     start.record(stream)
     t0 = time.perf_counter()
     for step in range(args.steps):
-        pre, dom, post = graphs[step % len(graphs)]
-        pre.launch(stream)
-        dom_events[step][0].record(stream)
-        dom.launch(stream)
-        dom_events[step][1].record(stream)
-        post.launch(stream)
+        enqueue(0, len(launches), step % args.copies)
     stop.record(stream)
     stop.synchronize()
     wall_s = time.perf_counter() - t0
     total_ms = stop.elapsed_ms(start)
-    dom_ms = float(np.mean([e1.elapsed_ms(e0) for e0, e1 in dom_events]))
+
+    # Dominant operation: back-to-back launches over rotating weight copies
+    # (each launch streams its matrix from HBM), bracketed by one event pair
+    # on the backend's stream.  One launch is the activation prologue kernel
+    # plus the GEMV kernel.
+    di = launches.index(DOMINANT)
+    dom_reps = 8 * args.copies
+    for r in range(args.copies):
+        launch(di, r)
+    backend.synchronize()
+    d0, d1 = hiptime.Event(), hiptime.Event()
+    d0.record(stream)
+    for r in range(dom_reps):
+        launch(di, r)
+    d1.record(stream)
+    d1.synchronize()
+    dom_ms = d1.elapsed_ms(d0) / dom_reps
 
     ms_per_step = total_ms / args.steps
     value_gbs = step_bytes * args.steps / (total_ms / 1e3) / 1e9
@@ -164,26 +217,20 @@ def main() -> int:
     dom_bytes = algorithmic_bytes(n, k, b, fmt)
     achieved = dom_bytes / (dom_ms / 1e3) / 1e9
 
-    # Per-launch table (outside the timed region): each launch runs right
-    # after a spacer launch of the 65536x2048 INT8 head on another copy, which
-    # keeps the queue busy while the host records the bracketing events and
-    # streams 137 MB through the Infinity Cache.
+    # Per-launch table (outside the timed region): each operation launched
+    # back to back over the rotating copies between one event pair.  Matrices
+    # far smaller than the 256 MB Infinity Cache stay resident in it here.
     log("per-launch table")
-    repeats = 5
-    table = np.zeros((repeats, len(launches)))
-    pairs = [[(hiptime.Event(), hiptime.Event()) for _ in launches] for _ in range(repeats)]
-    for r in range(repeats):
-        for i in range(len(launches)):
-            launch(di, r + 1)
-            pairs[r][i][0].record(stream)
-            launch(i, r)
-            pairs[r][i][1].record(stream)
-    backend.synchronize()
-    for r in range(repeats):
-        table[r] = [e1.elapsed_ms(e0) for e0, e1 in pairs[r]]
+    repeats = 4 * args.copies
     detail = {}
     for i, (fmt_i, (n_i, k_i), b_i) in enumerate(launches):
-        us = float(np.median(table[:, i])) * 1e3
+        e0, e1 = hiptime.Event(), hiptime.Event()
+        e0.record(stream)
+        for r in range(repeats):
+            launch(i, r)
+        e1.record(stream)
+        e1.synchronize()
+        us = e1.elapsed_ms(e0) / repeats * 1e3
         detail[f"{fmt_i}:{n_i}x{k_i}:B{b_i}"] = {
             "us": round(us, 2),
             "GBs": round(algorithmic_bytes(n_i, k_i, b_i, fmt_i) / (us / 1e6) / 1e9, 1)}
@@ -216,7 +263,8 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": DOMINANT_TRAFFIC_BYTES,
+            "algorithmic_bytes": dom_bytes,
             "avg_launch_us": round(dom_ms * 1e3, 3),
         },
         "detail": detail,
