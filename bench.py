@@ -125,8 +125,9 @@ def main() -> int:
                          "counter calibration) for rocprofv3, and print no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: the packed GEMV path is single-device "
-              "(sharding is described in DESIGN.md); run it with --gpus 1", file=sys.stderr)
+        print("bench.py measures one GPU only: this build runs the packed GEMV path on a "
+              "single device (multi-GPU row sharding is a design note, not built); "
+              "run it with --gpus 1", file=sys.stderr)
         return 2
 
     from runtime_amd import convert, hiptime

@@ -4,10 +4,10 @@
  *
  * The ABI mirrors the `InferenceOps` trait of the reference
  * (crates/engine-api/src/inference.rs:33-425) one entry point per trait
- * method, with the same operand order.  A Rust `crates/backend-hip` would bind
- * these symbols one-to-one (see INTEGRATION.md for the binding).  Every entry
- * point takes plain pointers, sizes and opaque handles; no C++ or torch types
- * cross the boundary.
+ * method, with the same operand order.  A Rust `crates/backend-hip` binds
+ * these symbols one-to-one from an `extern "C"` block.  Every entry point
+ * takes plain pointers, sizes and opaque handles; no C++ or torch types cross
+ * the boundary.
  *
  * Threading: one context is single-threaded and cooperative, like the
  * reference's `Rc`/`RefCell` backends (engine-api/src/resources.rs:90-99).
