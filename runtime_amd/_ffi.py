@@ -43,6 +43,17 @@ class Report(ctypes.Structure):
                 ("pending_operations", ctypes.c_uint32)]
 
 
+class MflConfig(ctypes.Structure):
+    """mfl_config (include/minifield_lfm2.h)."""
+    _fields_ = [("hidden", ctypes.c_uint32), ("intermediate", ctypes.c_uint32),
+                ("attention_heads", ctypes.c_uint32), ("key_value_heads", ctypes.c_uint32),
+                ("head_dim", ctypes.c_uint32), ("conv_width", ctypes.c_uint32),
+                ("vocab", ctypes.c_uint32), ("layer_count", ctypes.c_uint32),
+                ("layer_kinds", ctypes.POINTER(ctypes.c_uint8)), ("rope_theta", ctypes.c_float),
+                ("norm_epsilon", ctypes.c_float), ("block_norm_epsilon", ctypes.c_float),
+                ("max_tokens", ctypes.c_uint64)]
+
+
 P = ctypes.c_void_p
 PP = ctypes.POINTER(ctypes.c_void_p)
 S = ctypes.c_int  # mfh_status
@@ -109,6 +120,17 @@ SIGNATURES = {
                            ctypes.c_uint32]),
     "mfh_gated_short_convolution": (S, [P, P, P, P, P, ctypes.c_uint32, ctypes.c_uint32]),
     "mfh_swiglu": (S, [P, P, P, P]),
+    # LFM2 token pass (minifield_lfm2.h)
+    "mfl_create": (S, [P, ctypes.POINTER(MflConfig), PP]),
+    "mfl_destroy": (None, [P]),
+    "mfl_set_weight": (S, [P, ctypes.c_uint32, ctypes.c_uint32, P, P]),
+    "mfl_reset": (S, [P]),
+    "mfl_length": (ctypes.c_uint64, [P]),
+    "mfl_append": (S, [P, c_u32_p, SZ, P, ctypes.c_int]),
+    "mfl_sample": (S, [P]),
+    "mfl_generate": (S, [P, ctypes.c_uint32, P]),
+    "mfl_logits": (P, [P]),
+    "mfl_sampled": (P, [P]),
     # diagnostics
     "mfh_stream": (P, [P]),
     "mfh_set_kernel_path": (ctypes.c_int, [P, ctypes.c_int]),

@@ -350,12 +350,20 @@ __device__ __forceinline__ Rotation rotation(float position, uint32_t column, ui
     return {float(cos(double(angle))), float(sin(double(angle)))};
 }
 
+// Token t's position as the reference's `position as f32`: a staged f32
+// array, or base + t converted here (u64 -> f32 rounds to nearest, as on the
+// host).
+__device__ __forceinline__ float position_of(const Positions &p, uint64_t token)
+{
+    return p.staged ? p.staged[token] : float(p.base + token);
+}
+
 // One thread per (token, head, column < half).
 __global__ __launch_bounds__(kBlock) void rotary_kernel(float *__restrict__ out,
                                                         const float *__restrict__ in,
-                                                        const float *__restrict__ positions,
-                                                        uint64_t tokens, uint32_t heads,
-                                                        uint32_t head_dim, float theta)
+                                                        Positions positions, uint64_t tokens,
+                                                        uint32_t heads, uint32_t head_dim,
+                                                        float theta)
 {
     const uint32_t half = head_dim / 2;
     const uint64_t total = tokens * heads * half;
@@ -364,7 +372,7 @@ __global__ __launch_bounds__(kBlock) void rotary_kernel(float *__restrict__ out,
         const uint64_t segment = i / half;
         const uint32_t column = uint32_t(i - segment * half);
         const uint64_t token = segment / heads;
-        const Rotation rot = rotation(positions[token], column, head_dim, theta);
+        const Rotation rot = rotation(position_of(positions, token), column, head_dim, theta);
         const uint64_t base = segment * head_dim;
         const float first = in[base + column];
         const float second = in[base + half + column];
@@ -379,7 +387,7 @@ __global__ __launch_bounds__(kBlock) void rotary_kernel(float *__restrict__ out,
 __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(
     float *__restrict__ query_out, float *__restrict__ key_out, const float *__restrict__ query,
     const float *__restrict__ key, const float *__restrict__ query_weight,
-    const float *__restrict__ key_weight, const float *__restrict__ positions, uint64_t tokens,
+    const float *__restrict__ key_weight, Positions positions, uint64_t tokens,
     uint32_t query_heads, uint32_t key_heads, uint32_t head_dim, float theta, float epsilon)
 {
     const int lane = threadIdx.x & 63;
@@ -406,7 +414,7 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(
         }
         squares = wave_sum(squares);
         const float reciprocal = 1.0f / sqrtf(squares / dim_f + epsilon);
-        const float position = positions[token];
+        const float position = position_of(positions, token);
         for (uint32_t c = lane; c < half; c += 64) {
             const float first = (in[c] * reciprocal) * weight[c];
             const float second = (in[half + c] * reciprocal) * weight[half + c];
@@ -662,7 +670,7 @@ void launch_head_rms(hipStream_t stream, float *out, const float *in, const floa
             out, in, weight, segments, head_dim, epsilon);
 }
 
-void launch_rotary(hipStream_t stream, float *out, const float *in, const float *positions,
+void launch_rotary(hipStream_t stream, float *out, const float *in, const Positions &positions,
                    uint64_t tokens, uint32_t heads, uint32_t head_dim, float theta)
 {
     const uint64_t total = tokens * heads * (head_dim / 2);
@@ -673,7 +681,7 @@ void launch_rotary(hipStream_t stream, float *out, const float *in, const float 
 
 void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, const float *query,
                          const float *key, const float *query_weight, const float *key_weight,
-                         const float *positions, uint64_t tokens, uint32_t query_heads,
+                         const Positions &positions, uint64_t tokens, uint32_t query_heads,
                          uint32_t key_heads, uint32_t head_dim, float theta, float epsilon)
 {
     const uint64_t segments = tokens * (query_heads + key_heads);

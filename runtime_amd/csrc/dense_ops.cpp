@@ -91,15 +91,27 @@ mfh_status check_epsilon(mfh_ctx *ctx, float epsilon)
     return MFH_OK;
 }
 
-// Positions as the reference converts them (`position as f32`, round to
-// nearest), staged for the kernels.
-const float *stage_positions(mfh_ctx *ctx, const uint64_t *positions, size_t count,
-                             mfh_status *status)
+// Positions for the rotary kernels.  Consecutive positions (every decode and
+// prefill pass of the executor) travel as their base in the kernel
+// arguments; anything else is staged as f32 values converted like the
+// reference's `position as f32` (round to nearest).
+Positions stage_positions(mfh_ctx *ctx, const uint64_t *positions, size_t count,
+                          mfh_status *status)
 {
+    Positions p;
+    *status = MFH_OK;
+    bool consecutive = count > 0 && positions[0] <= UINT64_MAX - count;
+    for (size_t i = 1; consecutive && i < count; ++i)
+        consecutive = positions[i] == positions[0] + i;
+    if (consecutive) {
+        p.base = positions[0];
+        return p;
+    }
     std::vector<float> staged(count);
     for (size_t i = 0; i < count; ++i)
         staged[i] = float(positions[i]);
-    return static_cast<const float *>(stage(ctx, staged.data(), count * sizeof(float), status));
+    p.staged = static_cast<const float *>(stage(ctx, staged.data(), count * sizeof(float), status));
+    return p;
 }
 
 // Element-wise add/multiply admission (dense.rs:166-182).
@@ -520,7 +532,7 @@ mfh_status mfh_split_half_rotary(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *i
     mark_written(output);
     if (tokens == 0)
         return MFH_OK;
-    const float *pos = stage_positions(ctx, positions, position_count, &s);
+    const Positions pos = stage_positions(ctx, positions, position_count, &s);
     if (s)
         return s;
     launch_rotary(ctx->stream, dev_f32(output), dev_f32(input), pos, tokens, heads, head_dim,
@@ -618,7 +630,7 @@ mfh_status mfh_qk_norm_rope(mfh_ctx *ctx, mfh_buf *query_out, mfh_buf *key_out,
     mark_written(key_out);
     if (query_tokens == 0)
         return MFH_OK;
-    const float *pos = stage_positions(ctx, positions, position_count, &s);
+    const Positions pos = stage_positions(ctx, positions, position_count, &s);
     if (s)
         return s;
     launch_qk_norm_rope(ctx->stream, dev_f32(query_out), dev_f32(key_out), dev_f32(query),

@@ -112,12 +112,17 @@ void launch_row_rms(hipStream_t stream, float *out, float *sum, const float *lef
                     float epsilon);
 void launch_head_rms(hipStream_t stream, float *out, const float *in, const float *weight,
                      uint64_t segments, uint32_t head_dim, float epsilon);
-// `positions` holds one f32 position per token.
-void launch_rotary(hipStream_t stream, float *out, const float *in, const float *positions,
+// Per-token rotary positions: `staged` (one f32 per token, device memory) or,
+// when null, the consecutive positions base, base + 1, ...
+struct Positions {
+    const float *staged = nullptr;
+    uint64_t base = 0;
+};
+void launch_rotary(hipStream_t stream, float *out, const float *in, const Positions &positions,
                    uint64_t tokens, uint32_t heads, uint32_t head_dim, float theta);
 void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, const float *query,
                          const float *key, const float *query_weight, const float *key_weight,
-                         const float *positions, uint64_t tokens, uint32_t query_heads,
+                         const Positions &positions, uint64_t tokens, uint32_t query_heads,
                          uint32_t key_heads, uint32_t head_dim, float theta, float epsilon);
 void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
                 const float *value, float *key_cache, float *value_cache, const GqaShape &g);

@@ -1,0 +1,484 @@
+// LFM2 token pass over the backend's own C ABI: a restatement of the
+// reference executor's `append_tokens` / `sample_epilogue`
+// (crates/executor-core/src/lfm2/executor/execution.rs:35-585).
+//
+// Every operation is issued through the same mfh_* entry points an external
+// caller uses, in the reference's order and with its role routing.  What this
+// file adds is buffer management suited to a device: every intermediate of a
+// pass lives in a per-row-count workspace allocated once, so steady-state
+// decode allocates nothing and never waits on the host.
+#include <map>
+#include <memory>
+#include <vector>
+
+#include "../../include/minifield_lfm2.h"
+#include "internal.hpp"
+#include "kernels.hpp"
+
+namespace mfh {
+namespace {
+
+struct Weight {
+    const mfh_buf *tensor = nullptr;
+    const mfh_buf *scales = nullptr;  // null: dense f32
+    bool packed() const { return scales != nullptr; }
+};
+
+struct LayerWeights {
+    Weight operator_norm, ffn_norm;
+    Weight conv_kernel, conv_in, conv_out;
+    Weight query_norm, key_norm, query, key, value, output;
+    Weight w1, w2, w3;
+};
+
+// Owned buffer handle.
+struct Owned {
+    mfh_buf *buf = nullptr;
+    Owned() = default;
+    Owned(const Owned &) = delete;
+    Owned &operator=(const Owned &) = delete;
+    ~Owned()
+    {
+        if (buf)
+            mfh_release(buf);
+    }
+};
+
+mfh_status alloc(mfh_ctx *ctx, Owned &o, uint64_t rows, uint64_t cols, mfh_alloc_class cls,
+                 bool zeroed)
+{
+    const uint64_t dims[2] = {rows, cols};
+    return mfh_alloc_f32(ctx, dims, 2, cls, zeroed ? 1 : 0, &o.buf);
+}
+
+// Every intermediate of one pass over `rows` tokens (execution.rs allocates
+// these per call as Scratch).  x/u ping-pong between layers.
+struct Workspace {
+    uint64_t rows = 0;
+    Owned x[2], u[2], op, projection, convolved;
+    Owned q, k, v, q_rope, k_rope, attention;
+    Owned residual, ffn_input, gate, up, hidden, down;
+};
+
+struct LayerState {
+    Owned history;           // conv: [conv_width - 1, hidden]
+    Owned key, value;        // attention: [max_tokens, kv_width]
+    uint64_t length = 0;
+};
+
+}  // namespace
+}  // namespace mfh
+
+using namespace mfh;
+
+struct mfl_model {
+    mfh_ctx *ctx = nullptr;
+    mfl_config config{};
+    std::vector<uint8_t> kinds;
+    uint64_t kv_width = 0;
+    Weight embedding, embedding_norm;
+    std::vector<LayerWeights> layers;
+    std::vector<LayerState> state;
+    uint64_t length = 0;
+    std::map<uint64_t, std::unique_ptr<Workspace>> workspaces;
+    Owned logits, sampled;
+};
+
+namespace mfh {
+namespace {
+
+mfh_status workspace(mfl_model *m, uint64_t rows, Workspace **out)
+{
+    auto it = m->workspaces.find(rows);
+    if (it != m->workspaces.end()) {
+        *out = it->second.get();
+        return MFH_OK;
+    }
+    auto ws = std::make_unique<Workspace>();
+    ws->rows = rows;
+    mfh_ctx *c = m->ctx;
+    const uint64_t h = m->config.hidden, inter = m->config.intermediate, kv = m->kv_width;
+    const mfh_alloc_class S = MFH_CLASS_SCRATCH;
+    mfh_status s = MFH_OK;
+    for (int i = 0; i < 2 && !s; ++i) {
+        s = alloc(c, ws->x[i], rows, h, S, false);
+        if (!s)
+            s = alloc(c, ws->u[i], rows, h, S, false);
+    }
+    const struct {
+        Owned *o;
+        uint64_t cols;
+    } plan[] = {{&ws->op, h},          {&ws->projection, 3 * h}, {&ws->convolved, h},
+                {&ws->q, h},           {&ws->k, kv},             {&ws->v, kv},
+                {&ws->q_rope, h},      {&ws->k_rope, kv},        {&ws->attention, h},
+                {&ws->residual, h},    {&ws->ffn_input, h},      {&ws->gate, inter},
+                {&ws->up, inter},      {&ws->hidden, inter},     {&ws->down, h}};
+    for (const auto &p : plan)
+        if (!s)
+            s = alloc(c, *p.o, rows, p.cols, S, false);
+    if (s)
+        return s;
+    *out = ws.get();
+    m->workspaces.emplace(rows, std::move(ws));
+    return MFH_OK;
+}
+
+// weight_linear (execution.rs:12-25).
+mfh_status weight_linear(mfh_ctx *c, mfh_buf *out, const mfh_buf *in, const Weight &w)
+{
+    if (!w.tensor)
+        return fail(c, MFH_MISSING_REQUIRED_TENSOR, "LFM2 weight role is not attached");
+    if (w.packed())
+        return mfh_packed_linear(c, out, in, w.tensor, w.scales);
+    return mfh_linear(c, out, in, w.tensor);
+}
+
+// The pair/fused conditions compare the stored quantization of two roles
+// (role_quant, weights.rs:588): packed streams of one shape share a format
+// exactly when their code widths agree.
+bool same_packed_format(const Weight &a, const Weight &b)
+{
+    return a.packed() && b.packed() && a.tensor->dims[1] == b.tensor->dims[1] &&
+           a.scales->dims[1] == b.scales->dims[1];
+}
+
+mfh_status need(mfh_ctx *c, const Weight &w)
+{
+    return w.tensor ? MFH_OK
+                    : fail(c, MFH_MISSING_REQUIRED_TENSOR, "LFM2 weight role is not attached");
+}
+
+// The FFN of one layer on `ffn_rows` rows (execution.rs:289-497).
+mfh_status ffn(mfl_model *m, const LayerWeights &lw, Workspace &ws, mfh_buf *ffn_input,
+               mfh_buf *down)
+{
+    mfh_ctx *c = m->ctx;
+    mfh_status s;
+    const uint64_t ffn_rows = ws.rows;
+    const bool pair = same_packed_format(lw.w1, lw.w3);
+    if (ffn_rows >= 96 && pair && lw.w2.packed()) {
+        // Fused prefill: SwiGLU in the gate/up epilogue, then the down GEMM.
+        if ((s = mfh_packed_swiglu_pair(c, ws.hidden.buf, ffn_input, lw.w1.tensor, lw.w1.scales,
+                                        lw.w3.tensor, lw.w3.scales)))
+            return s;
+        return mfh_packed_linear(c, down, ws.hidden.buf, lw.w2.tensor, lw.w2.scales);
+    }
+    if (pair) {
+        s = mfh_packed_linear_pair(c, ws.gate.buf, ws.up.buf, ffn_input, lw.w1.tensor,
+                                   lw.w1.scales, lw.w3.tensor, lw.w3.scales);
+    } else {
+        s = weight_linear(c, ws.gate.buf, ffn_input, lw.w1);
+        if (!s)
+            s = weight_linear(c, ws.up.buf, ffn_input, lw.w3);
+    }
+    if (s)
+        return s;
+    if ((s = need(c, lw.w2)))
+        return s;
+    if (lw.w2.packed())
+        return mfh_packed_swiglu_linear(c, down, ws.gate.buf, ws.up.buf, lw.w2.tensor,
+                                        lw.w2.scales);
+    if ((s = mfh_swiglu(c, ws.hidden.buf, ws.gate.buf, ws.up.buf)))
+        return s;
+    return weight_linear(c, down, ws.hidden.buf, lw.w2);
+}
+
+// append_tokens (execution.rs:35-540).
+mfh_status append(mfl_model *m, const uint32_t *tokens, size_t count, const mfh_buf *device_ids,
+                  bool produce_logits)
+{
+    mfh_ctx *c = m->ctx;
+    const mfl_config &cfg = m->config;
+    uint64_t rows = count;
+    if (device_ids) {
+        mfh_status s = check_f32(c, device_ids);
+        if (s)
+            return s;
+        if (device_ids->rank != 1)
+            return fail(c, MFH_INVALID_SHAPE, "device token-id buffer must be rank one");
+        rows = device_ids->dims[0];
+    }
+    if (rows == 0)
+        return fail(c, MFH_INVALID_ARGUMENT, "token pass requires at least one token");
+    for (size_t i = 0; !device_ids && i < count; ++i)
+        if (tokens[i] >= cfg.vocab)
+            return fail(c, MFH_OUT_OF_BOUNDS, "valid token ID exceeds loaded model vocabulary");
+    if (m->length > UINT64_MAX - rows)
+        return fail(c, MFH_OVERFLOW, "prefix logical length overflows u64");
+    if (m->length + rows > cfg.max_tokens)
+        return fail(c, MFH_OUT_OF_BOUNDS, "append exceeds configured logical prefix capacity");
+    if (!m->embedding.tensor || !m->embedding_norm.tensor)
+        return fail(c, MFH_MISSING_REQUIRED_TENSOR, "LFM2 weight role is not attached");
+
+    Workspace *ws = nullptr, *ws1 = nullptr;
+    mfh_status s = workspace(m, rows, &ws);
+    if (!s)
+        s = workspace(m, 1, &ws1);
+    if (s)
+        return s;
+    std::vector<uint64_t> positions(rows);
+    for (uint64_t i = 0; i < rows; ++i)
+        positions[i] = m->length + i;
+
+    // Embedding gather, then the first layer's operator norm.
+    int p = 0;
+    mfh_buf *x = ws->x[p].buf, *u = ws->u[p].buf;
+    if (m->embedding.packed())
+        s = mfh_packed_gather_rows(c, x, m->embedding.tensor, m->embedding.scales, tokens,
+                                   device_ids ? 0 : count, device_ids);
+    else
+        s = mfh_gather_rows(c, x, m->embedding.tensor, tokens, device_ids ? 0 : count,
+                            device_ids);
+    if (s)
+        return s;
+    if ((s = need(c, m->layers[0].operator_norm)) ||
+        (s = mfh_row_rms_norm(c, u, x, m->layers[0].operator_norm.tensor, cfg.block_norm_epsilon)))
+        return s;
+
+    const uint32_t L = cfg.layer_count;
+    for (uint32_t index = 0; index < L; ++index) {
+        const LayerWeights &lw = m->layers[index];
+        LayerState &st = m->state[index];
+        if (m->kinds[index] == 0) {
+            if ((s = weight_linear(c, ws->projection.buf, u, lw.conv_in)) || (s = need(c, lw.conv_kernel)) ||
+                (s = mfh_gated_short_convolution(c, ws->convolved.buf, ws->projection.buf,
+                                                 lw.conv_kernel.tensor, st.history.buf,
+                                                 cfg.hidden, cfg.conv_width)) ||
+                (s = weight_linear(c, ws->op.buf, ws->convolved.buf, lw.conv_out)))
+                return s;
+        } else {
+            if ((s = weight_linear(c, ws->q.buf, u, lw.query)))
+                return s;
+            if (same_packed_format(lw.key, lw.value))
+                s = mfh_packed_linear_pair(c, ws->k.buf, ws->v.buf, u, lw.key.tensor,
+                                           lw.key.scales, lw.value.tensor, lw.value.scales);
+            else if (!(s = weight_linear(c, ws->k.buf, u, lw.key)))
+                s = weight_linear(c, ws->v.buf, u, lw.value);
+            if (s)
+                return s;
+            if ((s = need(c, lw.query_norm)) || (s = need(c, lw.key_norm)) ||
+                (s = mfh_qk_norm_rope(c, ws->q_rope.buf, ws->k_rope.buf, ws->q.buf, ws->k.buf,
+                                      lw.query_norm.tensor, lw.key_norm.tensor, positions.data(),
+                                      rows, cfg.attention_heads, cfg.head_dim, cfg.rope_theta,
+                                      cfg.key_value_heads, cfg.head_dim, cfg.block_norm_epsilon)) ||
+                (s = mfh_causal_gqa(c, ws->attention.buf, ws->q_rope.buf, ws->k_rope.buf,
+                                    ws->v.buf, st.key.buf, st.value.buf, &st.length,
+                                    cfg.attention_heads, cfg.key_value_heads, cfg.head_dim)) ||
+                (s = weight_linear(c, ws->op.buf, ws->attention.buf, lw.output)))
+                return s;
+        }
+        if ((s = need(c, lw.ffn_norm)) ||
+            (s = mfh_add_row_rms_norm(c, ws->residual.buf, ws->ffn_input.buf, x, ws->op.buf,
+                                      lw.ffn_norm.tensor, cfg.block_norm_epsilon)))
+            return s;
+        // The last layer's FFN runs on the last row only (execution.rs:282-306).
+        const bool last = index + 1 == L;
+        Workspace *fw = ws;
+        mfh_buf *ffn_input = ws->ffn_input.buf, *residual = ws->residual.buf;
+        if (last && rows > 1) {
+            fw = ws1;
+            if ((s = mfh_copy_rect_2d(c, ws1->ffn_input.buf, ws->ffn_input.buf, rows - 1, 0, 0, 0,
+                                      1, cfg.hidden)) ||
+                (s = mfh_copy_rect_2d(c, ws1->residual.buf, ws->residual.buf, rows - 1, 0, 0, 0,
+                                      1, cfg.hidden)))
+                return s;
+            ffn_input = ws1->ffn_input.buf;
+            residual = ws1->residual.buf;
+        }
+        if ((s = ffn(m, lw, *fw, ffn_input, fw->down.buf)))
+            return s;
+        // Next layer's operator norm (or the final embedding norm) fused with
+        // the residual add.
+        mfh_buf *next_x = fw->x[1 - p].buf, *next_u = fw->u[1 - p].buf;
+        const Weight &next_norm = last ? m->embedding_norm : m->layers[index + 1].operator_norm;
+        const float eps = last ? cfg.norm_epsilon : cfg.block_norm_epsilon;
+        if ((s = need(c, next_norm)) ||
+            (s = mfh_add_row_rms_norm(c, next_x, next_u, residual, fw->down.buf, next_norm.tensor,
+                                      eps)))
+            return s;
+        p = 1 - p;
+        x = next_x;
+        u = next_u;
+    }
+    if (produce_logits && (s = weight_linear(c, m->logits.buf, u, m->embedding)))
+        return s;
+    m->length += rows;
+    return MFH_OK;
+}
+
+}  // namespace
+}  // namespace mfh
+
+extern "C" {
+
+mfh_status mfl_create(mfh_ctx *ctx, const mfl_config *config, mfl_model **out)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    if (!config || !out)
+        return fail(ctx, MFH_INVALID_ARGUMENT, "LFM2 configuration or output pointer is null");
+    const mfl_config &c = *config;
+    // Lfm2Config::validate (config.rs:54-100).
+    if (c.hidden == 0 || c.intermediate == 0 || c.attention_heads == 0 ||
+        c.key_value_heads == 0 || c.conv_width == 0 || c.vocab == 0 || c.layer_count == 0 ||
+        !c.layer_kinds || c.head_dim == 0 || c.max_tokens == 0)
+        return fail(ctx, MFH_INVALID_ARGUMENT, "LFM2 configuration has a zero dimension");
+    if (uint64_t(c.attention_heads) * c.head_dim != c.hidden)
+        return fail(ctx, MFH_INVALID_SHAPE, "LFM2 hidden size must equal heads * head_dim");
+    if (c.attention_heads % c.key_value_heads != 0)
+        return fail(ctx, MFH_INVALID_SHAPE,
+                    "query heads must be a nonzero multiple of key/value heads");
+    for (uint32_t i = 0; i < c.layer_count; ++i)
+        if (c.layer_kinds[i] > 1)
+            return fail(ctx, MFH_INVALID_ARGUMENT, "unknown LFM2 layer kind");
+    auto m = std::make_unique<mfl_model>();
+    m->ctx = ctx;
+    m->config = c;
+    m->kinds.assign(c.layer_kinds, c.layer_kinds + c.layer_count);
+    m->config.layer_kinds = m->kinds.data();
+    m->kv_width = uint64_t(c.key_value_heads) * c.head_dim;
+    m->layers.resize(c.layer_count);
+    m->state = std::vector<LayerState>(c.layer_count);
+    mfh_status s = MFH_OK;
+    for (uint32_t i = 0; i < c.layer_count && !s; ++i) {
+        LayerState &st = m->state[i];
+        if (m->kinds[i] == 0) {
+            s = alloc(ctx, st.history, c.conv_width - 1, c.hidden, MFH_CLASS_CACHE, true);
+        } else {
+            s = alloc(ctx, st.key, c.max_tokens, m->kv_width, MFH_CLASS_CACHE, true);
+            if (!s)
+                s = alloc(ctx, st.value, c.max_tokens, m->kv_width, MFH_CLASS_CACHE, true);
+        }
+    }
+    if (!s)
+        s = alloc(ctx, m->logits, 1, c.vocab, MFH_CLASS_CACHE, true);
+    if (!s) {
+        const uint64_t dims[1] = {1};
+        s = mfh_alloc_f32(ctx, dims, 1, MFH_CLASS_CACHE, 1, &m->sampled.buf);
+    }
+    if (s)
+        return s;
+    *out = m.release();
+    return MFH_OK;
+}
+
+void mfl_destroy(mfl_model *model)
+{
+    delete model;
+}
+
+mfh_status mfl_set_weight(mfl_model *m, uint32_t role, uint32_t layer, const mfh_buf *tensor,
+                          const mfh_buf *scales)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    mfh_ctx *c = m->ctx;
+    mfh_status s = scales ? check_u8(c, tensor) : check_f32(c, tensor);
+    if (!s && scales)
+        s = check_f32(c, scales);
+    if (s)
+        return s;
+    Weight w{tensor, scales};
+    if (role == MFL_TOKEN_EMBEDDING) {
+        m->embedding = w;
+        return MFH_OK;
+    }
+    if (role == MFL_EMBEDDING_NORM) {
+        m->embedding_norm = w;
+        return MFH_OK;
+    }
+    if (role > MFL_FFN_W3)
+        return fail(c, MFH_INVALID_ARGUMENT, "unknown LFM2 weight role");
+    if (layer >= m->config.layer_count)
+        return fail(c, MFH_OUT_OF_BOUNDS, "LFM2 layer index exceeds the layer count");
+    const bool conv = m->kinds[layer] == 0;
+    const bool conv_role = role == MFL_CONV_KERNEL || role == MFL_CONV_IN || role == MFL_CONV_OUT;
+    const bool attention_role = role >= MFL_QUERY_NORM && role <= MFL_OUTPUT;
+    if ((conv && attention_role) || (!conv && conv_role))
+        return fail(c, MFH_UNEXPECTED_TENSOR, "LFM2 weight role does not match the layer kind");
+    LayerWeights &lw = m->layers[layer];
+    Weight *slot[] = {nullptr,          nullptr,         &lw.operator_norm, &lw.ffn_norm,
+                      &lw.conv_kernel,  &lw.conv_in,     &lw.conv_out,      &lw.query_norm,
+                      &lw.key_norm,     &lw.query,       &lw.key,           &lw.value,
+                      &lw.output,       &lw.w1,          &lw.w2,            &lw.w3};
+    *slot[role] = w;
+    return MFH_OK;
+}
+
+mfh_status mfl_reset(mfl_model *m)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    DeviceGuard guard(m->ctx->device);
+    for (uint32_t i = 0; i < m->config.layer_count; ++i) {
+        LayerState &st = m->state[i];
+        st.length = 0;
+        if (st.history.buf && st.history.buf->elements)
+            launch_fill_f32(m->ctx->stream, static_cast<float *>(st.history.buf->dev),
+                            st.history.buf->elements, 0.0f);
+    }
+    m->length = 0;
+    return MFH_OK;
+}
+
+uint64_t mfl_length(const mfl_model *m)
+{
+    return m ? m->length : 0;
+}
+
+mfh_status mfl_append(mfl_model *m, const uint32_t *tokens, size_t count,
+                      const mfh_buf *device_ids, int produce_logits)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    if (device_ids && tokens)
+        return fail(m->ctx, MFH_INVALID_ARGUMENT, "token ids must be either host or device ids");
+    if (!device_ids && count && !tokens)
+        return fail(m->ctx, MFH_INVALID_ARGUMENT, "host id pointer is null");
+    return append(m, tokens, count, device_ids, produce_logits != 0);
+}
+
+mfh_status mfl_sample(mfl_model *m)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    return mfh_argmax(m->ctx, m->sampled.buf, m->logits.buf);
+}
+
+mfh_status mfl_generate(mfl_model *m, uint32_t steps, mfh_buf *ids_out)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    mfh_ctx *c = m->ctx;
+    const uint64_t dims[1] = {steps};
+    mfh_status s = check_output(c, ids_out, dims, 1);
+    if (s)
+        return s;
+    if (m->length + steps > m->config.max_tokens)
+        return fail(c, MFH_OUT_OF_BOUNDS, "append exceeds configured logical prefix capacity");
+    mark_written(ids_out);
+    for (uint32_t i = 0; i < steps; ++i) {
+        if ((s = mfl_sample(m)))
+            return s;
+        {
+            DeviceGuard guard(c->device);
+            launch_copy(c->stream, static_cast<float *>(ids_out->dev) + i,
+                        static_cast<const float *>(m->sampled.buf->dev), 1);
+        }
+        if ((s = append(m, nullptr, 0, m->sampled.buf, true)))
+            return s;
+    }
+    return MFH_OK;
+}
+
+const mfh_buf *mfl_logits(const mfl_model *m)
+{
+    return m ? m->logits.buf : nullptr;
+}
+
+const mfh_buf *mfl_sampled(const mfl_model *m)
+{
+    return m ? m->sampled.buf : nullptr;
+}
+
+}  // extern "C"

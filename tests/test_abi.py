@@ -14,7 +14,7 @@ from runtime_amd import _ffi
 
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 HEADERS = sorted((ROOT / "include").glob("*.h"))
-DECL = re.compile(r"^\s*(?:const\s+)?[\w\s\*]*?\b(mf[hc]_\w+)\s*\(", re.MULTILINE)
+DECL = re.compile(r"^\s*(?:const\s+)?[\w\s\*]*?\b(mf[hcl]_\w+)\s*\(", re.MULTILINE)
 
 
 def declared_symbols() -> set[str]:

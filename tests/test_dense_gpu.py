@@ -191,12 +191,31 @@ def test_split_half_rotary_bitwise(backend, tokens, heads, dim, theta):
     assert bits_equal(backend.read(out), want)
 
 
+@pytest.mark.parametrize("base", [0, 2047, (1 << 24) - 2, (1 << 40) + 3])
+def test_rotary_consecutive_positions_bitwise(backend, base):
+    # Consecutive positions travel as a base in the kernel arguments; the
+    # device's u64 -> f32 conversion must round as the host's does (2^24 + 1
+    # rounds to 2^24 here).
+    say("rotary consecutive", base)
+    tokens, heads, dim = 4, 3, 64
+    x = rng_f32(45, (tokens, heads * dim))
+    positions = np.arange(base, base + tokens, dtype=np.uint64)
+    out = backend.allocate_f32(x.shape)
+    backend.split_half_rotary(out, up(backend, x), positions,
+                              RotarySpec(PackedHeadSpec(heads, dim), np.float32(1e6)))
+    want = oracle.split_half_rotary(x, positions, heads, dim, np.float32(1e6))
+    assert bits_equal(backend.read(out), want)
+
+
+@pytest.mark.parametrize("consecutive", [True, False])
 @pytest.mark.parametrize("tokens,qh,kvh,dim", [(1, 32, 8, 64), (1, 16, 8, 64), (6, 4, 2, 8)])
-def test_qk_norm_rope(backend, tokens, qh, kvh, dim):
-    say("qk_norm_rope", tokens, qh, kvh, dim)
+def test_qk_norm_rope(backend, tokens, qh, kvh, dim, consecutive):
+    say("qk_norm_rope", tokens, qh, kvh, dim, consecutive)
     q, k = rng_f32(50, (tokens, qh * dim)), rng_f32(51, (tokens, kvh * dim))
     qw, kw = rng_f32(52, (dim,)), rng_f32(53, (dim,))
     positions = np.arange(100, 100 + tokens, dtype=np.uint64)
+    if not consecutive:
+        positions = (positions * 7 + 3)[::-1].copy()
     q_out, k_out = backend.allocate_f32(q.shape), backend.allocate_f32(k.shape)
     backend.qk_norm_rope(q_out, k_out, up(backend, q), up(backend, k), up(backend, qw),
                          up(backend, kw), positions,
