@@ -74,6 +74,64 @@ def cpu_baseline(weights, xs) -> dict:
                       f"{total_bytes / 1e6:.0f} MB algorithmic, {seconds:.1f} s)"}
 
 
+# LFM2 workloads: (config, prompt tokens, greedy decode steps).
+LFM2_WORKLOADS = {
+    "350m": ("lfm2_350m", 128, 256),    # all-ternary 350M shape
+    "1.2b": ("lfm2_1_2b", 2048, 512),   # NF4 attn/conv, ternary FFN, INT8 embedding
+}
+
+
+def lfm2_decode(backend, name: str) -> dict:
+    """Random-init model of the named shape (seeded N(0, 0.02) weights
+    quantized per role, unit norm weights), a uniform-random prompt
+    (seed 0x7043_0001) prefilled as one token pass, then greedy decode on the
+    device (argmax -> device-id gather each step, no host round trip).
+    Decode tok/s = steps / device time of the decode loop (HIP events);
+    prefill tok/s likewise for the prompt pass."""
+    from runtime_amd import convert, hiptime, lfm2
+
+    factory, prompt_len, steps = LFM2_WORKLOADS[name]
+    cfg = getattr(lfm2, factory)(max_tokens=prompt_len + steps + 1)
+    t0 = time.perf_counter()
+    model = lfm2.Lfm2Model(backend, cfg)
+    lfm2.synthetic_weights(model)
+    weight_bytes = sum(
+        int(np.prod(shape)) * BITS[cfg.formats[lfm2._role_group(role)]] // 8
+        + int(np.prod(shape)) // 128 * 2
+        for role, _, shape, matmul in lfm2.role_shapes(cfg) if matmul)
+    backend.synchronize()
+    build_s = time.perf_counter() - t0
+    prompt = convert.token_ids(prompt_len, 0x7043_0001, cfg.vocab)
+    stream = backend.stream()
+    # Warm pass: builds the repacked layouts and the workspaces of both row
+    # counts, so the timed passes allocate nothing.
+    model.append(prompt)
+    model.generate(4)
+    backend.synchronize()
+    model.reset()
+    e0, e1, e2 = hiptime.Event(), hiptime.Event(), hiptime.Event()
+    e0.record(stream)
+    model.append(prompt)
+    e1.record(stream)
+    ids = model.generate(steps)
+    e2.record(stream)
+    e2.synchronize()
+    prefill_ms = e1.elapsed_ms(e0)
+    decode_ms = e2.elapsed_ms(e1)
+    tokens = backend.read(ids)
+    finite = bool(np.all(np.isfinite(tokens)))
+    model.close()
+    log(f"lfm2 {name}: prefill {prompt_len} in {prefill_ms:.1f} ms, "
+        f"decode {steps} in {decode_ms:.1f} ms")
+    return {"config": factory, "prompt": prompt_len, "decode_steps": steps,
+            "decode_tok_s": round(steps / (decode_ms / 1e3), 1),
+            "decode_ms_per_token": round(decode_ms / steps, 4),
+            "prefill_tok_s": round(prompt_len / (prefill_ms / 1e3), 1),
+            "weight_bytes_per_token": weight_bytes,
+            "decode_weight_GBs": round(weight_bytes / (decode_ms / steps / 1e3) / 1e9, 1),
+            "tokens_finite": finite, "build_s": round(build_s, 1)}
+
+
 def profile_only(backend, args) -> int:
     """Launch sequences for rocprofv3: `dominant` builds the 65536x2048 INT8
     head (same seed as the sweep) on `copies` buffers and launches it
@@ -83,6 +141,9 @@ def profile_only(backend, args) -> int:
     from runtime_amd import convert
     from runtime_amd.backend import WEIGHT
 
+    if args.profile.startswith("lfm2-"):
+        log(json.dumps(lfm2_decode(backend, args.profile[5:])))
+        return 0
     if args.profile == "copy":
         count = 64 << 20
         src = backend.allocate_f32((count,))
@@ -120,7 +181,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--profile", choices=["dominant", "copy"],
+    ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
+                    help="also time greedy decode of the LFM2 model shapes")
+    ap.add_argument("--profile", choices=["dominant", "copy", "lfm2-350m", "lfm2-1.2b"],
                     help="run only the dominant operation (or a 256 MiB device copy, the "
                          "counter calibration) for rocprofv3, and print no JSON line")
     args = ap.parse_args()
@@ -273,6 +336,11 @@ def main() -> int:
     if not args.no_cpu:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(weights, xs)
+    del dev_w, dev_x, dev_out, weights
+    if args.lfm2 != "none":
+        result["lfm2"] = {}
+        for name in (["350m", "1.2b"] if args.lfm2 == "both" else [args.lfm2]):
+            result["lfm2"][name] = lfm2_decode(backend, name)
     print(json.dumps(result))
     backend.close()
     return 0
