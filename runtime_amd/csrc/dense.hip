@@ -153,68 +153,82 @@ __global__ __launch_bounds__(kBlock) void gather_columns_kernel(float *__restric
 
 // Row argmax: first strict maximum among admitted finite values; any
 // admitted non-finite value, or no admitted value, gives NaN
-// (backend-cpu/src/dense.rs:373-473).  One 1024-thread block per row; each
-// thread scans a strided slice in increasing order, then (value, index)
-// pairs reduce with ties going to the lower index.
+// (backend-cpu/src/dense.rs:373-473).  A 1024-thread block scans a column
+// range, each thread a strided slice in increasing order, then (value,
+// index) candidates reduce with ties going to the lower index.  Wide rows
+// are cut into ranges scanned by separate blocks whose candidates a second
+// kernel reduces the same way.
 constexpr int kArgmaxBlock = 1024;
+constexpr uint32_t kArgmaxRange = 8192;
 
-// Whether candidate (ov, oi) replaces (best, index); UINT32_MAX marks none.
+struct Candidate {
+    float value;
+    uint32_t index;  // UINT32_MAX: no admitted value
+    int poisoned;
+};
+
+// Whether candidate (ov, oi) replaces (best, index).
 __device__ __forceinline__ bool takes(float ov, uint32_t oi, float best, uint32_t index)
 {
     return oi != UINT32_MAX && (index == UINT32_MAX || ov > best || (ov == best && oi < index));
 }
 
-__device__ void argmax_row(float *out, const float *__restrict__ row, uint32_t width,
-                           const uint64_t *__restrict__ mask)
+__device__ __forceinline__ void merge(Candidate &c, float ov, uint32_t oi, int op)
+{
+    c.poisoned |= op;
+    if (takes(ov, oi, c.value, c.index)) {
+        c.value = ov;
+        c.index = oi;
+    }
+}
+
+// Block-wide reduction; the result is valid in thread 0.
+__device__ Candidate reduce_candidates(Candidate c)
 {
     __shared__ float best_value[kArgmaxBlock / 64];
     __shared__ uint32_t best_index[kArgmaxBlock / 64];
     __shared__ int poison[kArgmaxBlock / 64];
-    float best = -__builtin_inff();
-    uint32_t index = UINT32_MAX;
-    int poisoned = 0;
-    for (uint32_t j = threadIdx.x; j < width; j += kArgmaxBlock) {
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        merge(c, __shfl_xor(c.value, offset, 64), __shfl_xor(c.index, offset, 64),
+              __shfl_xor(c.poisoned, offset, 64));
+    const int wave = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) {
+        best_value[wave] = c.value;
+        best_index[wave] = c.index;
+        poison[wave] = c.poisoned;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < kArgmaxBlock / 64; ++w)
+            merge(c, best_value[w], best_index[w], poison[w]);
+    return c;
+}
+
+__device__ Candidate scan_range(const float *__restrict__ row, uint32_t begin, uint32_t end,
+                                const uint64_t *__restrict__ mask)
+{
+    Candidate c{-__builtin_inff(), UINT32_MAX, 0};
+    for (uint32_t j = begin + threadIdx.x; j < end; j += kArgmaxBlock) {
         if (mask && !((mask[j >> 6] >> (j & 63)) & 1))
             continue;
         const float v = row[j];
         if (!isfinite(v)) {
-            poisoned = 1;
-        } else if (index == UINT32_MAX || v > best) {
+            c.poisoned = 1;
+        } else if (c.index == UINT32_MAX || v > c.value) {
             // Strictly greater only: a thread's indices increase, so equal
             // values keep the earlier one.
-            best = v;
-            index = j;
+            c.value = v;
+            c.index = j;
         }
     }
-#pragma unroll
-    for (int offset = 32; offset > 0; offset >>= 1) {
-        const float ov = __shfl_xor(best, offset, 64);
-        const uint32_t oi = __shfl_xor(index, offset, 64);
-        poisoned |= __shfl_xor(poisoned, offset, 64);
-        if (takes(ov, oi, best, index)) {
-            best = ov;
-            index = oi;
-        }
-    }
-    const int wave = threadIdx.x >> 6;
-    if ((threadIdx.x & 63) == 0) {
-        best_value[wave] = best;
-        best_index[wave] = index;
-        poison[wave] = poisoned;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < kArgmaxBlock / 64; ++w) {
-            poisoned |= poison[w];
-            if (takes(best_value[w], best_index[w], best, index)) {
-                best = best_value[w];
-                index = best_index[w];
-            }
-        }
-        *out = (poisoned || index == UINT32_MAX) ? __builtin_nanf("") : float(index);
-    }
-    // The shared slots are rewritten by the next row.
-    __syncthreads();
+    return reduce_candidates(c);
+}
+
+__device__ __forceinline__ float argmax_marker(const Candidate &c)
+{
+    return (c.poisoned || c.index == UINT32_MAX) ? __builtin_nanf("") : float(c.index);
 }
 
 __global__ __launch_bounds__(kArgmaxBlock) void argmax_kernel(float *__restrict__ out,
@@ -222,8 +236,37 @@ __global__ __launch_bounds__(kArgmaxBlock) void argmax_kernel(float *__restrict_
                                                               uint32_t rows, uint32_t width,
                                                               const uint64_t *__restrict__ mask)
 {
-    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x)
-        argmax_row(out + r, in + uint64_t(r) * width, width, mask);
+    for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+        const Candidate c = scan_range(in + uint64_t(r) * width, 0, width, mask);
+        if (threadIdx.x == 0)
+            out[r] = argmax_marker(c);
+    }
+}
+
+// Stage 1 of the wide-row path: block b scans range b % ranges of row
+// b / ranges.
+__global__ __launch_bounds__(kArgmaxBlock) void argmax_range_kernel(
+    Candidate *__restrict__ partial, const float *__restrict__ in, uint32_t width,
+    uint32_t ranges, const uint64_t *__restrict__ mask)
+{
+    const uint32_t r = blockIdx.x / ranges, range = blockIdx.x % ranges;
+    const uint32_t begin = range * kArgmaxRange;
+    const uint32_t end = width - begin < kArgmaxRange ? width : begin + kArgmaxRange;
+    const Candidate c = scan_range(in + uint64_t(r) * width, begin, end, mask);
+    if (threadIdx.x == 0)
+        partial[blockIdx.x] = c;
+}
+
+__global__ __launch_bounds__(kArgmaxBlock) void argmax_final_kernel(
+    float *__restrict__ out, const Candidate *__restrict__ partial, uint32_t ranges)
+{
+    Candidate c{-__builtin_inff(), UINT32_MAX, 0};
+    const Candidate *row = partial + uint64_t(blockIdx.x) * ranges;
+    for (uint32_t i = threadIdx.x; i < ranges; i += kArgmaxBlock)
+        merge(c, row[i].value, row[i].index, row[i].poisoned);
+    c = reduce_candidates(c);
+    if (threadIdx.x == 0)
+        out[blockIdx.x] = argmax_marker(c);
 }
 
 // ---- element-wise ------------------------------------------------------
@@ -546,6 +589,114 @@ __global__ __launch_bounds__(kBlock) void gqa_kernel(float *__restrict__ out,
     }
 }
 
+// Split-key attention for few (token, head) pairs (decode): the visible keys
+// of one (token, key/value head) are cut into kSplitKeys-wide ranges, one
+// block per range serving every query head of the group.  A block stores,
+// per query head, its range maximum m, its exponent sum l = sum exp(s - m)
+// and the unnormalised sum acc = sum exp(s - m) * v; the combine kernel
+// rescales the ranges to the global maximum.  Scores keep the reference's
+// sequential dot; the softmax normalisation is regrouped (exp(s - m) *
+// exp(m - M) / L for exp(s - M) / L), a reassociation within f32 rounding.
+constexpr int kSplitKeys = 256;
+constexpr uint32_t kSplitMaxGroup = 8;
+constexpr uint32_t kSplitMaxDim = 256;
+
+__global__ __launch_bounds__(kBlock) void gqa_split_kernel(float *__restrict__ partial,
+                                                           const float *__restrict__ query,
+                                                           const float *__restrict__ key_cache,
+                                                           const float *__restrict__ value_cache,
+                                                           GqaShape g, uint32_t splits)
+{
+    __shared__ float q[kSplitMaxGroup * kSplitMaxDim];
+    __shared__ float p[kSplitMaxGroup][kSplitKeys];
+    __shared__ float stats[2][kSplitMaxGroup];
+    __shared__ float scratch[kBlock / 64];
+
+    const uint32_t split = blockIdx.x % splits;
+    const uint64_t pair = blockIdx.x / splits;
+    const uint32_t kv_head = uint32_t(pair % g.key_value_heads);
+    const uint64_t token = pair / g.key_value_heads;
+    const uint32_t d = g.head_dim, group = g.group;
+    const uint64_t kv_width = uint64_t(g.key_value_heads) * d;
+    const uint64_t visible = g.initial_len + token + 1;
+    const uint64_t begin = uint64_t(split) * kSplitKeys;
+    const uint32_t count =
+        begin >= visible ? 0u : uint32_t(visible - begin < kSplitKeys ? visible - begin : kSplitKeys);
+    // Record layout: [token][query head][split] of (m, l, acc[d]).
+    const uint64_t record = uint64_t(d) + 2;
+    const uint32_t head0 = kv_head * group;
+    float *out = partial + ((token * g.query_heads + head0) * splits + split) * record;
+
+    const float *qrow = query + (token * g.query_heads + head0) * uint64_t(d);
+    for (uint32_t i = threadIdx.x; i < group * d; i += kBlock)
+        q[i] = qrow[i];
+    __syncthreads();
+
+    // Scores: thread j owns key begin + j for every head of the group.
+    const float *keys = key_cache + kv_head * uint64_t(d);
+    if (threadIdx.x < count) {
+        const float *krow = keys + (begin + threadIdx.x) * kv_width;
+        for (uint32_t h = 0; h < group; ++h) {
+            const float *qh = q + h * d;
+            float dot = 0.0f;
+            for (uint32_t c = 0; c < d; ++c)
+                dot += qh[c] * krow[c];
+            p[h][threadIdx.x] = dot * g.scale;
+        }
+    }
+    for (uint32_t h = 0; h < group; ++h) {
+        const float s = threadIdx.x < count ? p[h][threadIdx.x] : -__builtin_inff();
+        const float m = block_max(s, scratch);
+        const float e = threadIdx.x < count ? expf(s - m) : 0.0f;
+        if (threadIdx.x < count)
+            p[h][threadIdx.x] = e;
+        const float l = block_sum(e, scratch);
+        if (threadIdx.x == 0) {
+            stats[0][h] = m;
+            stats[1][h] = l;
+        }
+    }
+    __syncthreads();
+    const float *values = value_cache + kv_head * uint64_t(d);
+    for (uint32_t t = threadIdx.x; t < group * d; t += kBlock) {
+        const uint32_t h = t / d, dim = t - h * d;
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < count; ++j)
+            acc += p[h][j] * values[(begin + j) * kv_width + dim];
+        out[uint64_t(h) * splits * record + 2 + dim] = acc;
+    }
+    if (threadIdx.x < group) {
+        out[uint64_t(threadIdx.x) * splits * record] = stats[0][threadIdx.x];
+        out[uint64_t(threadIdx.x) * splits * record + 1] = stats[1][threadIdx.x];
+    }
+}
+
+// One block per (token, query head): out = sum_s acc_s e^(m_s - M) / L with
+// M = max m_s and L = sum l_s e^(m_s - M), ranges in order.  Empty ranges
+// (l = 0) are skipped; a NaN anywhere reaches the output.
+__global__ __launch_bounds__(kBlock) void gqa_combine_kernel(float *__restrict__ out,
+                                                             const float *__restrict__ partial,
+                                                             uint32_t head_dim, uint32_t splits)
+{
+    const uint64_t record = uint64_t(head_dim) + 2;
+    const float *rec = partial + uint64_t(blockIdx.x) * splits * record;
+    float maximum = -__builtin_inff();
+    for (uint32_t s = 0; s < splits; ++s)
+        if (rec[s * record + 1] != 0.0f)
+            maximum = fmaxf(maximum, rec[s * record]);
+    float denominator = 0.0f;
+    for (uint32_t s = 0; s < splits; ++s)
+        if (rec[s * record + 1] != 0.0f)
+            denominator += rec[s * record + 1] * expf(rec[s * record] - maximum);
+    for (uint32_t dim = threadIdx.x; dim < head_dim; dim += kBlock) {
+        float acc = 0.0f;
+        for (uint32_t s = 0; s < splits; ++s)
+            if (rec[s * record + 1] != 0.0f)
+                acc += rec[s * record + 2 + dim] * expf(rec[s * record] - maximum);
+        out[uint64_t(blockIdx.x) * head_dim + dim] = acc / denominator;
+    }
+}
+
 // ---- gated short convolution -------------------------------------------
 
 // u = B * V per (token, channel); out = (sum over taps of kernel * u) * C,
@@ -619,12 +770,35 @@ void launch_gather_columns(hipStream_t stream, float *out, const float *in, cons
                                                                              width, count);
 }
 
-void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
-                   const uint64_t *mask)
+namespace {
+
+// Ranges per row of the wide-row path, or 0 when one block per row is used.
+uint32_t argmax_ranges(uint32_t rows, uint32_t width)
 {
-    if (rows)
-        argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, in, rows, width,
-                                                                      mask);
+    const uint32_t ranges = (width + kArgmaxRange - 1) / kArgmaxRange;
+    return (ranges >= 2 && rows <= 64) ? ranges : 0;
+}
+
+}  // namespace
+
+size_t argmax_scratch_bytes(uint32_t rows, uint32_t width)
+{
+    return size_t(argmax_ranges(rows, width)) * rows * sizeof(Candidate);
+}
+
+void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
+                   const uint64_t *mask, void *scratch)
+{
+    if (!rows)
+        return;
+    if (const uint32_t ranges = argmax_ranges(rows, width)) {
+        Candidate *partial = static_cast<Candidate *>(scratch);
+        argmax_range_kernel<<<rows * ranges, kArgmaxBlock, 0, stream>>>(partial, in, width,
+                                                                       ranges, mask);
+        argmax_final_kernel<<<rows, kArgmaxBlock, 0, stream>>>(out, partial, ranges);
+        return;
+    }
+    argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, in, rows, width, mask);
 }
 
 void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
@@ -691,8 +865,34 @@ void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, c
             query_heads, key_heads, head_dim, theta, epsilon);
 }
 
+namespace {
+
+// Key ranges of the split path, or 0 when one block per (token, query head)
+// already fills the device or the ranges would be too few to pay for the
+// combine launch.
+uint32_t gqa_splits(const GqaShape &g)
+{
+    const uint64_t pairs = g.tokens * g.query_heads;
+    const uint64_t longest = g.initial_len + g.tokens;
+    const uint64_t splits = (longest + kSplitKeys - 1) / kSplitKeys;
+    if (pairs >= 1024 || splits < 2 || g.group > kSplitMaxGroup || g.head_dim > kSplitMaxDim ||
+        splits * g.tokens * g.key_value_heads > (uint64_t(1) << 31))
+        return 0;
+    return uint32_t(splits);
+}
+
+}  // namespace
+
+size_t gqa_scratch_bytes(const GqaShape &g)
+{
+    const uint32_t splits = gqa_splits(g);
+    return splits ? size_t(g.tokens) * g.query_heads * splits * (g.head_dim + 2) * sizeof(float)
+                  : 0;
+}
+
 void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
-                const float *value, float *key_cache, float *value_cache, const GqaShape &g)
+                const float *value, float *key_cache, float *value_cache, const GqaShape &g,
+                float *scratch)
 {
     const uint64_t kv_width = uint64_t(g.key_value_heads) * g.head_dim;
     const uint64_t appended = g.tokens * kv_width;
@@ -702,6 +902,14 @@ void launch_gqa(hipStream_t stream, float *out, const float *query, const float 
     const uint64_t blocks = g.tokens * g.query_heads;
     if (!blocks)
         return;
+    const uint32_t splits = gqa_splits(g);
+    if (splits) {
+        gqa_split_kernel<<<unsigned(g.tokens * g.key_value_heads * splits), kBlock, 0, stream>>>(
+            scratch, query, key_cache, value_cache, g, splits);
+        gqa_combine_kernel<<<unsigned(blocks), kBlock, 0, stream>>>(out, scratch, g.head_dim,
+                                                                     splits);
+        return;
+    }
     const size_t lds = (size_t(g.head_dim) + kKeyChunk + kBlock) * sizeof(float);
     gqa_kernel<<<unsigned(blocks), kBlock, lds, stream>>>(out, query, key_cache, value_cache, g);
 }

@@ -197,8 +197,14 @@ mfh_status run_argmax(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input, const
         if (s)
             return s;
     }
-    launch_argmax(ctx->stream, dev_f32(output), dev_f32(input), uint32_t(input->dims[0]),
-                  uint32_t(input->dims[1]), dev_mask);
+    const uint32_t rows = uint32_t(input->dims[0]), width = uint32_t(input->dims[1]);
+    void *partials = nullptr;
+    if (const size_t bytes = argmax_scratch_bytes(rows, width)) {
+        partials = work_scratch(ctx, bytes);
+        if (!partials)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+    }
+    launch_argmax(ctx->stream, dev_f32(output), dev_f32(input), rows, width, dev_mask, partials);
     return launched(ctx);
 }
 
@@ -711,8 +717,14 @@ mfh_status mfh_causal_gqa(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *query,
     g.head_dim = head_dim;
     g.group = query_heads / key_value_heads;
     g.scale = 1.0f / std::sqrt(float(head_dim));
+    float *partials = nullptr;
+    if (const size_t bytes = gqa_scratch_bytes(g)) {
+        partials = static_cast<float *>(work_scratch(ctx, bytes));
+        if (!partials)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+    }
     launch_gqa(ctx->stream, dev_f32(output), dev_f32(query), dev_f32(key), dev_f32(value),
-               dev_f32(key_cache), dev_f32(value_cache), g);
+               dev_f32(key_cache), dev_f32(value_cache), g, partials);
     if ((s = launched(ctx)))
         return s;
     *cache_len = new_len;

@@ -98,9 +98,12 @@ void launch_gather_rows(hipStream_t stream, float *out, const float *table, cons
                         uint32_t count, uint32_t rows, uint64_t columns);
 void launch_gather_columns(hipStream_t stream, float *out, const float *in, const uint32_t *cols,
                            uint64_t rows, uint64_t width, uint32_t count);
-// `mask` is null for the unmasked selector.
+// `mask` is null for the unmasked selector.  Few wide rows are scanned by
+// several blocks per row whose candidates take argmax_scratch_bytes bytes of
+// `scratch` (0: none used).
+size_t argmax_scratch_bytes(uint32_t rows, uint32_t width);
 void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
-                   const uint64_t *mask);
+                   const uint64_t *mask, void *scratch);
 // op 0: left + right, op 1: left * right.
 void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
                    size_t count);
@@ -124,8 +127,13 @@ void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, c
                          const float *key, const float *query_weight, const float *key_weight,
                          const Positions &positions, uint64_t tokens, uint32_t query_heads,
                          uint32_t key_heads, uint32_t head_dim, float theta, float epsilon);
+// Appends the new rows, then attends.  Few (token, head) pairs over long
+// caches take a split-key path whose partials need gqa_scratch_bytes(g)
+// bytes of `scratch` (0: no scratch used).
+size_t gqa_scratch_bytes(const GqaShape &g);
 void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
-                const float *value, float *key_cache, float *value_cache, const GqaShape &g);
+                const float *value, float *key_cache, float *value_cache, const GqaShape &g,
+                float *scratch);
 void launch_short_conv(hipStream_t stream, float *out, const float *projection,
                        const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
                        uint32_t width);

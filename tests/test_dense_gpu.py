@@ -239,6 +239,11 @@ GQA_CASES = [
     (2, 3, 8, 4, 2, 96),             # head wider than a wave, two key groups
     (2, 3, 8, 2, 1, 256),
     (2, 3, 8, 2, 2, 320),            # two dimensions per thread
+    # split-key path (few (token, head) pairs over more than 256 keys)
+    (4, 700, 1024, 32, 8, 64),
+    (1, 3000, 4096, 6, 2, 128),
+    (1, 600, 1024, 8, 1, 64),
+    (2, 513, 1024, 16, 2, 256),
 ]
 
 
@@ -308,6 +313,21 @@ def test_argmax_poison_and_ties(backend):
     backend.argmax(out, up(backend, x))
     got = backend.read(out)
     assert got[0] == 1500 and np.isnan(got[1]) and np.isnan(got[2]) and got[3] == 0
+    assert bits_equal(got, oracle.argmax(x))
+
+
+def test_argmax_wide_rows_ties_and_poison(backend):
+    # Wide rows are scanned in ranges by separate blocks: ties across ranges
+    # keep the lower index and a NaN in any range poisons the row.
+    x = np.zeros((3, 40000), dtype=np.float32)
+    x[0, 9000] = x[0, 30000] = 5.0
+    x[1, 39999] = np.nan
+    x[2, 12345] = -np.inf
+    x[2, 20000] = 1.0
+    out = backend.allocate_f32((3,))
+    backend.argmax(out, up(backend, x))
+    got = backend.read(out)
+    assert got[0] == 9000 and np.isnan(got[1]) and np.isnan(got[2])
     assert bits_equal(got, oracle.argmax(x))
 
 
