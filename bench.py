@@ -113,7 +113,9 @@ def lfm2_decode(backend, name: str) -> dict:
     e0.record(stream)
     model.append(prompt)
     e1.record(stream)
+    h0 = time.perf_counter()
     ids = model.generate(steps)
+    host_ms = (time.perf_counter() - h0) * 1e3
     e2.record(stream)
     e2.synchronize()
     prefill_ms = e1.elapsed_ms(e0)
@@ -129,6 +131,7 @@ def lfm2_decode(backend, name: str) -> dict:
             "prefill_tok_s": round(prompt_len / (prefill_ms / 1e3), 1),
             "weight_bytes_per_token": weight_bytes,
             "decode_weight_GBs": round(weight_bytes / (decode_ms / steps / 1e3) / 1e9, 1),
+            "host_enqueue_ms_per_token": round(host_ms / steps, 4),
             "tokens_finite": finite, "build_s": round(build_s, 1)}
 
 

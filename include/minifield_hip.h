@@ -336,9 +336,9 @@ mfh_status mfh_swiglu(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *gate, const 
 /* The HIP stream (hipStream_t) all work of `ctx` is ordered on, so a caller
  * can bracket launches with its own HIP events. */
 void *mfh_stream(const mfh_ctx *ctx);
-/* Kernel path forced for packed GEMV/GEMM: 0 = automatic selection,
- * 1 = FP32 FMA kernels only, 2 = matrix-core kernels only.  Returns the
- * previous setting. */
+/* Kernel path for packed GEMV/GEMM: 0 = automatic selection, 1 = FP32 FMA
+ * kernels only, 2 = automatic but with the matrix-core GEMV's activation
+ * prologue run as a kernel of its own.  Returns the previous setting. */
 int mfh_set_kernel_path(mfh_ctx *ctx, int path);
 
 #ifdef __cplusplus

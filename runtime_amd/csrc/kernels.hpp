@@ -35,6 +35,9 @@ struct PackedCall {
     PackedStream a, b;
     float *out_a = nullptr;  // [m, n]
     float *out_b = nullptr;  // [m, n] (Pair only)
+    // Matrix-core GEMV: run the activation prologue as its own kernel even
+    // where the in-kernel one fits (diagnostics).
+    bool separate_prologue = false;
 };
 
 // Decode GEMV for m <= 8 on FP32 FMA units.

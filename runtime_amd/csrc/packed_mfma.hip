@@ -112,17 +112,27 @@ struct GroupX {
     bool bad;
 };
 
-__device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_t g, uint32_t m,
-                                             uint32_t k)
+// This lane's two raw values of activation group g of batch slot b.
+__device__ __forceinline__ void fetch_group(const float *x, uint32_t b, uint32_t g, uint32_t m,
+                                            uint32_t k, float (&v)[2])
 {
-    const uint32_t lane = threadIdx.x;
+    const uint32_t lane = threadIdx.x & 63;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t kk = g * 128 + h * 64 + lane;
+        v[h] = (b < m && kk < k) ? x[size_t(b) * k + kk] : 0.0f;
+    }
+}
+
+// The group's exponent (max |x| < 2^e) and non-finite flag, wave-wide.
+__device__ __forceinline__ GroupX finish_group(const float (&raw)[2])
+{
     GroupX r;
     r.bad = false;
     float mx = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-        const uint32_t kk = g * 128 + h * 64 + lane;
-        float v = (b < m && kk < k) ? x[size_t(b) * k + kk] : 0.0f;
+        float v = raw[h];
         if (!isfinite(v)) {
             r.bad = true;
             v = 0.0f;
@@ -138,6 +148,14 @@ __device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_
     return r;
 }
 
+__device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_t g, uint32_t m,
+                                             uint32_t k)
+{
+    float raw[2];
+    fetch_group(x, b, g, m, k, raw);
+    return finish_group(raw);
+}
+
 // Ternary operand fields.  Within a 64-wide kstep, k = 16q + 4e + f puts
 // weight k in bits [2f, 2f+2) of code byte e of lane block q (f = k % 4).
 // The tile layout stores field 3 as (c + 2) mod 4, and the B operand's four
@@ -149,16 +167,19 @@ __device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_
 // corr = sum_{f<3} 4^f u_f - 64 sum_{f=3} u_f turns that into
 // sum_k (c_k - 1) * 4^f u_k, i.e. sum_k (c_k - 1) v_k to within 2^5 units of
 // the 2^30-scaled group maximum per weight.
+//
+// emit_digits: one wave writes the fragment bytes of activation group g of
+// batch slot b; kstep indices are relative to `s0`.  Lane 0 stores the
+// group factor 2^(e - 30) (NaN for a non-finite group) and, for ternary, the
+// correction.
 template <Format F>
-__global__ __launch_bounds__(64) void digits_kernel(const float *x, uint32_t m, uint32_t k,
-                                                    uint32_t groups, uint32_t nfrag,
-                                                    int8_t *afrag, float *xf, int2 *corr)
+__device__ __forceinline__ void emit_group(const GroupX &gx, uint32_t b, uint32_t g,
+                                           uint32_t nfrag, uint32_t s0, int8_t *afrag,
+                                           float *xf_out, int2 *corr_out)
 {
-    const uint32_t g = blockIdx.x, b = blockIdx.y;
-    const uint32_t lane = threadIdx.x;
-    const GroupX gx = load_group(x, b, g, m, k);
+    const uint32_t lane = threadIdx.x & 63;
     if (lane == 0)
-        xf[b * groups + g] = gx.bad ? __builtin_nanf("") : ldexpf(1.0f, gx.e - 30);
+        *xf_out = gx.bad ? __builtin_nanf("") : ldexpf(1.0f, gx.e - 30);
     long long corr_sum = 0;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
@@ -179,7 +200,7 @@ __global__ __launch_bounds__(64) void digits_kernel(const float *x, uint32_t m, 
         d[1] = int(int8_t(((vp >> 16) & 255) ^ 0x80));
         d[2] = int(int8_t(((vp >> 8) & 255) ^ 0x80));
         d[3] = int(int8_t((vp & 255) ^ 0x80));
-        const uint32_t s = kk / 64, r = kk % 64;
+        const uint32_t s = kk / 64 - s0, r = kk % 64;
         const uint32_t q = r / 16, c = r % 16;
         const uint32_t byte = (F == Format::Ternary) ? (4 * (c & 3) + (c >> 2)) : c;
 #pragma unroll
@@ -195,9 +216,55 @@ __global__ __launch_bounds__(64) void digits_kernel(const float *x, uint32_t m, 
         if (lane == 0) {
             // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
             const long long lo = ((corr_sum + 32768) & 65535) - 32768;
-            corr[size_t(b) * groups + g] = int2{int((corr_sum - lo) >> 16), int(lo)};
+            *corr_out = int2{int((corr_sum - lo) >> 16), int(lo)};
         }
     }
+}
+
+template <Format F>
+__global__ __launch_bounds__(64) void digits_kernel(const float *x, uint32_t m, uint32_t k,
+                                                    uint32_t groups, uint32_t nfrag,
+                                                    int8_t *afrag, float *xf, int2 *corr)
+{
+    const uint32_t g = blockIdx.x, b = blockIdx.y;
+    emit_group<F>(load_group(x, b, g, m, k), b, g, nfrag, 0, afrag, xf + b * groups + g,
+                  corr + b * groups + g);
+}
+
+// In-kernel prologue of one wave: the fragments of groups [g0, g0 + gpw) for
+// the live batch slots (b < m) into the wave's LDS area `frag`; slots at or
+// beyond m stay zero.  Loads of up to four groups are issued before any is
+// reduced.
+template <Format F, int NF>
+__device__ __forceinline__ void wave_prologue(const float *x, uint32_t m, uint32_t k, uint32_t g0,
+                                              uint32_t gpw, uint32_t s0, int8_t *frag,
+                                              float *fxf, int2 *fcorr)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t live = m < 4u * NF ? m : 4u * NF;
+    if (live < 4u * NF) {
+        v4i *zf = reinterpret_cast<v4i *>(frag);
+        for (uint32_t i = lane; i < gpw * 2 * NF * 64; i += 64)
+            zf[i] = v4i{0, 0, 0, 0};
+        for (uint32_t i = lane; i < 4 * NF * gpw; i += 64) {
+            fxf[i] = 0.0f;
+            fcorr[i] = int2{0, 0};
+        }
+    }
+    constexpr uint32_t kChunk = 4;
+    for (uint32_t b = 0; b < live; ++b)
+        for (uint32_t c0 = 0; c0 < gpw; c0 += kChunk) {
+            float raw[kChunk][2];
+#pragma unroll
+            for (uint32_t c = 0; c < kChunk; ++c)
+                if (c0 + c < gpw)
+                    fetch_group(x, b, g0 + c0 + c, m, k, raw[c]);
+#pragma unroll
+            for (uint32_t c = 0; c < kChunk; ++c)
+                if (c0 + c < gpw)
+                    emit_group<F>(finish_group(raw[c]), b, g0 + c0 + c, NF, s0, frag,
+                                  fxf + b * gpw + c0 + c, fcorr + b * gpw + c0 + c);
+        }
 }
 
 __global__ __launch_bounds__(64) void halves_kernel(const float *x, uint32_t m, uint32_t k,
@@ -242,7 +309,8 @@ struct MfmaArgs {
     const uint8_t *tiles[2];
     const void *scales[2];
     float *out[2];
-    uint32_t m, n, k_pad;
+    const float *x;  // activations [m, k] (in-kernel prologue)
+    uint32_t m, n, k, k_pad;
     uint32_t ksteps_per_wave;
 };
 
@@ -305,8 +373,8 @@ struct I8Block {
 };
 
 template <Format F, int T, int S, int NF>
-__device__ __forceinline__ void i8_load(I8Block<F, T, S, NF> &blk, const v4u *const (&wp)[S][T],
-                                        const v4i *ap, uint32_t index)
+__device__ __forceinline__ void i8_load_w(I8Block<F, T, S, NF> &blk,
+                                          const v4u *const (&wp)[S][T], uint32_t index)
 {
     using B = I8Block<F, T, S, NF>;
 #pragma unroll
@@ -316,11 +384,25 @@ __device__ __forceinline__ void i8_load(I8Block<F, T, S, NF> &blk, const v4u *co
 #pragma unroll
             for (int l = 0; l < B::LOADS; ++l)
                 blk.w[st][t][l] = wp[st][t][(index * B::LOADS + l) * 64];
+}
+
+template <Format F, int T, int S, int NF, typename AP>
+__device__ __forceinline__ void i8_load_a(I8Block<F, T, S, NF> &blk, AP ap, uint32_t index)
+{
+    using B = I8Block<F, T, S, NF>;
 #pragma unroll
     for (int ks = 0; ks < B::LB; ++ks)
 #pragma unroll
         for (int f = 0; f < NF; ++f)
             blk.af[ks][f] = ap[((index * B::LB + ks) * NF + f) * 64];
+}
+
+template <Format F, int T, int S, int NF, typename AP>
+__device__ __forceinline__ void i8_load(I8Block<F, T, S, NF> &blk, const v4u *const (&wp)[S][T],
+                                        AP ap, uint32_t index)
+{
+    i8_load_w(blk, wp, index);
+    i8_load_a(blk, ap, index);
 }
 
 template <Format F, int T, int S, int NF, bool HALF>
@@ -399,9 +481,19 @@ __device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF> &blk,
     }
 }
 
+// Bytes of dynamic LDS past the reduction area that the in-kernel prologue
+// uses per wave: the wave's digit fragments, group factors and corrections.
+__host__ __device__ constexpr size_t fused_wave_bytes(uint32_t ksteps_per_wave, int nf)
+{
+    return size_t(ksteps_per_wave) * nf * 1024 + size_t(4 * nf) * (ksteps_per_wave / 2) * 12;
+}
+
 // At most 8 waves per block: two per SIMD leaves 256 VGPRs per wave for the
-// double-buffered loop blocks.
-template <Format F, int T, int S, int NF, bool HALF, Epilogue E>
+// double-buffered loop blocks.  With FUSED each wave first computes the
+// digit fragments of its own K range from x into LDS (emit_digits) while its
+// first weights are in flight; otherwise digits_kernel wrote them to global
+// scratch.
+template <Format F, int T, int S, int NF, bool HALF, Epilogue E, bool FUSED>
 __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
 {
     using B = I8Block<F, T, S, NF>;
@@ -446,17 +538,46 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
                 accf[st][t][f] = 0.0f;
 
     B buf0, buf1;
-    if (nblk > 0)
-        i8_load(buf0, wp, ap, 0);
-    for (uint32_t i = 0; i < nblk; i += 2) {
-        if (i + 1 < nblk)
-            i8_load(buf1, wp, ap, i + 1);
-        i8_compute<F, T, S, NF, HALF>(buf0, accf, sp, xp, cp, i);
-        if (i + 1 < nblk) {
-            if (i + 2 < nblk)
-                i8_load(buf0, wp, ap, i + 2);
-            i8_compute<F, T, S, NF, HALF>(buf1, accf, sp, xp, cp, i + 1);
+    auto main_loop = [&](auto afp) {
+        for (uint32_t i = 0; i < nblk; i += 2) {
+            if (i + 1 < nblk)
+                i8_load(buf1, wp, afp, i + 1);
+            i8_compute<F, T, S, NF, HALF>(buf0, accf, sp, xp, cp, i);
+            if (i + 1 < nblk) {
+                if (i + 2 < nblk)
+                    i8_load(buf0, wp, afp, i + 2);
+                i8_compute<F, T, S, NF, HALF>(buf1, accf, sp, xp, cp, i + 1);
+            }
         }
+    };
+    if constexpr (FUSED) {
+        extern __shared__ float lds_dyn[];
+        const uint32_t waves = blockDim.x >> 6;
+        const uint32_t gpw = a.ksteps_per_wave / 2;
+        const size_t frag_bytes = size_t(a.ksteps_per_wave) * NF * 1024;
+        char *base = reinterpret_cast<char *>(lds_dyn + size_t(waves) * S * T * NF * 64);
+        int8_t *frag = reinterpret_cast<int8_t *>(base + wave * frag_bytes);
+        float *fxf = reinterpret_cast<float *>(base + waves * frag_bytes) + wave * 4 * NF * gpw;
+        int2 *fcorr = reinterpret_cast<int2 *>(base + waves * frag_bytes +
+                                               size_t(waves) * 4 * NF * gpw * sizeof(float)) +
+                      wave * 4 * NF * gpw;
+        if (nblk > 0)
+            i8_load_w(buf0, wp, 0);
+        wave_prologue<F, NF>(a.x, a.m, a.k, g_begin, gpw, s_begin, frag, fxf, fcorr);
+        __syncthreads();
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            xp[f] = fxf + (4 * f + q) * gpw;
+            cp[f] = fcorr + (4 * f + q) * gpw;
+        }
+        const v4i *lap = reinterpret_cast<const v4i *>(frag) + lane;
+        if (nblk > 0)
+            i8_load_a(buf0, lap, 0);
+        main_loop(lap);
+    } else {
+        if (nblk > 0)
+            i8_load(buf0, wp, ap, 0);
+        main_loop(ap);
     }
 
     uint32_t batch[NF];
@@ -714,35 +835,48 @@ size_t reduce_lds_bytes(int waves, int t)
     return size_t(waves) * S * t * NB * 64 * sizeof(float);
 }
 
-template <Format F, int T, int S, int NF, bool HALF>
+template <Format F, int T, int S, int NF, bool HALF, bool FUSED>
 void launch_i8(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves)
 {
-    const size_t lds = reduce_lds_bytes<S, NF>(waves, T);
+    size_t lds = reduce_lds_bytes<S, NF>(waves, T);
+    if constexpr (FUSED)
+        lds += size_t(waves) * fused_wave_bytes(args.ksteps_per_wave, NF);
     if constexpr (S == 1) {
-        gemv_i8_kernel<F, T, 1, NF, HALF, Epilogue::Single>
+        gemv_i8_kernel<F, T, 1, NF, HALF, Epilogue::Single, FUSED>
             <<<blocks, 64 * waves, lds, stream>>>(args);
     } else if (e == Epilogue::Pair) {
-        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::Pair><<<blocks, 64 * waves, lds, stream>>>(args);
+        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::Pair, FUSED>
+            <<<blocks, 64 * waves, lds, stream>>>(args);
     } else {
-        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::SwigluPair>
+        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::SwigluPair, FUSED>
             <<<blocks, 64 * waves, lds, stream>>>(args);
     }
 }
 
+template <Format F, int T, int S, int NF, bool FUSED>
+void launch_i8_half(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks,
+                    int waves, bool half)
+{
+    if (half)
+        launch_i8<F, T, S, NF, true, FUSED>(stream, args, e, blocks, waves);
+    else
+        launch_i8<F, T, S, NF, false, FUSED>(stream, args, e, blocks, waves);
+}
+
 template <Format F, int T, int S>
 void launch_i8_nf(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves,
-                  int nf, bool half)
+                  int nf, bool half, bool fused)
 {
     if (nf == 1) {
-        if (half)
-            launch_i8<F, T, S, 1, true>(stream, args, e, blocks, waves);
+        if (fused)
+            launch_i8_half<F, T, S, 1, true>(stream, args, e, blocks, waves, half);
         else
-            launch_i8<F, T, S, 1, false>(stream, args, e, blocks, waves);
+            launch_i8_half<F, T, S, 1, false>(stream, args, e, blocks, waves, half);
     } else {
-        if (half)
-            launch_i8<F, T, S, 2, true>(stream, args, e, blocks, waves);
+        if (fused)
+            launch_i8_half<F, T, S, 2, true>(stream, args, e, blocks, waves, half);
         else
-            launch_i8<F, T, S, 2, false>(stream, args, e, blocks, waves);
+            launch_i8_half<F, T, S, 2, false>(stream, args, e, blocks, waves, half);
     }
 }
 
@@ -779,6 +913,9 @@ Scratch carve(void *scratch, uint32_t k_pad)
     return s;
 }
 
+// Largest grid that takes the in-kernel prologue (see gemv_i8_format).
+constexpr unsigned kFusedMaxBlocks = 512;
+
 template <Format F>
 void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
 {
@@ -787,14 +924,29 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t n_tiles = pad_to(call.n, 64) / 16;
     const int nf = call.m <= 4 ? 1 : 2;
     Scratch sc = carve(scratch, k_pad);
-    digits_kernel<F><<<dim3(groups, 4 * nf), 64, 0, stream>>>(
-        call.x, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag), sc.xf, sc.corr);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const uint32_t ksteps = k_pad / 64;
     Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1);
     if (plan.tiles_per_block == 2)
         plan.tiles_per_block = 1;  // T in {1, 4} are instantiated
+    // The in-kernel prologue keeps the fragments of every wave in LDS; it is
+    // used while that (plus the reduction area) fits in 64 KB, so blocks
+    // stay small enough for several to share a CU.
+    const size_t fused_lds =
+        size_t(plan.waves) * (fused_wave_bytes(ksteps / plan.waves, nf) +
+                              size_t(streams) * plan.tiles_per_block * nf * 64 * sizeof(float));
+    // Every block recomputes the prologue for all of K, so a large grid
+    // (the LM head) or many activation rows are faster with the separate
+    // prologue kernel.
+    const unsigned grid = n_tiles / plan.tiles_per_block;
+    const bool fused = !call.separate_prologue && call.m <= 2 && fused_lds <= 64 * 1024 &&
+                       grid <= kFusedMaxBlocks;
+    if (!fused)
+        digits_kernel<F><<<dim3(groups, 4 * nf), 64, 0, stream>>>(
+            call.x, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag), sc.xf, sc.corr);
     MfmaArgs args{};
+    args.x = call.x;
+    args.k = call.k;
     args.afrag = sc.afrag;
     args.xf = sc.xf;
     args.corr = sc.corr;
@@ -812,11 +964,11 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {
         if (plan.tiles_per_block == 4)
-            launch_i8_nf<F, 4, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half);
+            launch_i8_nf<F, 4, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half, fused);
         else
-            launch_i8_nf<F, 1, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half);
+            launch_i8_nf<F, 1, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half, fused);
     } else {
-        launch_i8_nf<F, 1, 2>(stream, args, call.epilogue, blocks, plan.waves, nf, half);
+        launch_i8_nf<F, 1, 2>(stream, args, call.epilogue, blocks, plan.waves, nf, half, fused);
     }
 }
 

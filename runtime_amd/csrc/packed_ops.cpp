@@ -135,6 +135,7 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
         void *scratch = digits_scratch(ctx, gemv_mfma_scratch_bytes(call));
         if (!scratch)
             return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        call.separate_prologue = ctx->kernel_path == 2;
         launch_gemv_mfma(stream, call, scratch);
     } else if (call.m <= 8) {
         launch_gemv_fma(stream, call);

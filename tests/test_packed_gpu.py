@@ -21,9 +21,10 @@ from tests.conftest import assert_close, max_rel_err
 
 pytestmark = pytest.mark.gpu
 SCHEMES = ["ternary", "nf4", "int8"]
-# auto selects the matrix-core decode GEMV for ternary/INT8 at m <= 8;
-# fma forces the FP32-FMA kernels everywhere.
-PATHS = {"auto": 0, "fma": 1}
+# auto selects the matrix-core decode GEMV at m <= 8 (activation prologue
+# inside the GEMV kernel where it fits); fma forces the FP32-FMA kernels
+# everywhere; split runs the matrix-core prologue as a kernel of its own.
+PATHS = {"auto": 0, "fma": 1, "split": 2}
 
 
 def say(*parts):
