@@ -58,6 +58,10 @@ void launch_tile_scales(hipStream_t stream, Format format, const float *scales, 
 
 // Prefill GEMM for larger m: LDS-staged dequantized tiles with FP32 FMA.
 void launch_gemm_fma(hipStream_t stream, const PackedCall &call);
+// Prefill GEMM on matrix cores (binary16 hi/lo activations, exact weight
+// levels, f32 group epilogue).  `scratch` holds gemm_mfma_scratch_bytes.
+size_t gemm_mfma_scratch_bytes(const PackedCall &call);
+void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch);
 
 // out[i] = silu(gate[i]) * up[i], the reference's SwiGLU staging
 // (backend-cpu/src/packed.rs:431-441).

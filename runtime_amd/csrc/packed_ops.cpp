@@ -139,6 +139,11 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
         launch_gemv_mfma(stream, call, scratch);
     } else if (call.m <= 8) {
         launch_gemv_fma(stream, call);
+    } else if (ctx->kernel_path != 1) {
+        void *scratch = digits_scratch(ctx, gemm_mfma_scratch_bytes(call));
+        if (!scratch)
+            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        launch_gemm_mfma(stream, call, scratch);
     } else {
         launch_gemm_fma(stream, call);
     }
