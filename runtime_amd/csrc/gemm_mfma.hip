@@ -15,16 +15,18 @@
 //   power of two, so this equals the reference's scale * dot.  NF4 drops
 //   the lo * lo product, which is below 2^-22 of each term.
 //
-// Tiling.  A 256-lane block computes a 128 (m) x 128 (n) output tile, split
-// over S weight streams of 128 / S columns each.  Four waves own 64 x 64
-// (S = 1) or 64 x 32-per-stream (S = 2) quadrants.  K advances in 32-wide
-// stages: the activation halves and the decoded weight levels are staged
-// through LDS, double buffered.  The load of stage s + 1 runs from global
-// memory while stage s feeds the MFMAs.
+// Tiling.  A 512-lane block computes a 128 (m) x 128 (n) output tile, split
+// over S weight streams of 128 / S columns each.  Eight waves (4 x 2) own
+// 32 x 64 (S = 1) or 32 x 32-per-stream (S = 2) pieces.  K advances in
+// kBK-wide stages: the activation halves and the decoded weight levels are
+// staged through LDS, double buffered.  The load of stage s + 1 runs from
+// global memory while stage s feeds the MFMAs.
 //
 // Grid mapping.  Workgroups are dealt round-robin to the 8 XCDs.  Block b
 // computes tile (b % 8) * (tiles / 8) + b / 8, so each XCD's L2 holds a
 // contiguous run of tiles: neighbouring n-tiles of the same m rows.
+#include <algorithm>
+
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -36,10 +38,16 @@ namespace {
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-constexpr int kBM = 128;     // rows per block tile
-constexpr int kBN = 128;     // columns per block tile (all streams)
-constexpr int kBK = 32;      // k per stage (one MFMA k-block)
-constexpr int kRow = kBK + 8;  // LDS row pitch in halves (80 bytes: conflict-free 16-lane reads)
+#ifndef MFH_GEMM_KBK
+#define MFH_GEMM_KBK 64
+#endif
+constexpr int kThreads = 512;     // 8 waves: 4 (m) x 2 (n)
+constexpr int kBM = 128;          // rows per block tile
+constexpr int kBN = 128;          // columns per block tile (all streams)
+constexpr int kBK = MFH_GEMM_KBK; // k per stage (32 or 64: whole MFMA k-blocks)
+// LDS row pitch in halves: kBK + 8 (80 or 144 bytes) puts the 16 rows read
+// by one lane group on distinct banks.
+constexpr int kRow = kBK + 8;
 
 __constant__ float kLevels[16] = {
     -1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f,
@@ -107,8 +115,10 @@ struct GemmArgs {
     const uint8_t *codes[2];
     const float *scales[2];
     float *out[2];
+    float *partial;       // split-K: [chunk][stream][m][n] raw sums
     uint32_t m, n, k;
     uint32_t tiles_n, tiles;
+    uint32_t chunks;      // K split into `chunks` runs of whole groups
 };
 
 // Level planes of one weight stream: NF4 needs hi and lo.
@@ -145,11 +155,14 @@ __device__ __forceinline__ void decode16(const uint8_t *src, bool live, const _F
 }
 
 template <Format F, int S, Epilogue E>
-__global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g)
+__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
 {
     constexpr int P = Planes<F>::value;
-    constexpr int BNS = kBN / S;      // columns per stream
-    constexpr int TJ = BNS / 32;      // 16-column tiles per stream per wave
+    constexpr int BNS = kBN / S;       // columns per stream
+    constexpr int TI = kBM / 4 / 16;   // 16-row tiles per wave (4 wave rows)
+    constexpr int TJ = BNS / 2 / 16;   // 16-column tiles per stream per wave (2 wave columns)
+    constexpr int KB = kBK / 32;       // MFMA k-blocks per stage
+    constexpr int SPG = 128 / kBK;     // stages per 128-group
     __shared__ _Float16 As[2][2][kBM][kRow];          // [stage][hi, lo][row][k]
     __shared__ _Float16 Bs[2][S][P][BNS][kRow];       // [stage][stream][plane][n][k]
     __shared__ _Float16 nf[2][16];
@@ -164,31 +177,38 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g)
         __syncthreads();
     }
 
-    // XCD-aware tile order.
-    uint32_t tile = blockIdx.x;
-    if (g.tiles % 8 == 0)
-        tile = (blockIdx.x % 8) * (g.tiles / 8) + blockIdx.x / 8;
+    // XCD-aware tile order over (chunk, tile) blocks.
+    const uint32_t blocks = g.tiles * g.chunks;
+    uint32_t block = blockIdx.x;
+    if (blocks % 8 == 0)
+        block = (blockIdx.x % 8) * (blocks / 8) + blockIdx.x / 8;
+    const uint32_t chunk = block / g.tiles, tile = block % g.tiles;
     const uint32_t m0 = (tile / g.tiles_n) * kBM, n0 = (tile % g.tiles_n) * BNS;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
-    const uint32_t groups = g.k / 128, stages = g.k / kBK;
+    const uint32_t groups = g.k / 128;
+    const uint32_t chunk_stages = g.k / kBK / g.chunks;
+    const uint32_t s_begin = chunk * chunk_stages, s_end = s_begin + chunk_stages;
     const size_t row_bytes = size_t(g.k) / weights_per_byte(F);
 
-    // Global -> register staging: A = (row tid / 2, 16 k at (tid & 1) * 16)
-    // of both halves; B = (stream, n, 16 k) per thread.
-    const uint32_t a_row = tid >> 1, a_k = (tid & 1) * 16;
+    // Global -> register staging, 16 consecutive k per thread and operand:
+    // A = (row, k part) of both halves; B = (stream, n, k part).
+    constexpr int APR = kBK / 16;  // A threads per row
+    const uint32_t a_row = tid / APR, a_k = (tid % APR) * 16;
     const bool a_live = m0 + a_row < g.m;
-    const uint32_t b_st = tid / (256 / S), b_local = tid % (256 / S);
-    const uint32_t b_n = b_local >> 1, b_k = (b_local & 1) * 16;
+    const uint32_t b_st = tid / (kThreads / S), b_local = tid % (kThreads / S);
+    const uint32_t b_n = b_local / APR, b_k = (b_local % APR) * 16;
     const bool b_live = n0 + b_n < g.n;
     const uint8_t *b_src = g.codes[b_st] + size_t(b_live ? n0 + b_n : 0) * row_bytes;
+    const _Float16 *a_hi = g.xh + size_t(a_live ? m0 + a_row : 0) * g.k;
+    const _Float16 *a_lo = g.xl + size_t(a_live ? m0 + a_row : 0) * g.k;
 
     v8h a_reg[2][2], b_hi[2], b_lo[2];
     auto fetch = [&](uint32_t s) {
         const uint32_t k0 = s * kBK + a_k;
         if (a_live) {
-            const v8h *ph = reinterpret_cast<const v8h *>(g.xh + size_t(m0 + a_row) * g.k + k0);
-            const v8h *pl = reinterpret_cast<const v8h *>(g.xl + size_t(m0 + a_row) * g.k + k0);
+            const v8h *ph = reinterpret_cast<const v8h *>(a_hi + k0);
+            const v8h *pl = reinterpret_cast<const v8h *>(a_lo + k0);
             a_reg[0][0] = ph[0];
             a_reg[0][1] = ph[1];
             a_reg[1][0] = pl[0];
@@ -214,11 +234,11 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g)
         }
     };
 
-    v4f acc[S][4][TJ], total[S][4][TJ];
+    v4f acc[S][TI][TJ], total[S][TI][TJ];
 #pragma unroll
     for (int st = 0; st < S; ++st)
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < TI; ++i)
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
                 acc[st][i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
@@ -226,57 +246,64 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g)
             }
 
     const int li = lane & 15, lq = lane >> 4;
-    fetch(0);
+    const int row_base = wm * (kBM / 4), col_base = wn * (BNS / 2);
+    fetch(s_begin);
     store(0);
     __syncthreads();
-    for (uint32_t s = 0; s < stages; ++s) {
-        const int buf = s & 1;
-        if (s + 1 < stages)
+    for (uint32_t s = s_begin; s < s_end; ++s) {
+        const int buf = (s - s_begin) & 1;
+        if (s + 1 < s_end)
             fetch(s + 1);
-        v8h ah[4], al[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            ah[i] = *reinterpret_cast<const v8h *>(&As[buf][0][wm * 64 + i * 16 + li][lq * 8]);
-            al[i] = *reinterpret_cast<const v8h *>(&As[buf][1][wm * 64 + i * 16 + li][lq * 8]);
-        }
+        for (int kb = 0; kb < KB; ++kb) {
+            v8h ah[TI], al[TI];
 #pragma unroll
-        for (int st = 0; st < S; ++st)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const int nrow = wn * (BNS / 2) + j * 16 + li;
-                const v8h bh = *reinterpret_cast<const v8h *>(&Bs[buf][st][0][nrow][lq * 8]);
-                v8h bl;
-                if constexpr (P == 2)
-                    bl = *reinterpret_cast<const v8h *>(&Bs[buf][st][1][nrow][lq * 8]);
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    v4f c = acc[st][i][j];
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh, c, 0, 0, 0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh, c, 0, 0, 0);
-                    if constexpr (P == 2)
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl, c, 0, 0, 0);
-                    acc[st][i][j] = c;
-                }
+            for (int i = 0; i < TI; ++i) {
+                const int row = row_base + i * 16 + li;
+                ah[i] = *reinterpret_cast<const v8h *>(&As[buf][0][row][kb * 32 + lq * 8]);
+                al[i] = *reinterpret_cast<const v8h *>(&As[buf][1][row][kb * 32 + lq * 8]);
             }
-        if ((s & 3) == 3) {
-            // Group epilogue: total += group_sum * (2^e[m] * scale[n]).
-            const uint32_t grp = s >> 2;
-            float fx[4][4];
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int st = 0; st < S; ++st)
+#pragma unroll
+                for (int j = 0; j < TJ; ++j) {
+                    const int nrow = col_base + j * 16 + li;
+                    const v8h bh =
+                        *reinterpret_cast<const v8h *>(&Bs[buf][st][0][nrow][kb * 32 + lq * 8]);
+                    v8h bl;
+                    if constexpr (P == 2)
+                        bl = *reinterpret_cast<const v8h *>(
+                            &Bs[buf][st][1][nrow][kb * 32 + lq * 8]);
+#pragma unroll
+                    for (int i = 0; i < TI; ++i) {
+                        v4f c = acc[st][i][j];
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh, c, 0, 0, 0);
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh, c, 0, 0, 0);
+                        if constexpr (P == 2)
+                            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl, c, 0, 0, 0);
+                        acc[st][i][j] = c;
+                    }
+                }
+        }
+        if (s % SPG == SPG - 1) {
+            // Group epilogue: total += group_sum * (2^e[m] * scale[n]).
+            const uint32_t grp = s / SPG;
+            float fx[TI][4];
+#pragma unroll
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const uint32_t mm = m0 + wm * 64 + i * 16 + lq * 4 + r;
+                    const uint32_t mm = m0 + row_base + i * 16 + lq * 4 + r;
                     fx[i][r] = mm < g.m ? g.factor[size_t(mm) * groups + grp] : 0.0f;
                 }
 #pragma unroll
             for (int st = 0; st < S; ++st)
 #pragma unroll
                 for (int j = 0; j < TJ; ++j) {
-                    const uint32_t nn = n0 + wn * (BNS / 2) + j * 16 + li;
+                    const uint32_t nn = n0 + col_base + j * 16 + li;
                     const float sc = nn < g.n ? g.scales[st][size_t(nn) * groups + grp] : 0.0f;
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
+                    for (int i = 0; i < TI; ++i) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             total[st][i][j][r] += acc[st][i][j][r] * (fx[i][r] * sc);
@@ -284,24 +311,32 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g)
                     }
                 }
         }
-        if (s + 1 < stages)
+        if (s + 1 < s_end)
             store(buf ^ 1);
         __syncthreads();
     }
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t mm = m0 + wm * 64 + i * 16 + lq * 4 + r;
+            const uint32_t mm = m0 + row_base + i * 16 + lq * 4 + r;
             if (mm >= g.m)
                 continue;
 #pragma unroll
             for (int j = 0; j < TJ; ++j) {
-                const uint32_t nn = n0 + wn * (BNS / 2) + j * 16 + li;
+                const uint32_t nn = n0 + col_base + j * 16 + li;
                 if (nn >= g.n)
                     continue;
                 const size_t o = size_t(mm) * g.n + nn;
+                if (g.chunks > 1) {
+                    // Raw sums per chunk; splitk_reduce_kernel finishes them.
+                    const size_t plane = size_t(g.m) * g.n;
+#pragma unroll
+                    for (int st = 0; st < S; ++st)
+                        g.partial[(size_t(chunk) * S + st) * plane + o] = total[st][i][j][r];
+                    continue;
+                }
                 if constexpr (E == Epilogue::Single) {
                     g.out[0][o] = total[0][i][j][r];
                 } else if constexpr (E == Epilogue::Pair) {
@@ -314,29 +349,93 @@ __global__ __launch_bounds__(256) void gemm_mfma_kernel(GemmArgs g)
         }
 }
 
+// Split-K epilogue: chunk sums in chunk order, then the operation's epilogue.
+template <int S, Epilogue E>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(float *__restrict__ out0,
+                                                            float *__restrict__ out1,
+                                                            const float *__restrict__ partial,
+                                                            size_t plane, uint32_t chunks)
+{
+    const size_t stride = size_t(gridDim.x) * 256;
+    for (size_t o = size_t(blockIdx.x) * 256 + threadIdx.x; o < plane; o += stride) {
+        float v[S];
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+            float sum = 0.0f;
+            for (uint32_t c = 0; c < chunks; ++c)
+                sum += partial[(size_t(c) * S + st) * plane + o];
+            v[st] = sum;
+        }
+        if constexpr (E == Epilogue::Single) {
+            out0[o] = v[0];
+        } else if constexpr (E == Epilogue::Pair) {
+            out0[o] = v[0];
+            out1[o] = v[S - 1];
+        } else {
+            out0[o] = silu_mul(v[0], v[S - 1]);
+        }
+    }
+}
+
 template <Format F>
 void launch_format(hipStream_t stream, const PackedCall &call, const GemmArgs &args)
 {
-    const unsigned grid = args.tiles;
+    const unsigned grid = args.tiles * args.chunks;
+    const size_t plane = size_t(args.m) * args.n;
+    const unsigned rgrid = unsigned(std::min<size_t>((plane + 255) / 256, 65536));
     switch (call.epilogue) {
     case Epilogue::Single:
-        gemm_mfma_kernel<F, 1, Epilogue::Single><<<grid, 256, 0, stream>>>(args);
+        gemm_mfma_kernel<F, 1, Epilogue::Single><<<grid, kThreads, 0, stream>>>(args);
+        if (args.chunks > 1)
+            splitk_reduce_kernel<1, Epilogue::Single><<<rgrid, 256, 0, stream>>>(
+                args.out[0], args.out[1], args.partial, plane, args.chunks);
         break;
     case Epilogue::Pair:
-        gemm_mfma_kernel<F, 2, Epilogue::Pair><<<grid, 256, 0, stream>>>(args);
+        gemm_mfma_kernel<F, 2, Epilogue::Pair><<<grid, kThreads, 0, stream>>>(args);
+        if (args.chunks > 1)
+            splitk_reduce_kernel<2, Epilogue::Pair><<<rgrid, 256, 0, stream>>>(
+                args.out[0], args.out[1], args.partial, plane, args.chunks);
         break;
     case Epilogue::SwigluPair:
-        gemm_mfma_kernel<F, 2, Epilogue::SwigluPair><<<grid, 256, 0, stream>>>(args);
+        gemm_mfma_kernel<F, 2, Epilogue::SwigluPair><<<grid, kThreads, 0, stream>>>(args);
+        if (args.chunks > 1)
+            splitk_reduce_kernel<2, Epilogue::SwigluPair><<<rgrid, 256, 0, stream>>>(
+                args.out[0], args.out[1], args.partial, plane, args.chunks);
         break;
     }
+}
+
+// K chunks for a grid of `tiles` output tiles: enough to give every CU a
+// block, in whole groups, each chunk at least 4 groups deep.
+uint32_t split_chunks(uint32_t tiles, uint32_t groups)
+{
+    uint32_t chunks = 1;
+    while (tiles * chunks * 2 <= 256 && groups % (chunks * 2) == 0 && groups / (chunks * 2) >= 4)
+        chunks *= 2;
+    return chunks;
+}
+
+}  // namespace
+
+namespace {
+
+uint32_t tiles_of(const PackedCall &call, uint32_t *tiles_n)
+{
+    const int S = call.epilogue == Epilogue::Single ? 1 : 2;
+    *tiles_n = (call.n + kBN / S - 1) / (kBN / S);
+    return *tiles_n * ((call.m + kBM - 1) / kBM);
 }
 
 }  // namespace
 
 size_t gemm_mfma_scratch_bytes(const PackedCall &call)
 {
+    uint32_t tiles_n;
+    const uint32_t chunks = split_chunks(tiles_of(call, &tiles_n), call.k / 128);
+    const int S = call.epilogue == Epilogue::Single ? 1 : 2;
+    const size_t partial = chunks > 1 ? size_t(chunks) * S * call.m * call.n * sizeof(float) : 0;
     return size_t(call.m) * call.k * 2 * sizeof(_Float16) +
-           size_t(call.m) * (call.k / 128) * sizeof(float);
+           size_t(call.m) * (call.k / 128) * sizeof(float) + partial;
 }
 
 void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
@@ -347,7 +446,6 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     _Float16 *xl = xh + size_t(call.m) * call.k;
     float *factor = reinterpret_cast<float *>(xl + size_t(call.m) * call.k);
     split_kernel<<<dim3(groups, call.m), 64, 0, stream>>>(call.x, call.m, call.k, xh, xl, factor);
-    const int S = call.epilogue == Epilogue::Single ? 1 : 2;
     GemmArgs args{};
     args.xh = xh;
     args.xl = xl;
@@ -361,8 +459,9 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     args.m = call.m;
     args.n = call.n;
     args.k = call.k;
-    args.tiles_n = (call.n + kBN / S - 1) / (kBN / S);
-    args.tiles = args.tiles_n * ((call.m + kBM - 1) / kBM);
+    args.tiles = tiles_of(call, &args.tiles_n);
+    args.chunks = split_chunks(args.tiles, groups);
+    args.partial = factor + size_t(call.m) * groups;
     switch (call.format) {
     case Format::Ternary: launch_format<Format::Ternary>(stream, call, args); break;
     case Format::Nf4: launch_format<Format::Nf4>(stream, call, args); break;
