@@ -74,6 +74,60 @@ def cpu_baseline(weights, xs) -> dict:
                       f"{total_bytes / 1e6:.0f} MB algorithmic, {seconds:.1f} s)"}
 
 
+# Prefill GEMM workload: M tokens x (N x K) weights, every format.
+GEMM_MS = [512, 2048]
+GEMM_SHAPES = [(8192, 2048), (2048, 8192)]
+F16_MFMA_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+# MFMA products issued per algorithmic product: activations as binary16
+# hi + lo, NF4 levels as hi + lo without the lo * lo term.
+MFMA_PASSES = {"ternary": 2, "int8": 2, "nf4": 3}
+
+
+def prefill_gemm(backend, reps: int = 5) -> dict:
+    """Packed GEMM at M in {512, 2048} x {8192x2048, 2048x8192} x 3 formats
+    on the matrix-core kernel and on the FP32-FMA kernel (seeded N(0, 0.02)
+    weights, N(0, 1) activations).  Reports algorithmic TFLOP/s (2*M*N*K),
+    its fraction of the dense f16 MFMA peak, and the fraction counting the
+    MFMA products actually issued (hi/lo passes)."""
+    from runtime_amd import convert, hiptime
+    from runtime_amd.backend import WEIGHT
+
+    stream = backend.stream()
+    cases = {}
+    for fmt in FORMATS:
+        for si, (n, k) in enumerate(GEMM_SHAPES):
+            codes, scales16 = convert.packed_weights(n, k, fmt, 0x5EED0101 + si)
+            scales = convert.f16_to_f32(scales16)
+            cb = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
+            sb = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
+            for m in GEMM_MS:
+                xb = backend.upload_f32((m, k), convert.normal((m, k), 0xAC70101 + m))
+                out = backend.allocate_f32((m, n))
+                row = {}
+                for label, path in (("mfma", 0), ("fma", 1)):
+                    previous = backend.set_kernel_path(path)
+                    backend.packed_linear(out, xb, cb, sb)
+                    backend.synchronize()
+                    e0, e1 = hiptime.Event(), hiptime.Event()
+                    e0.record(stream)
+                    for _ in range(reps):
+                        backend.packed_linear(out, xb, cb, sb)
+                    e1.record(stream)
+                    e1.synchronize()
+                    backend.set_kernel_path(previous)
+                    us = e1.elapsed_ms(e0) / reps * 1e3
+                    row[label + "_us"] = round(us, 1)
+                    row[label + "_TFLOPs"] = round(2 * m * n * k / (us / 1e6) / 1e12, 1)
+                row["mfma_util"] = round(row["mfma_TFLOPs"] / F16_MFMA_PEAK_TFLOPS, 4)
+                row["mfma_issued_util"] = round(row["mfma_util"] * MFMA_PASSES[fmt], 4)
+                row["fma_util"] = round(row["fma_TFLOPs"] / FP32_PEAK_TFLOPS, 4)
+                cases[f"{fmt}:M{m}:{n}x{k}"] = row
+    best = max(cases.items(), key=lambda kv: kv[1]["mfma_TFLOPs"])
+    return {"workload": "packed GEMM M{512,2048} x {8192x2048,2048x8192} x {ternary,nf4,int8}",
+            "peak_f16_TFLOPs": F16_MFMA_PEAK_TFLOPS, "best": best[0], "cases": cases}
+
+
 # LFM2 workloads: (config, prompt tokens, greedy decode steps).
 LFM2_WORKLOADS = {
     "350m": ("lfm2_350m", 128, 256),    # all-ternary 350M shape
@@ -184,6 +238,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--copies", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM cases")
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
     ap.add_argument("--profile", choices=["dominant", "copy", "lfm2-350m", "lfm2-1.2b"],
@@ -340,6 +395,9 @@ def main() -> int:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(weights, xs)
     del dev_w, dev_x, dev_out, weights
+    if not args.no_gemm:
+        log("prefill GEMM")
+        result["prefill_gemm"] = prefill_gemm(backend)
     if args.lfm2 != "none":
         result["lfm2"] = {}
         for name in (["350m", "1.2b"] if args.lfm2 == "both" else [args.lfm2]):
