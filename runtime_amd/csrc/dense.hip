@@ -326,6 +326,42 @@ __global__ __launch_bounds__(kBlock) void row_rms_kernel(float *__restrict__ out
 {
     __shared__ float scratch[kBlock / 64];
     const float width_f = float(width);
+    constexpr uint32_t kHeld = 8;
+    if (width <= kHeld * kBlock) {
+        // The row (and the weight) stay in registers: every load is issued
+        // before the reduction, then one pass writes the outputs.
+        for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
+            const uint64_t base = r * width;
+            float v[kHeld], w[kHeld];
+#pragma unroll
+            for (uint32_t i = 0; i < kHeld; ++i) {
+                const uint32_t c = threadIdx.x + i * kBlock;
+                v[i] = c < width ? in[base + c] : 0.0f;
+                w[i] = c < width ? weight[c] : 0.0f;
+                if (ADD)
+                    v[i] = v[i] + (c < width ? right[base + c] : 0.0f);
+            }
+            float squares = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < kHeld; ++i) {
+                const uint32_t c = threadIdx.x + i * kBlock;
+                if (c < width) {
+                    if (ADD)
+                        sum[base + c] = v[i];
+                    squares += v[i] * v[i];
+                }
+            }
+            squares = block_sum(squares, scratch);
+            const float reciprocal = 1.0f / sqrtf(squares / width_f + epsilon);
+#pragma unroll
+            for (uint32_t i = 0; i < kHeld; ++i) {
+                const uint32_t c = threadIdx.x + i * kBlock;
+                if (c < width)
+                    out[base + c] = (v[i] * reciprocal) * w[i];
+            }
+        }
+        return;
+    }
     for (uint64_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const uint64_t base = r * width;
         float squares = 0.0f;
@@ -591,15 +627,28 @@ __global__ __launch_bounds__(kBlock) void gqa_kernel(float *__restrict__ out,
 
 // Split-key attention for few (token, head) pairs (decode): the visible keys
 // of one (token, key/value head) are cut into kSplitKeys-wide ranges, one
-// block per range serving every query head of the group.  A block stores,
+// block per range serving every query head of the group.  The block stages
+// its range's key and value rows in LDS with coalesced loads, then stores,
 // per query head, its range maximum m, its exponent sum l = sum exp(s - m)
 // and the unnormalised sum acc = sum exp(s - m) * v; the combine kernel
 // rescales the ranges to the global maximum.  Scores keep the reference's
 // sequential dot; the softmax normalisation is regrouped (exp(s - m) *
 // exp(m - M) / L for exp(s - M) / L), a reassociation within f32 rounding.
-constexpr int kSplitKeys = 256;
-constexpr uint32_t kSplitMaxGroup = 8;
-constexpr uint32_t kSplitMaxDim = 256;
+constexpr int kSplitKeys = 64;
+// Limits of the split path: its dynamic LDS (below) and the combine
+// kernel's per-range weights.
+constexpr size_t kSplitMaxLds = 64 * 1024;
+constexpr uint32_t kSplitMaxRanges = 8192;
+
+// Dynamic LDS of gqa_split_kernel: q [group][d], keys [kSplitKeys][d + 1]
+// (the pad puts consecutive keys on distinct banks), values
+// [kSplitKeys][d], probabilities [group][kSplitKeys].
+__host__ __device__ inline size_t gqa_split_lds(uint32_t group, uint32_t d)
+{
+    return (size_t(group) * d + size_t(kSplitKeys) * (d + 1) + size_t(kSplitKeys) * d +
+            size_t(group) * kSplitKeys) *
+           sizeof(float);
+}
 
 __global__ __launch_bounds__(kBlock) void gqa_split_kernel(float *__restrict__ partial,
                                                            const float *__restrict__ query,
@@ -607,16 +656,17 @@ __global__ __launch_bounds__(kBlock) void gqa_split_kernel(float *__restrict__ p
                                                            const float *__restrict__ value_cache,
                                                            GqaShape g, uint32_t splits)
 {
-    __shared__ float q[kSplitMaxGroup * kSplitMaxDim];
-    __shared__ float p[kSplitMaxGroup][kSplitKeys];
-    __shared__ float stats[2][kSplitMaxGroup];
-    __shared__ float scratch[kBlock / 64];
+    extern __shared__ float lds[];
+    const uint32_t d = g.head_dim, group = g.group;
+    float *q = lds;
+    float *kl = q + group * d;
+    float *vl = kl + kSplitKeys * (d + 1);
+    float *p = vl + kSplitKeys * d;
 
     const uint32_t split = blockIdx.x % splits;
     const uint64_t pair = blockIdx.x / splits;
     const uint32_t kv_head = uint32_t(pair % g.key_value_heads);
     const uint64_t token = pair / g.key_value_heads;
-    const uint32_t d = g.head_dim, group = g.group;
     const uint64_t kv_width = uint64_t(g.key_value_heads) * d;
     const uint64_t visible = g.initial_len + token + 1;
     const uint64_t begin = uint64_t(split) * kSplitKeys;
@@ -630,69 +680,96 @@ __global__ __launch_bounds__(kBlock) void gqa_split_kernel(float *__restrict__ p
     const float *qrow = query + (token * g.query_heads + head0) * uint64_t(d);
     for (uint32_t i = threadIdx.x; i < group * d; i += kBlock)
         q[i] = qrow[i];
+    const float *keys = key_cache + begin * kv_width + kv_head * uint64_t(d);
+    const float *values = value_cache + begin * kv_width + kv_head * uint64_t(d);
+    for (uint32_t i = threadIdx.x; i < count * d; i += kBlock) {
+        const uint32_t key = i / d, c = i - key * d;
+        kl[key * (d + 1) + c] = keys[key * kv_width + c];
+        vl[i] = values[key * kv_width + c];
+    }
     __syncthreads();
 
-    // Scores: thread j owns key begin + j for every head of the group.
-    const float *keys = key_cache + kv_head * uint64_t(d);
-    if (threadIdx.x < count) {
-        const float *krow = keys + (begin + threadIdx.x) * kv_width;
-        for (uint32_t h = 0; h < group; ++h) {
+    // Scores of (head, key) items: the reference's sequential dot.
+    for (uint32_t i = threadIdx.x; i < group * kSplitKeys; i += kBlock) {
+        const uint32_t h = i / kSplitKeys, key = i % kSplitKeys;
+        if (key < count) {
             const float *qh = q + h * d;
+            const float *kr = kl + key * (d + 1);
             float dot = 0.0f;
             for (uint32_t c = 0; c < d; ++c)
-                dot += qh[c] * krow[c];
-            p[h][threadIdx.x] = dot * g.scale;
-        }
-    }
-    for (uint32_t h = 0; h < group; ++h) {
-        const float s = threadIdx.x < count ? p[h][threadIdx.x] : -__builtin_inff();
-        const float m = block_max(s, scratch);
-        const float e = threadIdx.x < count ? expf(s - m) : 0.0f;
-        if (threadIdx.x < count)
-            p[h][threadIdx.x] = e;
-        const float l = block_sum(e, scratch);
-        if (threadIdx.x == 0) {
-            stats[0][h] = m;
-            stats[1][h] = l;
+                dot += qh[c] * kr[c];
+            p[i] = dot * g.scale;
         }
     }
     __syncthreads();
-    const float *values = value_cache + kv_head * uint64_t(d);
+    // One wave per head (kSplitKeys == 64 keys, one per lane).
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    for (uint32_t h = wave; h < group; h += kBlock / 64) {
+        const float s = lane < count ? p[h * kSplitKeys + lane] : -__builtin_inff();
+        const float m = wave_max(s);
+        const float e = lane < count ? expf(s - m) : 0.0f;
+        p[h * kSplitKeys + lane] = e;
+        const float l = wave_sum(e);
+        if (lane == 0) {
+            out[uint64_t(h) * splits * record] = m;
+            out[uint64_t(h) * splits * record + 1] = l;
+        }
+    }
+    __syncthreads();
     for (uint32_t t = threadIdx.x; t < group * d; t += kBlock) {
         const uint32_t h = t / d, dim = t - h * d;
+        const float *ph = p + h * kSplitKeys;
         float acc = 0.0f;
         for (uint32_t j = 0; j < count; ++j)
-            acc += p[h][j] * values[(begin + j) * kv_width + dim];
+            acc += ph[j] * vl[j * d + dim];
         out[uint64_t(h) * splits * record + 2 + dim] = acc;
-    }
-    if (threadIdx.x < group) {
-        out[uint64_t(threadIdx.x) * splits * record] = stats[0][threadIdx.x];
-        out[uint64_t(threadIdx.x) * splits * record + 1] = stats[1][threadIdx.x];
     }
 }
 
 // One block per (token, query head): out = sum_s acc_s e^(m_s - M) / L with
-// M = max m_s and L = sum l_s e^(m_s - M), ranges in order.  Empty ranges
-// (l = 0) are skipped; a NaN anywhere reaches the output.
+// M = max m_s and L = sum l_s e^(m_s - M).  Empty ranges (l = 0) are
+// skipped; a NaN anywhere reaches the output.  The block's threads split the
+// ranges into kBlock / d interleaved parts, summed part by part at the end.
 __global__ __launch_bounds__(kBlock) void gqa_combine_kernel(float *__restrict__ out,
                                                              const float *__restrict__ partial,
                                                              uint32_t head_dim, uint32_t splits)
 {
+    extern __shared__ float lds[];
+    float *weight = lds;              // [splits] e^(m_s - M), 0 for empty ranges
+    float *part = lds + splits;       // [parts][head_dim]
+    __shared__ float scratch[kBlock / 64];
     const uint64_t record = uint64_t(head_dim) + 2;
     const float *rec = partial + uint64_t(blockIdx.x) * splits * record;
     float maximum = -__builtin_inff();
-    for (uint32_t s = 0; s < splits; ++s)
+    for (uint32_t s = threadIdx.x; s < splits; s += kBlock)
         if (rec[s * record + 1] != 0.0f)
             maximum = fmaxf(maximum, rec[s * record]);
+    maximum = block_max(maximum, scratch);
     float denominator = 0.0f;
-    for (uint32_t s = 0; s < splits; ++s)
-        if (rec[s * record + 1] != 0.0f)
-            denominator += rec[s * record + 1] * expf(rec[s * record] - maximum);
+    for (uint32_t s = threadIdx.x; s < splits; s += kBlock) {
+        // An empty range stores l = 0 and acc = 0: weight 0 drops it.
+        const float l = rec[s * record + 1];
+        const float w = l != 0.0f ? expf(rec[s * record] - maximum) : 0.0f;
+        weight[s] = w;
+        if (l != 0.0f)
+            denominator += l * w;
+    }
+    denominator = block_sum(denominator, scratch);  // also orders the weight stores
+    const uint32_t parts = head_dim <= kBlock ? kBlock / head_dim : 1;
+    const uint32_t part_id = threadIdx.x / head_dim, dim0 = threadIdx.x % head_dim;
+    if (part_id < parts) {
+        for (uint32_t dim = dim0; dim < head_dim; dim += kBlock) {
+            float acc = 0.0f;
+            for (uint32_t s = part_id; s < splits; s += parts)
+                acc += rec[s * record + 2 + dim] * weight[s];
+            part[part_id * head_dim + dim] = acc;
+        }
+    }
+    __syncthreads();
     for (uint32_t dim = threadIdx.x; dim < head_dim; dim += kBlock) {
-        float acc = 0.0f;
-        for (uint32_t s = 0; s < splits; ++s)
-            if (rec[s * record + 1] != 0.0f)
-                acc += rec[s * record + 2 + dim] * expf(rec[s * record] - maximum);
+        float acc = part[dim];
+        for (uint32_t pi = 1; pi < parts; ++pi)
+            acc += part[pi * head_dim + dim];
         out[uint64_t(blockIdx.x) * head_dim + dim] = acc / denominator;
     }
 }
@@ -875,7 +952,8 @@ uint32_t gqa_splits(const GqaShape &g)
     const uint64_t pairs = g.tokens * g.query_heads;
     const uint64_t longest = g.initial_len + g.tokens;
     const uint64_t splits = (longest + kSplitKeys - 1) / kSplitKeys;
-    if (pairs >= 1024 || splits < 2 || g.group > kSplitMaxGroup || g.head_dim > kSplitMaxDim ||
+    if (pairs >= 1024 || splits < 2 || splits > kSplitMaxRanges ||
+        gqa_split_lds(g.group, g.head_dim) > kSplitMaxLds ||
         splits * g.tokens * g.key_value_heads > (uint64_t(1) << 31))
         return 0;
     return uint32_t(splits);
@@ -904,10 +982,12 @@ void launch_gqa(hipStream_t stream, float *out, const float *query, const float 
         return;
     const uint32_t splits = gqa_splits(g);
     if (splits) {
-        gqa_split_kernel<<<unsigned(g.tokens * g.key_value_heads * splits), kBlock, 0, stream>>>(
+        gqa_split_kernel<<<unsigned(g.tokens * g.key_value_heads * splits), kBlock,
+                           gqa_split_lds(g.group, g.head_dim), stream>>>(
             scratch, query, key_cache, value_cache, g, splits);
-        gqa_combine_kernel<<<unsigned(blocks), kBlock, 0, stream>>>(out, scratch, g.head_dim,
-                                                                     splits);
+        const size_t combine_lds = (size_t(splits) + kBlock) * sizeof(float);
+        gqa_combine_kernel<<<unsigned(blocks), kBlock, combine_lds, stream>>>(
+            out, scratch, g.head_dim, splits);
         return;
     }
     const size_t lds = (size_t(g.head_dim) + kKeyChunk + kBlock) * sizeof(float);

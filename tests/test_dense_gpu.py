@@ -239,11 +239,15 @@ GQA_CASES = [
     (2, 3, 8, 4, 2, 96),             # head wider than a wave, two key groups
     (2, 3, 8, 2, 1, 256),
     (2, 3, 8, 2, 2, 320),            # two dimensions per thread
-    # split-key path (few (token, head) pairs over more than 256 keys)
+    # split-key path (few (token, head) pairs over more than 64 keys)
     (4, 700, 1024, 32, 8, 64),
-    (1, 3000, 4096, 6, 2, 128),
+    (1, 3000, 4096, 6, 2, 128),      # LDS too large for the split path
     (1, 600, 1024, 8, 1, 64),
-    (2, 513, 1024, 16, 2, 256),
+    (2, 513, 1024, 16, 2, 256),      # LDS too large for the split path
+    (1, 64, 128, 4, 4, 32),          # two ranges, the last holding one key
+    (1, 200, 256, 16, 8, 64),        # ragged last range
+    (3, 130, 256, 8, 2, 96),         # group of four, 96-wide heads
+    (1, 2500, 2561, 32, 8, 64),      # decode at the end of a 2048-token prefill
 ]
 
 
