@@ -231,15 +231,20 @@ __device__ __forceinline__ float argmax_marker(const Candidate &c)
     return (c.poisoned || c.index == UINT32_MAX) ? __builtin_nanf("") : float(c.index);
 }
 
+// `copy` (may be null) receives the same selectors as `out`.
 __global__ __launch_bounds__(kArgmaxBlock) void argmax_kernel(float *__restrict__ out,
+                                                              float *__restrict__ copy,
                                                               const float *__restrict__ in,
                                                               uint32_t rows, uint32_t width,
                                                               const uint64_t *__restrict__ mask)
 {
     for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
         const Candidate c = scan_range(in + uint64_t(r) * width, 0, width, mask);
-        if (threadIdx.x == 0)
+        if (threadIdx.x == 0) {
             out[r] = argmax_marker(c);
+            if (copy)
+                copy[r] = argmax_marker(c);
+        }
     }
 }
 
@@ -258,15 +263,19 @@ __global__ __launch_bounds__(kArgmaxBlock) void argmax_range_kernel(
 }
 
 __global__ __launch_bounds__(kArgmaxBlock) void argmax_final_kernel(
-    float *__restrict__ out, const Candidate *__restrict__ partial, uint32_t ranges)
+    float *__restrict__ out, float *__restrict__ copy, const Candidate *__restrict__ partial,
+    uint32_t ranges)
 {
     Candidate c{-__builtin_inff(), UINT32_MAX, 0};
     const Candidate *row = partial + uint64_t(blockIdx.x) * ranges;
     for (uint32_t i = threadIdx.x; i < ranges; i += kArgmaxBlock)
         merge(c, row[i].value, row[i].index, row[i].poisoned);
     c = reduce_candidates(c);
-    if (threadIdx.x == 0)
+    if (threadIdx.x == 0) {
         out[blockIdx.x] = argmax_marker(c);
+        if (copy)
+            copy[blockIdx.x] = argmax_marker(c);
+    }
 }
 
 // ---- element-wise ------------------------------------------------------
@@ -682,10 +691,41 @@ __global__ __launch_bounds__(kBlock) void gqa_split_kernel(float *__restrict__ p
         q[i] = qrow[i];
     const float *keys = key_cache + begin * kv_width + kv_head * uint64_t(d);
     const float *values = value_cache + begin * kv_width + kv_head * uint64_t(d);
-    for (uint32_t i = threadIdx.x; i < count * d; i += kBlock) {
-        const uint32_t key = i / d, c = i - key * d;
-        kl[key * (d + 1) + c] = keys[key * kv_width + c];
-        vl[i] = values[key * kv_width + c];
+    if (d % 4 == 0) {
+        // float4 loads, up to kStage per thread issued before any is stored.
+        constexpr uint32_t kStage = 8;
+        const uint32_t quads = count * d / 4;
+        for (uint32_t base = 0; base < quads; base += kStage * kBlock) {
+            float4 kq[kStage], vq[kStage];
+#pragma unroll
+            for (uint32_t u = 0; u < kStage; ++u) {
+                const uint32_t i = base + u * kBlock + threadIdx.x;
+                if (i < quads) {
+                    const uint32_t key = 4 * i / d, c = 4 * i - key * d;
+                    kq[u] = *reinterpret_cast<const float4 *>(keys + key * kv_width + c);
+                    vq[u] = *reinterpret_cast<const float4 *>(values + key * kv_width + c);
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kStage; ++u) {
+                const uint32_t i = base + u * kBlock + threadIdx.x;
+                if (i < quads) {
+                    const uint32_t key = 4 * i / d, c = 4 * i - key * d;
+                    float *kr = kl + key * (d + 1) + c;
+                    kr[0] = kq[u].x;
+                    kr[1] = kq[u].y;
+                    kr[2] = kq[u].z;
+                    kr[3] = kq[u].w;
+                    reinterpret_cast<float4 *>(vl)[i] = vq[u];
+                }
+            }
+        }
+    } else {
+        for (uint32_t i = threadIdx.x; i < count * d; i += kBlock) {
+            const uint32_t key = i / d, c = i - key * d;
+            kl[key * (d + 1) + c] = keys[key * kv_width + c];
+            vl[i] = values[key * kv_width + c];
+        }
     }
     __syncthreads();
 
@@ -864,7 +904,7 @@ size_t argmax_scratch_bytes(uint32_t rows, uint32_t width)
 }
 
 void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
-                   const uint64_t *mask, void *scratch)
+                   const uint64_t *mask, void *scratch, float *copy)
 {
     if (!rows)
         return;
@@ -872,10 +912,11 @@ void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t row
         Candidate *partial = static_cast<Candidate *>(scratch);
         argmax_range_kernel<<<rows * ranges, kArgmaxBlock, 0, stream>>>(partial, in, width,
                                                                        ranges, mask);
-        argmax_final_kernel<<<rows, kArgmaxBlock, 0, stream>>>(out, partial, ranges);
+        argmax_final_kernel<<<rows, kArgmaxBlock, 0, stream>>>(out, copy, partial, ranges);
         return;
     }
-    argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, in, rows, width, mask);
+    argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, copy, in, rows, width,
+                                                                  mask);
 }
 
 void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
@@ -974,7 +1015,7 @@ void launch_gqa(hipStream_t stream, float *out, const float *query, const float 
 {
     const uint64_t kv_width = uint64_t(g.key_value_heads) * g.head_dim;
     const uint64_t appended = g.tokens * kv_width;
-    if (appended)
+    if (appended && key)
         cache_append_kernel<<<grid_for(appended), kBlock, 0, stream>>>(
             key_cache, value_cache, key, value, g.initial_len * kv_width, appended);
     const uint64_t blocks = g.tokens * g.query_heads;

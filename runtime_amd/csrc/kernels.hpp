@@ -25,6 +25,24 @@ enum class Epilogue : int {
     SwigluPair = 2, // out_a = silu(x . a) * (x . b)
 };
 
+// How the matrix-core GEMV's activation prologue forms x as it reads it, so
+// that the producing elementwise step needs no kernel of its own (decode).
+enum class XKind : uint32_t {
+    Plain = 0,   // x = a
+    AddRms = 1,  // s = a + b (b may be null); x = (s * rsqrt(mean(s^2) + eps)) * w
+    Swiglu = 2,  // x = silu(a) * b
+    Conv = 3,    // one token of the gated short convolution (m = 1)
+};
+struct XForm {
+    XKind kind = XKind::Plain;
+    const float *a = nullptr;  // Plain x; AddRms left; Swiglu gate; Conv projection [1, 3k]
+    const float *b = nullptr;  // AddRms right; Swiglu up; Conv history [width - 1, k]
+    const float *w = nullptr;  // AddRms norm weight [k]; Conv kernel [k, width]
+    float *side = nullptr;     // AddRms: s [m, k] (may be null); Conv: next history
+    float epsilon = 0.0f;
+    uint32_t width = 0;        // Conv taps
+};
+
 struct PackedCall {
     Format format = Format::Ternary;
     Epilogue epilogue = Epilogue::Single;
@@ -38,7 +56,18 @@ struct PackedCall {
     // Matrix-core GEMV: run the activation prologue as its own kernel even
     // where the in-kernel one fits (diagnostics).
     bool separate_prologue = false;
+    // Matrix-core GEMV only: a transform other than Plain replaces `x`.
+    XForm xform;
 };
+
+// A matrix-core GEMV (m <= 2; m = 1 for Conv) whose activation prologue
+// applies `xform`, over admitted weights of n rows and width k (the LFM2
+// decode step).  Fails with MFH_UNSUPPORTED where that kernel does not serve
+// the call, before anything is enqueued.
+mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uint32_t m,
+                        uint32_t n, uint32_t k, const mfh_buf *codes_a, const mfh_buf *scales_a,
+                        const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
+                        float *out_b);
 
 // Decode GEMV for m <= 8 on FP32 FMA units.
 void launch_gemv_fma(hipStream_t stream, const PackedCall &call);
@@ -109,8 +138,9 @@ void launch_gather_columns(hipStream_t stream, float *out, const float *in, cons
 // several blocks per row whose candidates take argmax_scratch_bytes bytes of
 // `scratch` (0: none used).
 size_t argmax_scratch_bytes(uint32_t rows, uint32_t width);
+// `copy`, when non-null, receives the selectors too.
 void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
-                   const uint64_t *mask, void *scratch);
+                   const uint64_t *mask, void *scratch, float *copy = nullptr);
 // op 0: left + right, op 1: left * right.
 void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
                    size_t count);
@@ -134,9 +164,10 @@ void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, c
                          const float *key, const float *query_weight, const float *key_weight,
                          const Positions &positions, uint64_t tokens, uint32_t query_heads,
                          uint32_t key_heads, uint32_t head_dim, float theta, float epsilon);
-// Appends the new rows, then attends.  Few (token, head) pairs over long
-// caches take a split-key path whose partials need gqa_scratch_bytes(g)
-// bytes of `scratch` (0: no scratch used).
+// Appends the new rows (unless `key` is null: the caller has already written
+// them at row `initial_len` of both caches), then attends.  Few (token,
+// head) pairs over long caches take a split-key path whose partials need
+// gqa_scratch_bytes(g) bytes of `scratch` (0: no scratch used).
 size_t gqa_scratch_bytes(const GqaShape &g);
 void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
                 const float *value, float *key_cache, float *value_cache, const GqaShape &g,

@@ -7,6 +7,7 @@
 // file adds is buffer management suited to a device: every intermediate of a
 // pass lives in a per-row-count workspace allocated once, so steady-state
 // decode allocates nothing and never waits on the host.
+#include <cmath>
 #include <map>
 #include <memory>
 #include <vector>
@@ -61,7 +62,10 @@ struct Workspace {
 };
 
 struct LayerState {
-    Owned history;           // conv: [conv_width - 1, hidden]
+    // conv: [conv_width - 1, hidden], two copies: the fused decode step reads
+    // one and writes the rolled history into the other.
+    Owned history[2];
+    int current = 0;         // the copy that holds the history
     Owned key, value;        // attention: [max_tokens, kv_width]
     uint64_t length = 0;
 };
@@ -183,6 +187,165 @@ mfh_status ffn(mfl_model *m, const LayerWeights &lw, Workspace &ws, mfh_buf *ffn
     return weight_linear(c, down, ws.hidden.buf, lw.w2);
 }
 
+float *dev(const Owned &o)
+{
+    return static_cast<float *>(o.buf->dev);
+}
+
+const float *dev(const Weight &w)
+{
+    return static_cast<const float *>(w.tensor->dev);
+}
+
+// Whether the one-token step can run fused: every matmul role packed (the
+// K/V and FFN gate/up pairs in one format each), every norm and kernel
+// attached, and the matrix-core GEMV in use (kernel path 0 or 2; with 2 the
+// transforms run in the separate prologue kernels).
+bool fused_decode_ready(const mfl_model *m)
+{
+    if (m->ctx->kernel_path == 1 || !m->embedding.packed() || !m->embedding_norm.tensor)
+        return false;
+    for (uint32_t i = 0; i < m->config.layer_count; ++i) {
+        const LayerWeights &lw = m->layers[i];
+        if (!lw.operator_norm.tensor || !lw.ffn_norm.tensor || !same_packed_format(lw.w1, lw.w3) ||
+            !lw.w2.packed())
+            return false;
+        if (m->kinds[i] == 0) {
+            if (!lw.conv_in.packed() || !lw.conv_out.packed() || !lw.conv_kernel.tensor)
+                return false;
+        } else if (!lw.query.packed() || !same_packed_format(lw.key, lw.value) ||
+                   !lw.output.packed() || !lw.query_norm.tensor || !lw.key_norm.tensor) {
+            return false;
+        }
+    }
+    return true;
+}
+
+// One decode token with the elementwise steps folded into the products'
+// activation prologues (see XForm): per convolution block the in
+// projection (residual add + operator norm), the out projection (the
+// convolution) and the gate/up pair (residual add + FFN norm, with SwiGLU in
+// its epilogue); attention blocks write K and V straight into their cache
+// rows.  Same operations and order as append() on one row; only the f32
+// reduction trees of the norms differ.
+mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_logits)
+{
+    mfh_ctx *c = m->ctx;
+    const mfl_config &cfg = m->config;
+    const uint32_t h = cfg.hidden, inter = cfg.intermediate;
+    const uint32_t kv = uint32_t(m->kv_width);
+    Workspace *ws = nullptr;
+    mfh_status s = workspace(m, 1, &ws);
+    if (s)
+        return s;
+    if ((s = mfh_packed_gather_rows(c, ws->x[0].buf, m->embedding.tensor, m->embedding.scales,
+                                    nullptr, 0, device_ids)))
+        return s;
+    DeviceGuard guard(c->device);
+    float *x = dev(ws->x[0]);
+    float *residual = dev(ws->residual), *down = dev(ws->down), *op = dev(ws->op);
+    // The block input is left + right (layer 0: the embedding row alone).
+    const float *left = x, *right = nullptr;
+    const auto norm_of = [&](const Weight &w, float *side) {
+        XForm t;
+        t.kind = XKind::AddRms;
+        t.a = left;
+        t.b = right;
+        t.w = dev(w);
+        t.side = side;
+        t.epsilon = cfg.block_norm_epsilon;
+        return t;
+    };
+    const uint64_t position = m->length;
+    for (uint32_t index = 0; index < cfg.layer_count; ++index) {
+        const LayerWeights &lw = m->layers[index];
+        LayerState &st = m->state[index];
+        float *block_input_side = right ? x : nullptr;
+        if (m->kinds[index] == 0) {
+            if ((s = packed_xform(c, Epilogue::Single, norm_of(lw.operator_norm, block_input_side),
+                                  1, 3 * h, h, lw.conv_in.tensor, lw.conv_in.scales, nullptr,
+                                  nullptr, dev(ws->projection), nullptr)))
+                return s;
+            XForm conv;
+            conv.kind = XKind::Conv;
+            conv.a = dev(ws->projection);
+            conv.b = dev(st.history[st.current]);
+            conv.w = dev(lw.conv_kernel);
+            conv.side = dev(st.history[1 - st.current]);
+            conv.width = cfg.conv_width;
+            if ((s = packed_xform(c, Epilogue::Single, conv, 1, h, h, lw.conv_out.tensor,
+                                  lw.conv_out.scales, nullptr, nullptr, op, nullptr)))
+                return s;
+            st.current = 1 - st.current;
+        } else {
+            float *key_row = dev(st.key) + position * kv;
+            float *value_row = dev(st.value) + position * kv;
+            if ((s = packed_xform(c, Epilogue::Single, norm_of(lw.operator_norm, block_input_side),
+                                  1, h, h, lw.query.tensor, lw.query.scales, nullptr, nullptr,
+                                  dev(ws->q), nullptr)) ||
+                (s = packed_xform(c, Epilogue::Pair, norm_of(lw.operator_norm, nullptr), 1, kv, h,
+                                  lw.key.tensor, lw.key.scales, lw.value.tensor, lw.value.scales,
+                                  dev(ws->k), value_row)))
+                return s;
+            Positions positions;
+            positions.base = position;
+            launch_qk_norm_rope(c->stream, dev(ws->q_rope), key_row, dev(ws->q), dev(ws->k),
+                                dev(lw.query_norm), dev(lw.key_norm), positions, 1,
+                                cfg.attention_heads, cfg.key_value_heads, cfg.head_dim,
+                                cfg.rope_theta, cfg.block_norm_epsilon);
+            GqaShape g;
+            g.tokens = 1;
+            g.initial_len = st.length;
+            g.query_heads = cfg.attention_heads;
+            g.key_value_heads = cfg.key_value_heads;
+            g.head_dim = cfg.head_dim;
+            g.group = cfg.attention_heads / cfg.key_value_heads;
+            g.scale = 1.0f / std::sqrt(float(cfg.head_dim));
+            float *partials = nullptr;
+            if (const size_t bytes = gqa_scratch_bytes(g)) {
+                partials = static_cast<float *>(work_scratch(c, bytes));
+                if (!partials)
+                    return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+            }
+            launch_gqa(c->stream, dev(ws->attention), dev(ws->q_rope), nullptr, nullptr,
+                       dev(st.key), dev(st.value), g, partials);
+            st.length += 1;
+            XForm plain;
+            plain.a = dev(ws->attention);
+            if ((s = packed_xform(c, Epilogue::Single, plain, 1, h, h, lw.output.tensor,
+                                  lw.output.scales, nullptr, nullptr, op, nullptr)))
+                return s;
+        }
+        // FFN: residual = block input + op, normed into the gate/up pair,
+        // whose epilogue forms silu(gate) * up (the value packed_swiglu_linear
+        // stages) for the down projection.
+        left = right ? x : left;
+        right = op;
+        if ((s = packed_xform(c, Epilogue::SwigluPair, norm_of(lw.ffn_norm, residual), 1, inter,
+                              h, lw.w1.tensor, lw.w1.scales, lw.w3.tensor, lw.w3.scales,
+                              dev(ws->hidden), nullptr)))
+            return s;
+        XForm hidden;
+        hidden.a = dev(ws->hidden);
+        if ((s = packed_xform(c, Epilogue::Single, hidden, 1, h, inter, lw.w2.tensor,
+                              lw.w2.scales, nullptr, nullptr, down, nullptr)))
+            return s;
+        left = residual;
+        right = down;
+    }
+    if (produce_logits) {
+        XForm head = norm_of(m->embedding_norm, nullptr);
+        head.epsilon = cfg.norm_epsilon;
+        if ((s = packed_xform(c, Epilogue::Single, head, 1, cfg.vocab, h, m->embedding.tensor,
+                              m->embedding.scales, nullptr, nullptr, dev(m->logits), nullptr)))
+            return s;
+    }
+    if (hipGetLastError() != hipSuccess)
+        return fail(c, MFH_BACKEND_FAILURE, "decode step launch failed");
+    m->length += 1;
+    return MFH_OK;
+}
+
 // append_tokens (execution.rs:35-540).
 mfh_status append(mfl_model *m, const uint32_t *tokens, size_t count, const mfh_buf *device_ids,
                   bool produce_logits)
@@ -209,6 +372,8 @@ mfh_status append(mfl_model *m, const uint32_t *tokens, size_t count, const mfh_
         return fail(c, MFH_OUT_OF_BOUNDS, "append exceeds configured logical prefix capacity");
     if (!m->embedding.tensor || !m->embedding_norm.tensor)
         return fail(c, MFH_MISSING_REQUIRED_TENSOR, "LFM2 weight role is not attached");
+    if (rows == 1 && device_ids && fused_decode_ready(m))
+        return decode_step(m, device_ids, produce_logits);
 
     Workspace *ws = nullptr, *ws1 = nullptr;
     mfh_status s = workspace(m, rows, &ws);
@@ -242,8 +407,9 @@ mfh_status append(mfl_model *m, const uint32_t *tokens, size_t count, const mfh_
         if (m->kinds[index] == 0) {
             if ((s = weight_linear(c, ws->projection.buf, u, lw.conv_in)) || (s = need(c, lw.conv_kernel)) ||
                 (s = mfh_gated_short_convolution(c, ws->convolved.buf, ws->projection.buf,
-                                                 lw.conv_kernel.tensor, st.history.buf,
-                                                 cfg.hidden, cfg.conv_width)) ||
+                                                 lw.conv_kernel.tensor,
+                                                 st.history[st.current].buf, cfg.hidden,
+                                                 cfg.conv_width)) ||
                 (s = weight_linear(c, ws->op.buf, ws->convolved.buf, lw.conv_out)))
                 return s;
         } else {
@@ -343,7 +509,8 @@ mfh_status mfl_create(mfh_ctx *ctx, const mfl_config *config, mfl_model **out)
     for (uint32_t i = 0; i < c.layer_count && !s; ++i) {
         LayerState &st = m->state[i];
         if (m->kinds[i] == 0) {
-            s = alloc(ctx, st.history, c.conv_width - 1, c.hidden, MFH_CLASS_CACHE, true);
+            for (int h = 0; h < 2 && !s; ++h)
+                s = alloc(ctx, st.history[h], c.conv_width - 1, c.hidden, MFH_CLASS_CACHE, true);
         } else {
             s = alloc(ctx, st.key, c.max_tokens, m->kv_width, MFH_CLASS_CACHE, true);
             if (!s)
@@ -413,9 +580,11 @@ mfh_status mfl_reset(mfl_model *m)
     for (uint32_t i = 0; i < m->config.layer_count; ++i) {
         LayerState &st = m->state[i];
         st.length = 0;
-        if (st.history.buf && st.history.buf->elements)
-            launch_fill_f32(m->ctx->stream, static_cast<float *>(st.history.buf->dev),
-                            st.history.buf->elements, 0.0f);
+        st.current = 0;
+        for (Owned &h : st.history)
+            if (h.buf && h.buf->elements)
+                launch_fill_f32(m->ctx->stream, static_cast<float *>(h.buf->dev),
+                                h.buf->elements, 0.0f);
     }
     m->length = 0;
     return MFH_OK;
@@ -457,13 +626,20 @@ mfh_status mfl_generate(mfl_model *m, uint32_t steps, mfh_buf *ids_out)
     if (m->length + steps > m->config.max_tokens)
         return fail(c, MFH_OUT_OF_BOUNDS, "append exceeds configured logical prefix capacity");
     mark_written(ids_out);
+    const uint32_t vocab = m->config.vocab;
     for (uint32_t i = 0; i < steps; ++i) {
-        if ((s = mfl_sample(m)))
-            return s;
         {
+            // mfl_sample, with the selector also written to ids_out[i].
             DeviceGuard guard(c->device);
-            launch_copy(c->stream, static_cast<float *>(ids_out->dev) + i,
-                        static_cast<const float *>(m->sampled.buf->dev), 1);
+            void *partials = nullptr;
+            if (const size_t bytes = argmax_scratch_bytes(1, vocab)) {
+                partials = work_scratch(c, bytes);
+                if (!partials)
+                    return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+            }
+            launch_argmax(c->stream, static_cast<float *>(m->sampled.buf->dev),
+                          static_cast<const float *>(m->logits.buf->dev), 1, vocab, nullptr,
+                          partials, static_cast<float *>(ids_out->dev) + i);
         }
         if ((s = append(m, nullptr, 0, m->sampled.buf, true)))
             return s;

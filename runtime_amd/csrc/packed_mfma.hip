@@ -38,6 +38,8 @@
 //            canonical code bytes [16s + 4q, +4) of row j = k 32s + 8q + 0..7.
 // Scales: [tile][group][16] as binary16 when every scale is exact in it,
 // otherwise f32.
+#include <type_traits>
+
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
@@ -102,6 +104,99 @@ __device__ __forceinline__ float silu_mul(float gate, float up)
     return (gate * sigmoid) * up;
 }
 
+__device__ __forceinline__ float wave_sum_f(float v)
+{
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+        v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// ---------------------------------------------------------------------------
+// Prologue transforms (XForm).  AddRms needs the row's reciprocal RMS before
+// any group can be formed: 1 / sqrt(sum(s^2) / k + eps), with s = a + b
+// (normalization_rotary.rs:11-83 for the formula).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float add_value(const XForm &t, size_t i)
+{
+    float v = t.a[i];
+    if (t.b)
+        v = v + t.b[i];
+    return v;
+}
+
+__device__ __forceinline__ float rms_reciprocal(float squares, uint32_t k, float epsilon)
+{
+    return 1.0f / sqrtf(squares / float(k) + epsilon);
+}
+
+// Sum `v` over the block (blockDim a multiple of 64), then the reciprocal
+// RMS; `scratch` holds blockDim / 64 floats.  Every thread gets the value.
+__device__ float block_reciprocal(float squares, uint32_t k, float epsilon, float *scratch)
+{
+    squares = wave_sum_f(squares);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0)
+        scratch[threadIdx.x >> 6] = squares;
+    __syncthreads();
+    float total = 0.0f;
+    for (uint32_t w = 0; w < blockDim.x / 64; ++w)
+        total += scratch[w];
+    return rms_reciprocal(total, k, epsilon);
+}
+
+// Element kk of activation row b after the transform of kind K, except
+// that AddRms returns s = a + b unscaled and its norm weight in `weight`
+// (the caller applies (s * reciprocal) * weight once the row's reciprocal is
+// known).  `writer` lanes also store the side output of the element (each
+// element has exactly one writer).
+template <XKind K>
+__device__ __forceinline__ float xform_load(const XForm &t, uint32_t b, uint32_t kk, uint32_t k,
+                                            bool writer, float &weight)
+{
+    const size_t i = size_t(b) * k + kk;
+    if constexpr (K == XKind::Plain) {
+        return t.a[i];
+    } else if constexpr (K == XKind::AddRms) {
+        const float v = add_value(t, i);
+        if (writer && t.side)
+            t.side[i] = v;
+        weight = t.w[kk];
+        return v;
+    } else if constexpr (K == XKind::Swiglu) {
+        return silu_mul(t.a[i], t.b[i]);
+    } else {
+        // One token of the gated short convolution (attention_convolution.rs:
+        // 220-340): u = B * x, taps oldest (history row 0) to current, times C.
+        const uint32_t rows = t.width - 1;
+        const float u = t.a[kk] * t.a[2 * size_t(k) + kk];
+        const float *taps = t.w + size_t(kk) * t.width;
+        float total = 0.0f;
+        for (uint32_t tap = 0; tap < rows; ++tap)
+            total += taps[tap] * t.b[size_t(tap) * k + kk];
+        total += taps[rows] * u;
+        if (writer) {
+            for (uint32_t r = 0; r + 1 < rows; ++r)
+                t.side[size_t(r) * k + kk] = t.b[size_t(r + 1) * k + kk];
+            if (rows)
+                t.side[size_t(rows - 1) * k + kk] = u;
+        }
+        return total * t.a[size_t(k) + kk];
+    }
+}
+
+// The same with the kind chosen at run time (the separate prologue kernels).
+__device__ __forceinline__ float xform_load_any(const XForm &t, uint32_t b, uint32_t kk,
+                                                uint32_t k, bool writer, float &weight)
+{
+    switch (t.kind) {
+    case XKind::Plain: return xform_load<XKind::Plain>(t, b, kk, k, writer, weight);
+    case XKind::AddRms: return xform_load<XKind::AddRms>(t, b, kk, k, writer, weight);
+    case XKind::Swiglu: return xform_load<XKind::Swiglu>(t, b, kk, k, writer, weight);
+    default: return xform_load<XKind::Conv>(t, b, kk, k, writer, weight);
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Activation prologues: one wave per (128-wide group, batch slot).  Slots at
 // or beyond m are written as zeros so every fragment byte is defined.
@@ -112,15 +207,19 @@ struct GroupX {
     bool bad;
 };
 
-// This lane's two raw values of activation group g of batch slot b.
-__device__ __forceinline__ void fetch_group(const float *x, uint32_t b, uint32_t g, uint32_t m,
-                                            uint32_t k, float (&v)[2])
+// This lane's two values of activation group g of batch slot b.
+__device__ __forceinline__ void fetch_group(const XForm &t, uint32_t b, uint32_t g, uint32_t m,
+                                            uint32_t k, float reciprocal, bool writer,
+                                            float (&v)[2])
 {
     const uint32_t lane = threadIdx.x & 63;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint32_t kk = g * 128 + h * 64 + lane;
-        v[h] = (b < m && kk < k) ? x[size_t(b) * k + kk] : 0.0f;
+        float weight = 0.0f;
+        v[h] = (b < m && kk < k) ? xform_load_any(t, b, kk, k, writer, weight) : 0.0f;
+        if (t.kind == XKind::AddRms)
+            v[h] = (v[h] * reciprocal) * weight;
     }
 }
 
@@ -148,14 +247,6 @@ __device__ __forceinline__ GroupX finish_group(const float (&raw)[2])
     return r;
 }
 
-__device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_t g, uint32_t m,
-                                             uint32_t k)
-{
-    float raw[2];
-    fetch_group(x, b, g, m, k, raw);
-    return finish_group(raw);
-}
-
 // Ternary operand fields.  Within a 64-wide kstep, k = 16q + 4e + f puts
 // weight k in bits [2f, 2f+2) of code byte e of lane block q (f = k % 4).
 // The tile layout stores field 3 as (c + 2) mod 4, and the B operand's four
@@ -172,10 +263,15 @@ __device__ __forceinline__ GroupX load_group(const float *x, uint32_t b, uint32_
 // batch slot b; kstep indices are relative to `s0`.  Lane 0 stores the
 // group factor 2^(e - 30) (NaN for a non-finite group) and, for ternary, the
 // correction.
+//
+// Fragment layout: kstep s, fragment b / 4, lane block q, row r at
+// ((s * nfrag + b / 4) * 4 + q) * rp + r (16 bytes each).  rp = 16 is the
+// MFMA lane order; the in-kernel prologue keeps only the live rows
+// (rp = 4 * m, nfrag = 1).
 template <Format F>
 __device__ __forceinline__ void emit_group(const GroupX &gx, uint32_t b, uint32_t g,
-                                           uint32_t nfrag, uint32_t s0, int8_t *afrag,
-                                           float *xf_out, int2 *corr_out)
+                                           uint32_t nfrag, uint32_t rp, uint32_t s0,
+                                           int8_t *afrag, float *xf_out, int2 *corr_out)
 {
     const uint32_t lane = threadIdx.x & 63;
     if (lane == 0)
@@ -206,7 +302,7 @@ __device__ __forceinline__ void emit_group(const GroupX &gx, uint32_t b, uint32_
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             const uint32_t row = 4 * (b % 4) + i;
-            afrag[((size_t(s) * nfrag + b / 4) * 64 + 16 * q + row) * 16 + byte] = int8_t(d[i]);
+            afrag[(((size_t(s) * nfrag + b / 4) * 4 + q) * rp + row) * 16 + byte] = int8_t(d[i]);
         }
     }
     if constexpr (F == Format::Ternary) {
@@ -221,58 +317,132 @@ __device__ __forceinline__ void emit_group(const GroupX &gx, uint32_t b, uint32_
     }
 }
 
-template <Format F>
-__global__ __launch_bounds__(64) void digits_kernel(const float *x, uint32_t m, uint32_t k,
-                                                    uint32_t groups, uint32_t nfrag,
-                                                    int8_t *afrag, float *xf, int2 *corr)
+// The separate prologue kernels: block (x, b) of kPrologueWaves waves forms
+// groups [x * kPrologueWaves, +kPrologueWaves) of batch slot b, one wave per
+// group; slots at or beyond m get zero fragments.  For AddRms the block
+// first reduces the row's squares together.  Every wave writes the side
+// outputs of its own elements.
+constexpr uint32_t kPrologueWaves = 4;
+
+__device__ __forceinline__ GroupX prologue_group(const XForm &t, uint32_t b, uint32_t g,
+                                                 uint32_t m, uint32_t k, float reciprocal)
 {
-    const uint32_t g = blockIdx.x, b = blockIdx.y;
-    emit_group<F>(load_group(x, b, g, m, k), b, g, nfrag, 0, afrag, xf + b * groups + g,
-                  corr + b * groups + g);
+    float raw[2];
+    fetch_group(t, b, g, m, k, reciprocal, true, raw);
+    return finish_group(raw);
 }
 
-// In-kernel prologue of one wave: the fragments of groups [g0, g0 + gpw) for
-// the live batch slots (b < m) into the wave's LDS area `frag`; slots at or
-// beyond m stay zero.  Loads of up to four groups are issued before any is
-// reduced.
-template <Format F, int NF>
-__device__ __forceinline__ void wave_prologue(const float *x, uint32_t m, uint32_t k, uint32_t g0,
-                                              uint32_t gpw, uint32_t s0, int8_t *frag,
-                                              float *fxf, int2 *fcorr)
+__device__ __forceinline__ float prologue_reciprocal(const XForm &t, uint32_t b, uint32_t m,
+                                                     uint32_t k, float *scratch)
 {
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t live = m < 4u * NF ? m : 4u * NF;
-    if (live < 4u * NF) {
-        v4i *zf = reinterpret_cast<v4i *>(frag);
-        for (uint32_t i = lane; i < gpw * 2 * NF * 64; i += 64)
-            zf[i] = v4i{0, 0, 0, 0};
-        for (uint32_t i = lane; i < 4 * NF * gpw; i += 64) {
-            fxf[i] = 0.0f;
-            fcorr[i] = int2{0, 0};
+    if (t.kind != XKind::AddRms || b >= m)  // uniform over the block
+        return 0.0f;
+    float squares = 0.0f;
+#pragma unroll 8
+    for (uint32_t kk = threadIdx.x; kk < k; kk += blockDim.x) {
+        const float v = add_value(t, size_t(b) * k + kk);
+        squares += v * v;
+    }
+    return block_reciprocal(squares, k, t.epsilon, scratch);
+}
+
+template <Format F>
+__global__ __launch_bounds__(64 * kPrologueWaves) void digits_kernel(XForm t, uint32_t m,
+                                                                     uint32_t k, uint32_t groups,
+                                                                     uint32_t nfrag,
+                                                                     int8_t *afrag, float *xf,
+                                                                     int2 *corr)
+{
+    __shared__ float scratch[kPrologueWaves];
+    const uint32_t b = blockIdx.y;
+    const uint32_t g = blockIdx.x * kPrologueWaves + (threadIdx.x >> 6);
+    const float reciprocal = prologue_reciprocal(t, b, m, k, scratch);
+    if (g >= groups)
+        return;
+    emit_group<F>(prologue_group(t, b, g, m, k, reciprocal), b, g, nfrag, 16, 0, afrag,
+                  xf + b * groups + g, corr + b * groups + g);
+}
+
+// The in-kernel prologue (m <= 2).  The block's waves take the 128-groups
+// round robin (wave w: groups w, w + W, ...; at most held_groups(K) each)
+// and load each batch row's values once, into registers.  AddRms reduces the
+// row's squares across the block from those registers, then scales them.
+// Each group is then handed to `emit(b, g, group)`; the fragments land in
+// one block-wide LDS array that every wave reads for its own K range.  The
+// kind is a template parameter so each instantiation holds only its own
+// loads (the convolution's eight loads per value get a smaller budget).
+__host__ __device__ constexpr uint32_t held_groups(XKind kind)
+{
+    return kind == XKind::Conv ? 2 : 8;
+}
+// Each wave forms its groups one after another, so a share above this many
+// costs more latency than the separate prologue kernel's launch.
+constexpr uint32_t kFusedGroupsPerWave = 2;
+
+template <XKind K, typename Emit>
+__device__ __forceinline__ void block_prologue(const XForm &t, uint32_t m, uint32_t k,
+                                               uint32_t groups, float *scratch, Emit emit)
+{
+    constexpr uint32_t kHeld = held_groups(K);
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
+    const bool writer = blockIdx.x == 0;
+    for (uint32_t b = 0; b < m; ++b) {
+        float v[kHeld][2], w[kHeld][2];
+#pragma unroll
+        for (uint32_t i = 0; i < kHeld; ++i) {
+            const uint32_t g = wave + i * waves;
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t kk = g * 128 + h * 64 + lane;
+                w[i][h] = 0.0f;
+                v[i][h] =
+                    (g < groups && kk < k) ? xform_load<K>(t, b, kk, k, writer, w[i][h]) : 0.0f;
+            }
+        }
+        if constexpr (K == XKind::AddRms) {
+            float squares = 0.0f;
+#pragma unroll
+            for (uint32_t i = 0; i < kHeld; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    squares += v[i][h] * v[i][h];
+            const float reciprocal = block_reciprocal(squares, k, t.epsilon, scratch);
+#pragma unroll
+            for (uint32_t i = 0; i < kHeld; ++i)
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                    v[i][h] = (v[i][h] * reciprocal) * w[i][h];
+        }
+        // One emission body, not unrolled: group i is always in v[0], and
+        // the held values shift down a slot per iteration (static indices
+        // keep them in registers).
+#pragma nounroll
+        for (uint32_t i = 0; i < kHeld; ++i) {
+            const uint32_t g = wave + i * waves;
+            if (g >= groups)  // wave-uniform
+                break;
+            emit(b, g, finish_group(v[0]));
+#pragma unroll
+            for (uint32_t j = 0; j + 1 < kHeld; ++j) {
+                v[j][0] = v[j + 1][0];
+                v[j][1] = v[j + 1][1];
+            }
         }
     }
-    constexpr uint32_t kChunk = 4;
-    for (uint32_t b = 0; b < live; ++b)
-        for (uint32_t c0 = 0; c0 < gpw; c0 += kChunk) {
-            float raw[kChunk][2];
-#pragma unroll
-            for (uint32_t c = 0; c < kChunk; ++c)
-                if (c0 + c < gpw)
-                    fetch_group(x, b, g0 + c0 + c, m, k, raw[c]);
-#pragma unroll
-            for (uint32_t c = 0; c < kChunk; ++c)
-                if (c0 + c < gpw)
-                    emit_group<F>(finish_group(raw[c]), b, g0 + c0 + c, NF, s0, frag,
-                                  fxf + b * gpw + c0 + c, fcorr + b * gpw + c0 + c);
-        }
 }
 
-__global__ __launch_bounds__(64) void halves_kernel(const float *x, uint32_t m, uint32_t k,
-                                                    uint32_t groups, _Float16 *afrag, float *xf)
+__global__ __launch_bounds__(64 * kPrologueWaves) void halves_kernel(XForm t, uint32_t m,
+                                                                     uint32_t k, uint32_t groups,
+                                                                     _Float16 *afrag, float *xf)
 {
-    const uint32_t g = blockIdx.x, b = blockIdx.y;
-    const uint32_t lane = threadIdx.x;
-    const GroupX gx = load_group(x, b, g, m, k);
+    __shared__ float scratch[kPrologueWaves];
+    const uint32_t b = blockIdx.y;
+    const uint32_t g = blockIdx.x * kPrologueWaves + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    const float reciprocal = prologue_reciprocal(t, b, m, k, scratch);
+    if (g >= groups)
+        return;
+    const GroupX gx = prologue_group(t, b, g, m, k, reciprocal);
     if (lane == 0)
         xf[b * groups + g] = gx.bad ? __builtin_nanf("") : ldexpf(1.0f, gx.e);
 #pragma unroll
@@ -287,6 +457,51 @@ __global__ __launch_bounds__(64) void halves_kernel(const float *x, uint32_t m, 
         afrag[(size_t(s) * 64 + 16 * q + 2 * b + 1) * 8 + pos] = lo;
     }
 }
+
+// NF4 fragment emission of group g of batch row b into the block-wide
+// fragment array (rp = 2 * m rows per lane block: hi and lo of each row)
+// and its factor 2^e into fxf[b * groups + g].
+__device__ __forceinline__ void emit_halves(const GroupX &gx, uint32_t b, uint32_t g,
+                                            uint32_t rp, uint32_t groups, _Float16 *frag,
+                                            float *fxf)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    if (lane == 0)
+        fxf[b * groups + g] = gx.bad ? __builtin_nanf("") : ldexpf(1.0f, gx.e);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t kk = g * 128 + h * 64 + lane;
+        const float v = gx.bad ? 0.0f : ldexpf(gx.x[h], -gx.e);
+        const _Float16 hi = _Float16(v);
+        const _Float16 lo = _Float16(v - float(hi));
+        const uint32_t s = kk / 32, r = kk % 32;
+        const uint32_t q = r / 8, pos = r % 8;
+        frag[((size_t(s) * 4 + q) * rp + 2 * b) * 8 + pos] = hi;
+        frag[((size_t(s) * 4 + q) * rp + 2 * b + 1) * 8 + pos] = lo;
+    }
+}
+
+// Activation fragment sources of the GEMV main loops: at(s, f, nf) is the
+// 16-byte operand of this lane for kstep s (relative to the wave's first)
+// and fragment f.
+template <typename V>
+struct GlobalFrag {
+    const V *p;  // already offset by the wave's first kstep and the lane
+    __device__ __forceinline__ V at(uint32_t s, int f, int nf) const
+    {
+        return p[(size_t(s) * nf + f) * 64];
+    }
+};
+template <typename V>
+struct LdsFrag {
+    const V *p;       // block fragments + (first kstep * 4 + q) * rp + j
+    uint32_t stride;  // 4 * rp
+    bool live;        // j < rp: lanes of dead rows read zeros
+    __device__ __forceinline__ V at(uint32_t s, int, int) const
+    {
+        return live ? p[size_t(s) * stride] : V{};
+    }
+};
 
 template <bool HALF>
 struct ScaleT;
@@ -309,7 +524,7 @@ struct MfmaArgs {
     const uint8_t *tiles[2];
     const void *scales[2];
     float *out[2];
-    const float *x;  // activations [m, k] (in-kernel prologue)
+    XForm xform;  // activation source of the prologue
     uint32_t m, n, k, k_pad;
     uint32_t ksteps_per_wave;
 };
@@ -387,19 +602,19 @@ __device__ __forceinline__ void i8_load_w(I8Block<F, T, S, NF> &blk,
 }
 
 template <Format F, int T, int S, int NF, typename AP>
-__device__ __forceinline__ void i8_load_a(I8Block<F, T, S, NF> &blk, AP ap, uint32_t index)
+__device__ __forceinline__ void i8_load_a(I8Block<F, T, S, NF> &blk, const AP &ap, uint32_t index)
 {
     using B = I8Block<F, T, S, NF>;
 #pragma unroll
     for (int ks = 0; ks < B::LB; ++ks)
 #pragma unroll
         for (int f = 0; f < NF; ++f)
-            blk.af[ks][f] = ap[((index * B::LB + ks) * NF + f) * 64];
+            blk.af[ks][f] = ap.at(index * B::LB + ks, f, NF);
 }
 
 template <Format F, int T, int S, int NF, typename AP>
 __device__ __forceinline__ void i8_load(I8Block<F, T, S, NF> &blk, const v4u *const (&wp)[S][T],
-                                        AP ap, uint32_t index)
+                                        const AP &ap, uint32_t index)
 {
     i8_load_w(blk, wp, index);
     i8_load_a(blk, ap, index);
@@ -482,18 +697,25 @@ __device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF> &blk,
 }
 
 // Bytes of dynamic LDS past the reduction area that the in-kernel prologue
-// uses per wave: the wave's digit fragments, group factors and corrections.
-__host__ __device__ constexpr size_t fused_wave_bytes(uint32_t ksteps_per_wave, int nf)
+// uses: the live rows (4 per batch row) of the digit fragments of all of K,
+// then 4 slots of group factors and corrections.
+__host__ __device__ constexpr size_t fused_bytes(uint32_t k_pad, uint32_t m)
 {
-    return size_t(ksteps_per_wave) * nf * 1024 + size_t(4 * nf) * (ksteps_per_wave / 2) * 12;
+    return size_t(k_pad) * 4 * m + size_t(4) * (k_pad / 128) * 12;
+}
+// The NF4 kernel's: hi/lo rows (2 per batch row) per 32-wide kstep, then 8
+// slots of group factors.
+__host__ __device__ constexpr size_t fused_bytes_nf4(uint32_t k_pad, uint32_t m)
+{
+    return size_t(k_pad) * 4 * m + size_t(8) * (k_pad / 128) * 4;
 }
 
 // At most 8 waves per block: two per SIMD leaves 256 VGPRs per wave for the
-// double-buffered loop blocks.  With FUSED each wave first computes the
-// digit fragments of its own K range from x into LDS (emit_digits) while its
-// first weights are in flight; otherwise digits_kernel wrote them to global
-// scratch.
-template <Format F, int T, int S, int NF, bool HALF, Epilogue E, bool FUSED>
+// double-buffered loop blocks.  PRO < 0: digits_kernel wrote the activation
+// fragments to global scratch.  Otherwise the block first forms them in LDS
+// with the in-kernel prologue of transform XKind(PRO) (block_prologue) while
+// each wave's first weights are in flight.
+template <Format F, int T, int S, int NF, bool HALF, Epilogue E, int PRO>
 __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
 {
     using B = I8Block<F, T, S, NF>;
@@ -519,7 +741,8 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
             sp[st][t] = reinterpret_cast<const ST *>(a.scales[st]) +
                         (size_t(tile0 + t) * groups + g_begin) * 16 + j;
         }
-    const v4i *ap = reinterpret_cast<const v4i *>(a.afrag) + size_t(s_begin) * NF * 64 + lane;
+    const GlobalFrag<v4i> ap{reinterpret_cast<const v4i *>(a.afrag) + size_t(s_begin) * NF * 64 +
+                             lane};
     const float *xp[NF];
     const int2 *cp[NF];
 #pragma unroll
@@ -550,27 +773,33 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
             }
         }
     };
-    if constexpr (FUSED) {
+    if constexpr (PRO >= 0) {
+        static_assert(NF == 1, "the in-kernel prologue serves m <= 2");
         extern __shared__ float lds_dyn[];
+        __shared__ float rms_scratch[8];
         const uint32_t waves = blockDim.x >> 6;
-        const uint32_t gpw = a.ksteps_per_wave / 2;
-        const size_t frag_bytes = size_t(a.ksteps_per_wave) * NF * 1024;
-        char *base = reinterpret_cast<char *>(lds_dyn + size_t(waves) * S * T * NF * 64);
-        int8_t *frag = reinterpret_cast<int8_t *>(base + wave * frag_bytes);
-        float *fxf = reinterpret_cast<float *>(base + waves * frag_bytes) + wave * 4 * NF * gpw;
-        int2 *fcorr = reinterpret_cast<int2 *>(base + waves * frag_bytes +
-                                               size_t(waves) * 4 * NF * gpw * sizeof(float)) +
-                      wave * 4 * NF * gpw;
+        const uint32_t rp = 4 * a.m;
+        // Fragments: k_pad / 64 ksteps x 4 lane blocks x rp rows x 16 bytes.
+        int8_t *frag = reinterpret_cast<int8_t *>(lds_dyn + size_t(waves) * S * T * NF * 64);
+        float *fxf = reinterpret_cast<float *>(frag + size_t(a.k_pad) * rp);
+        int2 *fcorr = reinterpret_cast<int2 *>(fxf + 4 * groups);
         if (nblk > 0)
             i8_load_w(buf0, wp, 0);
-        wave_prologue<F, NF>(a.x, a.m, a.k, g_begin, gpw, s_begin, frag, fxf, fcorr);
-        __syncthreads();
-#pragma unroll
-        for (int f = 0; f < NF; ++f) {
-            xp[f] = fxf + (4 * f + q) * gpw;
-            cp[f] = fcorr + (4 * f + q) * gpw;
+        for (uint32_t i = a.m * groups + threadIdx.x; i < 4 * groups; i += blockDim.x) {
+            fxf[i] = 0.0f;
+            fcorr[i] = int2{0, 0};
         }
-        const v4i *lap = reinterpret_cast<const v4i *>(frag) + lane;
+        block_prologue<XKind(PRO)>(a.xform, a.m, a.k, groups, rms_scratch,
+                                   [&](uint32_t b, uint32_t g, const GroupX &gx) {
+                                       emit_group<F>(gx, b, g, 1, rp, 0, frag,
+                                                     fxf + b * groups + g, fcorr + b * groups + g);
+                                   });
+        __syncthreads();
+        xp[0] = fxf + q * groups + g_begin;
+        cp[0] = fcorr + q * groups + g_begin;
+        const LdsFrag<v4i> lap{reinterpret_cast<const v4i *>(frag) + (size_t(s_begin) * 4 + q) * rp +
+                                   j,
+                               4 * rp, j < rp};
         if (nblk > 0)
             i8_load_a(buf0, lap, 0);
         main_loop(lap);
@@ -601,9 +830,9 @@ struct Nf4Block {
     v8h af[4];
 };
 
-template <int T, int S>
+template <int T, int S, typename AP>
 __device__ __forceinline__ void nf4_load(Nf4Block<T, S> &blk, const v4u *const (&wp)[S][T],
-                                         const v8h *ap, uint32_t index)
+                                         const AP &ap, uint32_t index)
 {
 #pragma unroll
     for (int st = 0; st < S; ++st)
@@ -612,7 +841,7 @@ __device__ __forceinline__ void nf4_load(Nf4Block<T, S> &blk, const v4u *const (
             blk.w[st][t] = wp[st][t][index * 64];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-        blk.af[ks] = ap[(index * 4 + ks) * 64];
+        blk.af[ks] = ap.at(index * 4 + ks, 0, 1);
 }
 
 template <int T, int S, bool HALF>
@@ -664,7 +893,7 @@ __device__ __forceinline__ void nf4_compute(const Nf4Block<T, S> &blk, float (&a
         }
 }
 
-template <int T, int S, bool HALF, Epilogue E>
+template <int T, int S, bool HALF, Epilogue E, int PRO>
 __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
 {
     using ST = typename ScaleT<HALF>::type;
@@ -706,7 +935,6 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
             sp[st][t] = reinterpret_cast<const ST *>(a.scales[st]) +
                         (size_t(tile0 + t) * groups + g_begin) * 16 + j;
         }
-    const v8h *ap = reinterpret_cast<const v8h *>(a.afrag) + size_t(s_begin) * 64 + lane;
     const float *xp[2] = {a.xf + (2 * q) * groups + g_begin, a.xf + (2 * q + 1) * groups + g_begin};
 
     float accf[S][T][2];
@@ -717,17 +945,43 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
             accf[st][t][0] = accf[st][t][1] = 0.0f;
 
     Nf4Block<T, S> buf0, buf1;
-    if (nblk > 0)
-        nf4_load(buf0, wp, ap, 0);
-    for (uint32_t i = 0; i < nblk; i += 2) {
-        if (i + 1 < nblk)
-            nf4_load(buf1, wp, ap, i + 1);
-        nf4_compute<T, S, HALF>(buf0, accf, sp, xp, lut, i);
-        if (i + 1 < nblk) {
-            if (i + 2 < nblk)
-                nf4_load(buf0, wp, ap, i + 2);
-            nf4_compute<T, S, HALF>(buf1, accf, sp, xp, lut, i + 1);
+    auto main_loop = [&](const auto &ap) {
+        if (nblk > 0)
+            nf4_load(buf0, wp, ap, 0);
+        for (uint32_t i = 0; i < nblk; i += 2) {
+            if (i + 1 < nblk)
+                nf4_load(buf1, wp, ap, i + 1);
+            nf4_compute<T, S, HALF>(buf0, accf, sp, xp, lut, i);
+            if (i + 1 < nblk) {
+                if (i + 2 < nblk)
+                    nf4_load(buf0, wp, ap, i + 2);
+                nf4_compute<T, S, HALF>(buf1, accf, sp, xp, lut, i + 1);
+            }
         }
+    };
+    if constexpr (PRO >= 0) {
+        extern __shared__ float lds_dyn[];
+        __shared__ float rms_scratch[8];
+        const uint32_t waves = blockDim.x >> 6;
+        const uint32_t rp = 2 * a.m;
+        _Float16 *frag = reinterpret_cast<_Float16 *>(lds_dyn + size_t(waves) * S * T * 2 * 64);
+        // Fragments: k_pad / 32 ksteps x 4 lane blocks x rp rows x 8 halves.
+        float *fxf = reinterpret_cast<float *>(frag + size_t(a.k_pad) * rp);
+        for (uint32_t i = a.m * groups + threadIdx.x; i < 8 * groups; i += blockDim.x)
+            fxf[i] = 0.0f;
+        block_prologue<XKind(PRO)>(a.xform, a.m, a.k, groups, rms_scratch,
+                                   [&](uint32_t b, uint32_t g, const GroupX &gx) {
+                                       emit_halves(gx, b, g, rp, groups, frag, fxf);
+                                   });
+        __syncthreads();
+        xp[0] = fxf + (2 * q) * groups + g_begin;
+        xp[1] = fxf + (2 * q + 1) * groups + g_begin;
+        main_loop(LdsFrag<v8h>{reinterpret_cast<const v8h *>(frag) + (size_t(s_begin) * 4 + q) * rp +
+                                   j,
+                               4 * rp, j < rp});
+    } else {
+        main_loop(GlobalFrag<v8h>{reinterpret_cast<const v8h *>(a.afrag) + size_t(s_begin) * 64 +
+                                  lane});
     }
     const uint32_t batch[2] = {2 * q, 2 * q + 1};
     reduce_and_store<S, T, 2, E>(a, accf, batch, tile0, j);
@@ -813,17 +1067,20 @@ struct Plan {
 
 // Tiles per block T and waves per block W (which split K).  Prefer the widest
 // T that still yields >= 2048 waves; each wave covers whole loop blocks.
-Plan plan_for(uint32_t n_tiles, uint32_t ksteps, uint32_t lb, int max_t)
+// `wide` tries 8 waves before 4, which halves each wave's share of the
+// in-kernel prologue (used when the narrower plan's share is too large).
+Plan plan_for(uint32_t n_tiles, uint32_t ksteps, uint32_t lb, int max_t, bool wide)
 {
     auto fits = [&](uint32_t w) { return ksteps % (w * lb) == 0; };
+    const int order[2] = {wide ? 8 : 4, wide ? 4 : 8};
     for (int t : {4, 2, 1}) {
         if (t > max_t || n_tiles % t)
             continue;
-        for (int w : {4, 8})
+        for (int w : order)
             if (fits(w) && uint64_t(n_tiles / t) * w >= 2048)
                 return Plan{t, w};
     }
-    for (int w : {8, 4, 2, 1})
+    for (int w : {8, 6, 4, 3, 2, 1})
         if (fits(w))
             return Plan{1, w};
     return Plan{1, 1};
@@ -835,62 +1092,126 @@ size_t reduce_lds_bytes(int waves, int t)
     return size_t(waves) * S * t * NB * 64 * sizeof(float);
 }
 
-template <Format F, int T, int S, int NF, bool HALF, bool FUSED>
-void launch_i8(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves)
+// Kernel instantiations by prologue: pro < 0 is the separate prologue
+// kernel, otherwise the in-kernel one with that XKind.  Single products
+// serve every kind, the two-stream epilogues the plain and norm prologues
+// (fused_kind_served).
+bool fused_kind_served(Epilogue e, XKind kind)
 {
-    size_t lds = reduce_lds_bytes<S, NF>(waves, T);
-    if constexpr (FUSED)
-        lds += size_t(waves) * fused_wave_bytes(args.ksteps_per_wave, NF);
-    if constexpr (S == 1) {
-        gemv_i8_kernel<F, T, 1, NF, HALF, Epilogue::Single, FUSED>
-            <<<blocks, 64 * waves, lds, stream>>>(args);
-    } else if (e == Epilogue::Pair) {
-        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::Pair, FUSED>
-            <<<blocks, 64 * waves, lds, stream>>>(args);
-    } else {
-        gemv_i8_kernel<F, T, 2, NF, HALF, Epilogue::SwigluPair, FUSED>
-            <<<blocks, 64 * waves, lds, stream>>>(args);
-    }
+    return e == Epilogue::Single || kind == XKind::Plain || kind == XKind::AddRms;
 }
 
-template <Format F, int T, int S, int NF, bool FUSED>
-void launch_i8_half(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks,
-                    int waves, bool half)
+template <Format F, int T, int S, int NF, bool HALF, Epilogue E, int PRO>
+void launch_i8_kernel(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves)
 {
-    if (half)
-        launch_i8<F, T, S, NF, true, FUSED>(stream, args, e, blocks, waves);
+    size_t lds = reduce_lds_bytes<S, NF>(waves, T);
+    if constexpr (PRO >= 0)
+        lds += fused_bytes(args.k_pad, args.m);
+    gemv_i8_kernel<F, T, S, NF, HALF, E, PRO><<<blocks, 64 * waves, lds, stream>>>(args);
+}
+
+template <Format F, int T, int S, int NF, bool HALF, Epilogue E>
+void launch_i8_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves, int pro)
+{
+    if constexpr (NF == 1) {
+        switch (pro) {
+        case int(XKind::Plain):
+            return launch_i8_kernel<F, T, S, NF, HALF, E, 0>(stream, args, blocks, waves);
+        case int(XKind::AddRms):
+            return launch_i8_kernel<F, T, S, NF, HALF, E, 1>(stream, args, blocks, waves);
+        case int(XKind::Swiglu):
+            if constexpr (E == Epilogue::Single)
+                return launch_i8_kernel<F, T, S, NF, HALF, E, 2>(stream, args, blocks, waves);
+            break;
+        case int(XKind::Conv):
+            if constexpr (E == Epilogue::Single)
+                return launch_i8_kernel<F, T, S, NF, HALF, E, 3>(stream, args, blocks, waves);
+            break;
+        default:
+            break;
+        }
+    }
+    launch_i8_kernel<F, T, S, NF, HALF, E, -1>(stream, args, blocks, waves);
+}
+
+template <Format F, int T, int S, int NF, bool HALF>
+void launch_i8(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves,
+               int pro)
+{
+    if constexpr (S == 1)
+        launch_i8_pro<F, T, 1, NF, HALF, Epilogue::Single>(stream, args, blocks, waves, pro);
+    else if (e == Epilogue::Pair)
+        launch_i8_pro<F, T, 2, NF, HALF, Epilogue::Pair>(stream, args, blocks, waves, pro);
     else
-        launch_i8<F, T, S, NF, false, FUSED>(stream, args, e, blocks, waves);
+        launch_i8_pro<F, T, 2, NF, HALF, Epilogue::SwigluPair>(stream, args, blocks, waves, pro);
 }
 
 template <Format F, int T, int S>
 void launch_i8_nf(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves,
-                  int nf, bool half, bool fused)
+                  int nf, bool half, int pro)
 {
     if (nf == 1) {
-        if (fused)
-            launch_i8_half<F, T, S, 1, true>(stream, args, e, blocks, waves, half);
+        if (half)
+            launch_i8<F, T, S, 1, true>(stream, args, e, blocks, waves, pro);
         else
-            launch_i8_half<F, T, S, 1, false>(stream, args, e, blocks, waves, half);
+            launch_i8<F, T, S, 1, false>(stream, args, e, blocks, waves, pro);
     } else {
-        if (fused)
-            launch_i8_half<F, T, S, 2, true>(stream, args, e, blocks, waves, half);
+        // The in-kernel prologue serves m <= 2 (one fragment) only.
+        if (half)
+            launch_i8<F, T, S, 2, true>(stream, args, e, blocks, waves, -1);
         else
-            launch_i8_half<F, T, S, 2, false>(stream, args, e, blocks, waves, half);
+            launch_i8<F, T, S, 2, false>(stream, args, e, blocks, waves, -1);
     }
 }
 
-template <int T, int S, bool HALF>
-void launch_nf4(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks, int waves)
+template <int T, int S, bool HALF, Epilogue E, int PRO>
+void launch_nf4_kernel(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves)
 {
-    const size_t lds = reduce_lds_bytes<S, 2>(waves, T);
-    if constexpr (S == 1) {
-        gemv_nf4_kernel<T, 1, HALF, Epilogue::Single><<<blocks, 64 * waves, lds, stream>>>(args);
-    } else if (e == Epilogue::Pair) {
-        gemv_nf4_kernel<T, 2, HALF, Epilogue::Pair><<<blocks, 64 * waves, lds, stream>>>(args);
-    } else {
-        gemv_nf4_kernel<T, 2, HALF, Epilogue::SwigluPair><<<blocks, 64 * waves, lds, stream>>>(args);
+    size_t lds = reduce_lds_bytes<S, 2>(waves, T);
+    if constexpr (PRO >= 0)
+        lds += fused_bytes_nf4(args.k_pad, args.m);
+    gemv_nf4_kernel<T, S, HALF, E, PRO><<<blocks, 64 * waves, lds, stream>>>(args);
+}
+
+template <int T, int S, bool HALF, Epilogue E>
+void launch_nf4_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves, int pro)
+{
+    switch (pro) {
+    case int(XKind::Plain):
+        return launch_nf4_kernel<T, S, HALF, E, 0>(stream, args, blocks, waves);
+    case int(XKind::AddRms):
+        return launch_nf4_kernel<T, S, HALF, E, 1>(stream, args, blocks, waves);
+    case int(XKind::Swiglu):
+        if constexpr (E == Epilogue::Single)
+            return launch_nf4_kernel<T, S, HALF, E, 2>(stream, args, blocks, waves);
+        break;
+    case int(XKind::Conv):
+        if constexpr (E == Epilogue::Single)
+            return launch_nf4_kernel<T, S, HALF, E, 3>(stream, args, blocks, waves);
+        break;
+    default:
+        break;
     }
+    launch_nf4_kernel<T, S, HALF, E, -1>(stream, args, blocks, waves);
+}
+
+template <int T, int S>
+void launch_nf4_variant(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned blocks,
+                        int waves, bool half, int pro)
+{
+    auto go = [&](auto half_tag) {
+        constexpr bool H = decltype(half_tag)::value;
+        if constexpr (S == 1)
+            launch_nf4_pro<T, 1, H, Epilogue::Single>(stream, args, blocks, waves, pro);
+        else if (e == Epilogue::Pair)
+            launch_nf4_pro<T, 2, H, Epilogue::Pair>(stream, args, blocks, waves, pro);
+        else
+            launch_nf4_pro<T, 2, H, Epilogue::SwigluPair>(stream, args, blocks, waves, pro);
+    };
+    if (half)
+        go(std::true_type{});
+    else
+        go(std::false_type{});
 }
 
 struct Scratch {
@@ -926,26 +1247,41 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     Scratch sc = carve(scratch, k_pad);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const uint32_t ksteps = k_pad / 64;
-    Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1);
-    if (plan.tiles_per_block == 2)
-        plan.tiles_per_block = 1;  // T in {1, 4} are instantiated
-    // The in-kernel prologue keeps the fragments of every wave in LDS; it is
-    // used while that (plus the reduction area) fits in 64 KB, so blocks
-    // stay small enough for several to share a CU.
-    const size_t fused_lds =
-        size_t(plan.waves) * (fused_wave_bytes(ksteps / plan.waves, nf) +
-                              size_t(streams) * plan.tiles_per_block * nf * 64 * sizeof(float));
-    // Every block recomputes the prologue for all of K, so a large grid
-    // (the LM head) or many activation rows are faster with the separate
-    // prologue kernel.
-    const unsigned grid = n_tiles / plan.tiles_per_block;
-    const bool fused = !call.separate_prologue && call.m <= 2 && fused_lds <= 64 * 1024 &&
-                       grid <= kFusedMaxBlocks;
+    XForm xform = call.xform;
+    if (xform.kind == XKind::Plain)
+        xform.a = call.x;
+    // The in-kernel prologue keeps the live fragment rows of all of K in
+    // LDS; it is used while that (plus the reduction area) fits in 64 KB, so
+    // blocks stay small enough for several to share a CU.  Every block
+    // recomputes the prologue, so a large grid (the LM head) or many
+    // activation rows are faster with the separate prologue kernel, and so
+    // is a wave share above kFusedGroupsPerWave groups.
+    auto tiles_of = [](Plan p) { return p.tiles_per_block == 4 ? 4 : 1; };  // T in {1, 4}
+    auto fusable = [&](Plan p) {
+        const int t = tiles_of(p);
+        const size_t lds = fused_bytes(k_pad, call.m) +
+                           size_t(p.waves) * streams * t * nf * 64 * sizeof(float);
+        const uint32_t share = (groups + p.waves - 1) / p.waves;
+        return !call.separate_prologue && call.m <= 2 && lds <= 64 * 1024 &&
+               n_tiles / t <= kFusedMaxBlocks && share <= kFusedGroupsPerWave &&
+               share <= held_groups(xform.kind) && fused_kind_served(call.epilogue, xform.kind);
+    };
+    Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1, false);
+    if (!fusable(plan)) {
+        const Plan wide = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1, true);
+        if (fusable(wide))
+            plan = wide;
+    }
+    plan.tiles_per_block = tiles_of(plan);
+    const bool fused = fusable(plan);
+    const int pro = fused ? int(xform.kind) : -1;
     if (!fused)
-        digits_kernel<F><<<dim3(groups, 4 * nf), 64, 0, stream>>>(
-            call.x, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag), sc.xf, sc.corr);
+        digits_kernel<F>
+            <<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 4 * nf), 64 * kPrologueWaves,
+               0, stream>>>(xform, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag),
+                            sc.xf, sc.corr);
     MfmaArgs args{};
-    args.x = call.x;
+    args.xform = xform;
     args.k = call.k;
     args.afrag = sc.afrag;
     args.xf = sc.xf;
@@ -964,11 +1300,11 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {
         if (plan.tiles_per_block == 4)
-            launch_i8_nf<F, 4, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half, fused);
+            launch_i8_nf<F, 4, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half, pro);
         else
-            launch_i8_nf<F, 1, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half, fused);
+            launch_i8_nf<F, 1, 1>(stream, args, call.epilogue, blocks, plan.waves, nf, half, pro);
     } else {
-        launch_i8_nf<F, 1, 2>(stream, args, call.epilogue, blocks, plan.waves, nf, half, fused);
+        launch_i8_nf<F, 1, 2>(stream, args, call.epilogue, blocks, plan.waves, nf, half, pro);
     }
 }
 
@@ -978,12 +1314,35 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = pad_to(call.n, 64) / 16;
     Scratch sc = carve(scratch, k_pad);
-    halves_kernel<<<dim3(groups, 8), 64, 0, stream>>>(call.x, call.m, call.k, groups,
-                                                      static_cast<_Float16 *>(sc.afrag), sc.xf);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const uint32_t ksteps = k_pad / 32;
-    Plan plan = plan_for(n_tiles, ksteps, 4, streams == 1 ? 2 : 1);
+    XForm xform = call.xform;
+    if (xform.kind == XKind::Plain)
+        xform.a = call.x;
+    // Same rule as the integer kernels (gemv_i8_format).
+    auto fusable = [&](Plan p) {
+        const size_t lds = fused_bytes_nf4(k_pad, call.m) +
+                           size_t(p.waves) * streams * p.tiles_per_block * 2 * 64 * sizeof(float);
+        const uint32_t share = (groups + p.waves - 1) / p.waves;
+        return !call.separate_prologue && call.m <= 2 && lds <= 64 * 1024 &&
+               n_tiles / p.tiles_per_block <= kFusedMaxBlocks && share <= kFusedGroupsPerWave &&
+               share <= held_groups(xform.kind) && fused_kind_served(call.epilogue, xform.kind);
+    };
+    Plan plan = plan_for(n_tiles, ksteps, 4, streams == 1 ? 2 : 1, false);
+    if (!fusable(plan)) {
+        const Plan wide = plan_for(n_tiles, ksteps, 4, streams == 1 ? 2 : 1, true);
+        if (fusable(wide))
+            plan = wide;
+    }
+    const bool fused = fusable(plan);
+    const int pro = fused ? int(xform.kind) : -1;
+    if (!fused)
+        halves_kernel<<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 8),
+                        64 * kPrologueWaves, 0, stream>>>(xform, call.m, call.k, groups,
+                                                          static_cast<_Float16 *>(sc.afrag), sc.xf);
     MfmaArgs args{};
+    args.xform = xform;
+    args.k = call.k;
     args.afrag = sc.afrag;
     args.xf = sc.xf;
     args.tiles[0] = call.a.tiles;
@@ -999,22 +1358,12 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const unsigned blocks = n_tiles / plan.tiles_per_block;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {
-        if (plan.tiles_per_block == 2) {
-            if (half)
-                launch_nf4<2, 1, true>(stream, args, call.epilogue, blocks, plan.waves);
-            else
-                launch_nf4<2, 1, false>(stream, args, call.epilogue, blocks, plan.waves);
-        } else {
-            if (half)
-                launch_nf4<1, 1, true>(stream, args, call.epilogue, blocks, plan.waves);
-            else
-                launch_nf4<1, 1, false>(stream, args, call.epilogue, blocks, plan.waves);
-        }
-    } else {
-        if (half)
-            launch_nf4<1, 2, true>(stream, args, call.epilogue, blocks, plan.waves);
+        if (plan.tiles_per_block == 2)
+            launch_nf4_variant<2, 1>(stream, args, call.epilogue, blocks, plan.waves, half, pro);
         else
-            launch_nf4<1, 2, false>(stream, args, call.epilogue, blocks, plan.waves);
+            launch_nf4_variant<1, 1>(stream, args, call.epilogue, blocks, plan.waves, half, pro);
+    } else {
+        launch_nf4_variant<1, 2>(stream, args, call.epilogue, blocks, plan.waves, half, pro);
     }
 }
 

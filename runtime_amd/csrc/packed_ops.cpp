@@ -153,6 +153,61 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
 }
 
 }  // namespace
+
+mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uint32_t m,
+                        uint32_t n, uint32_t k, const mfh_buf *codes_a, const mfh_buf *scales_a,
+                        const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
+                        float *out_b)
+{
+    Packed p;
+    mfh_status s = check_packed(ctx, codes_a, scales_a, &p);
+    if (s)
+        return s;
+    if (codes_b) {
+        Packed q;
+        if ((s = check_packed(ctx, codes_b, scales_b, &q)))
+            return s;
+        if (q.format != p.format || q.rows != p.rows || q.inner != p.inner)
+            return fail(ctx, MFH_INVALID_SHAPE,
+                        "packed linear pair requires equal weight and output shapes");
+    }
+    if (p.rows != n || p.inner != k)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
+    // Every operand the transform reads must be present (the kernels do not
+    // check): a, plus b for SwiGLU, w for the norm, and for the convolution
+    // its kernel, the rolled history output and (width > 1) the history.
+    bool operands = out_a && xform.a && (epilogue != Epilogue::Pair || out_b);
+    switch (xform.kind) {
+    case XKind::Plain: break;
+    case XKind::AddRms: operands = operands && xform.w; break;
+    case XKind::Swiglu: operands = operands && xform.b; break;
+    case XKind::Conv:
+        operands = operands && xform.w && xform.side && xform.width > 0 &&
+                   (xform.width == 1 || xform.b);
+        break;
+    }
+    if (!operands)
+        return fail(ctx, MFH_INVALID_ARGUMENT, "fused decode product is missing an operand");
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = epilogue;
+    call.m = m;
+    call.n = n;
+    call.k = k;
+    call.a = stream_of(codes_a, scales_a);
+    if (codes_b)
+        call.b = stream_of(codes_b, scales_b);
+    call.out_a = out_a;
+    call.out_b = out_b;
+    call.xform = xform;
+    if (xform.kind == XKind::Plain)
+        call.x = xform.a;  // the GEMV reads a Plain source from call.x
+    if (!use_mfma_gemv(ctx, call) || m == 0 || m > 2 || (xform.kind == XKind::Conv && m != 1))
+        return fail(ctx, MFH_UNSUPPORTED, "fused decode product needs the matrix-core GEMV");
+    DeviceGuard guard(ctx->device);
+    return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
+}
+
 }  // namespace mfh
 
 using namespace mfh;
@@ -347,6 +402,21 @@ mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf
         return fail(ctx, MFH_OVERFLOW, "packed SwiGLU row count exceeds the kernel index range");
     DeviceGuard guard(ctx->device);
     mark_written(output);
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = Epilogue::Single;
+    call.m = uint32_t(gate->dims[0]);
+    call.n = p.rows;
+    call.k = p.inner;
+    call.a = stream_of(codes, scales);
+    call.out_a = static_cast<float *>(output->dev);
+    if (use_mfma_gemv(ctx, call)) {
+        // The GEMV's activation prologue forms silu(gate) * up as it reads them.
+        call.xform.kind = XKind::Swiglu;
+        call.xform.a = static_cast<const float *>(gate->dev);
+        call.xform.b = static_cast<const float *>(up->dev);
+        return run_packed(ctx, call, codes, scales);
+    }
     const size_t count = size_t(gate->dims[0]) * p.inner;
     // Stage silu(gate) * up once, then run the plain packed product on it
     // (backend-cpu/src/packed.rs:425-455).
@@ -355,15 +425,7 @@ mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf
         return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
     launch_swiglu(ctx->stream, activated, static_cast<const float *>(gate->dev),
                   static_cast<const float *>(up->dev), count);
-    PackedCall call;
-    call.format = p.format;
-    call.epilogue = Epilogue::Single;
-    call.m = uint32_t(gate->dims[0]);
-    call.n = p.rows;
-    call.k = p.inner;
     call.x = activated;
-    call.a = stream_of(codes, scales);
-    call.out_a = static_cast<float *>(output->dev);
     return run_packed(ctx, call, codes, scales);
 }
 

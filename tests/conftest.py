@@ -37,6 +37,19 @@ def backend():
     b.close()
 
 
+# Kernel paths of mfh_set_kernel_path: automatic (in-kernel activation
+# prologue where it fits), FP32 FMA kernels only, automatic with the
+# prologue as a kernel of its own.
+PATHS = {"auto": 0, "fma": 1, "split": 2}
+
+
+@pytest.fixture(params=list(PATHS))
+def path(request, backend):
+    previous = backend.set_kernel_path(PATHS[request.param])
+    yield request.param
+    backend.set_kernel_path(previous)
+
+
 def max_rel_err(got: np.ndarray, want: np.ndarray) -> float:
     """max|got - want| / max|want| (0 when both are all-zero)."""
     got = np.asarray(got, dtype=np.float64)

@@ -54,8 +54,11 @@ def check_logits(got, want):
 
 
 @pytest.mark.parametrize("mix", list(MIXES))
-def test_prefill_then_teacher_forced_decode(backend, mix):
-    say("lfm2 decode", mix)
+def test_prefill_then_teacher_forced_decode(backend, path, mix):
+    # Device-id steps of a fully packed model take the fused decode step
+    # (auto: transforms in the GEMV kernels; split: in the prologue
+    # kernels); fma and the dense-conv mix run the op-by-op pass.
+    say("lfm2 decode", mix, path)
     cfg, model, ref = build(backend, mix)
     prompt = convert.token_ids(7, 0x7043_0001, cfg.vocab)
     model.append(prompt)

@@ -21,10 +21,10 @@ from tests.conftest import assert_close, max_rel_err
 
 pytestmark = pytest.mark.gpu
 SCHEMES = ["ternary", "nf4", "int8"]
-# auto selects the matrix-core decode GEMV at m <= 8 (activation prologue
-# inside the GEMV kernel where it fits); fma forces the FP32-FMA kernels
+# Every product test runs on each kernel path (the `path` fixture): auto
+# selects the matrix-core decode GEMV at m <= 8 (activation prologue inside
+# the GEMV kernel where it fits); fma forces the FP32-FMA kernels
 # everywhere; split runs the matrix-core prologue as a kernel of its own.
-PATHS = {"auto": 0, "fma": 1, "split": 2}
 
 
 def say(*parts):
@@ -49,13 +49,6 @@ def run_linear(backend, x, codes, scales):
     out = backend.allocate_f32((x.shape[0], codes.shape[0]))
     backend.packed_linear(out, xb, cb, sb)
     return backend.read(out)
-
-
-@pytest.fixture(params=list(PATHS))
-def path(request, backend):
-    previous = backend.set_kernel_path(PATHS[request.param])
-    yield request.param
-    backend.set_kernel_path(previous)
 
 
 # --- packed_linear ---------------------------------------------------------------
