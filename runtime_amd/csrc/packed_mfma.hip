@@ -579,76 +579,84 @@ __device__ __forceinline__ void reduce_and_store(const MfmaArgs &a, float (&vals
 // buffered in registers: the next block's weights and activation fragments
 // are in flight while the current one is computed.
 // ---------------------------------------------------------------------------
-template <Format F, int T, int S, int NF>
+template <Format F, int T, int S, int NF, bool HALF>
 struct I8Block {
     static constexpr int LB = Geo<F>::lb;
     static constexpr int LOADS = LB / Geo<F>::kpl;
+    static constexpr int GPB = LB / 2;  // 128-groups per loop block
+    using ST = typename ScaleT<HALF>::type;
     v4u w[S][T][LOADS];
+    ST sc[S][T][GPB];    // weight scales of the block's groups (this lane's row)
     v4i af[LB][NF];
+    float xf[GPB][NF];   // activation group factors
+    int2 cv[GPB][NF];    // ternary group corrections
 };
 
-template <Format F, int T, int S, int NF>
-__device__ __forceinline__ void i8_load_w(I8Block<F, T, S, NF> &blk,
-                                          const v4u *const (&wp)[S][T], uint32_t index)
+// Weights and their group scales of loop block `index`.
+template <Format F, int T, int S, int NF, bool HALF>
+__device__ __forceinline__ void i8_load_w(I8Block<F, T, S, NF, HALF> &blk,
+                                          const v4u *const (&wp)[S][T],
+                                          const typename ScaleT<HALF>::type *const (&sp)[S][T],
+                                          uint32_t index)
 {
-    using B = I8Block<F, T, S, NF>;
+    using B = I8Block<F, T, S, NF, HALF>;
 #pragma unroll
     for (int st = 0; st < S; ++st)
 #pragma unroll
-        for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t) {
 #pragma unroll
             for (int l = 0; l < B::LOADS; ++l)
                 blk.w[st][t][l] = wp[st][t][(index * B::LOADS + l) * 64];
+#pragma unroll
+            for (int gg = 0; gg < B::GPB; ++gg)
+                blk.sc[st][t][gg] = sp[st][t][(index * B::GPB + gg) * 16];
+        }
 }
 
-template <Format F, int T, int S, int NF, typename AP>
-__device__ __forceinline__ void i8_load_a(I8Block<F, T, S, NF> &blk, const AP &ap, uint32_t index)
+// Activation fragments and group constants of loop block `index`.
+template <Format F, int T, int S, int NF, bool HALF, typename AP>
+__device__ __forceinline__ void i8_load_a(I8Block<F, T, S, NF, HALF> &blk, const AP &ap,
+                                          const float *const (&xp)[NF],
+                                          const int2 *const (&cp)[NF], uint32_t index)
 {
-    using B = I8Block<F, T, S, NF>;
+    using B = I8Block<F, T, S, NF, HALF>;
 #pragma unroll
     for (int ks = 0; ks < B::LB; ++ks)
 #pragma unroll
         for (int f = 0; f < NF; ++f)
             blk.af[ks][f] = ap.at(index * B::LB + ks, f, NF);
-}
-
-template <Format F, int T, int S, int NF, typename AP>
-__device__ __forceinline__ void i8_load(I8Block<F, T, S, NF> &blk, const v4u *const (&wp)[S][T],
-                                        const AP &ap, uint32_t index)
-{
-    i8_load_w(blk, wp, index);
-    i8_load_a(blk, ap, index);
-}
-
-template <Format F, int T, int S, int NF, bool HALF>
-__device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF> &blk,
-                                           float (&accf)[S][T][NF],
-                                           const typename ScaleT<HALF>::type *const (&sp)[S][T],
-                                           const float *const (&xp)[NF],
-                                           const int2 *const (&cp)[NF], uint32_t gindex)
-{
-    using B = I8Block<F, T, S, NF>;
-    constexpr int GPB = B::LB / 2;
 #pragma unroll
-    for (int gg = 0; gg < GPB; ++gg) {
-        const uint32_t g = gindex * GPB + gg;
-        // Group constants: issued first so their latency overlaps the MFMAs.
-        float sc[S][T];
-#pragma unroll
-        for (int st = 0; st < S; ++st)
-#pragma unroll
-            for (int t = 0; t < T; ++t)
-                sc[st][t] = to_f32<HALF>(sp[st][t][g * 16]);
-        float xfv[NF];
-        int2 cv[NF];
+    for (int gg = 0; gg < B::GPB; ++gg)
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            xfv[f] = xp[f][g];
+            blk.xf[gg][f] = xp[f][index * B::GPB + gg];
             if constexpr (F == Format::Ternary)
-                cv[f] = cp[f][g];
+                blk.cv[gg][f] = cp[f][index * B::GPB + gg];
             else
-                cv[f] = int2{0, 0};
+                blk.cv[gg][f] = int2{0, 0};
         }
+}
+
+template <Format F, int T, int S, int NF, bool HALF, typename AP>
+__device__ __forceinline__ void i8_load(I8Block<F, T, S, NF, HALF> &blk,
+                                        const v4u *const (&wp)[S][T],
+                                        const typename ScaleT<HALF>::type *const (&sp)[S][T],
+                                        const AP &ap, const float *const (&xp)[NF],
+                                        const int2 *const (&cp)[NF], uint32_t index)
+{
+    i8_load_w(blk, wp, sp, index);
+    i8_load_a(blk, ap, xp, cp, index);
+}
+
+// One loop block: everything it reads was loaded with it (i8_load), so the
+// next block's loads stay in flight behind these MFMAs.
+template <Format F, int T, int S, int NF, bool HALF>
+__device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF, HALF> &blk,
+                                           float (&accf)[S][T][NF])
+{
+    using B = I8Block<F, T, S, NF, HALF>;
+#pragma unroll
+    for (int gg = 0; gg < B::GPB; ++gg) {
         v4i acci[S][T][NF];
 #pragma unroll
         for (int st = 0; st < S; ++st)
@@ -687,11 +695,13 @@ __device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF> &blk,
 #pragma unroll
                 for (int f = 0; f < NF; ++f) {
                     const v4i d = acci[st][t][f];
+                    const int2 cv = blk.cv[gg][f];
                     // |d.x| < 2^21, so the pairs combine exactly in int32.
-                    const int hi = (d.x << 8) + d.y - cv[f].x;
-                    const int lo = (d.z << 8) + d.w - cv[f].y;
+                    const int hi = (d.x << 8) + d.y - cv.x;
+                    const int lo = (d.z << 8) + d.w - cv.y;
                     const float gsum = float(hi) * 65536.0f + float(lo);
-                    accf[st][t][f] += gsum * (sc[st][t] * xfv[f]);
+                    accf[st][t][f] +=
+                        gsum * (to_f32<HALF>(blk.sc[st][t][gg]) * blk.xf[gg][f]);
                 }
     }
 }
@@ -718,7 +728,7 @@ __host__ __device__ constexpr size_t fused_bytes_nf4(uint32_t k_pad, uint32_t m)
 template <Format F, int T, int S, int NF, bool HALF, Epilogue E, int PRO>
 __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
 {
-    using B = I8Block<F, T, S, NF>;
+    using B = I8Block<F, T, S, NF, HALF>;
     using ST = typename ScaleT<HALF>::type;
     constexpr int KPL = Geo<F>::kpl;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -764,12 +774,12 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
     auto main_loop = [&](auto afp) {
         for (uint32_t i = 0; i < nblk; i += 2) {
             if (i + 1 < nblk)
-                i8_load(buf1, wp, afp, i + 1);
-            i8_compute<F, T, S, NF, HALF>(buf0, accf, sp, xp, cp, i);
+                i8_load(buf1, wp, sp, afp, xp, cp, i + 1);
+            i8_compute(buf0, accf);
             if (i + 1 < nblk) {
                 if (i + 2 < nblk)
-                    i8_load(buf0, wp, afp, i + 2);
-                i8_compute<F, T, S, NF, HALF>(buf1, accf, sp, xp, cp, i + 1);
+                    i8_load(buf0, wp, sp, afp, xp, cp, i + 2);
+                i8_compute(buf1, accf);
             }
         }
     };
@@ -784,7 +794,7 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
         float *fxf = reinterpret_cast<float *>(frag + size_t(a.k_pad) * rp);
         int2 *fcorr = reinterpret_cast<int2 *>(fxf + 4 * groups);
         if (nblk > 0)
-            i8_load_w(buf0, wp, 0);
+            i8_load_w(buf0, wp, sp, 0);
         for (uint32_t i = a.m * groups + threadIdx.x; i < 4 * groups; i += blockDim.x) {
             fxf[i] = 0.0f;
             fcorr[i] = int2{0, 0};
@@ -801,11 +811,11 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
                                    j,
                                4 * rp, j < rp};
         if (nblk > 0)
-            i8_load_a(buf0, lap, 0);
+            i8_load_a(buf0, lap, xp, cp, 0);
         main_loop(lap);
     } else {
         if (nblk > 0)
-            i8_load(buf0, wp, ap, 0);
+            i8_load(buf0, wp, sp, ap, xp, cp, 0);
         main_loop(ap);
     }
 
@@ -824,39 +834,38 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
 // slower -- the extra build work and LDS footprint cost more than the bank
 // conflicts it removes.
 constexpr uint32_t kLutCopies = 1;
-template <int T, int S>
+template <int T, int S, bool HALF>
 struct Nf4Block {
     v4u w[S][T];
+    typename ScaleT<HALF>::type sc[S][T];  // the group's weight scales (this lane's row)
     v8h af[4];
+    float xf[2];  // the group's activation factors of batch rows 2q, 2q + 1
 };
 
-template <int T, int S, typename AP>
-__device__ __forceinline__ void nf4_load(Nf4Block<T, S> &blk, const v4u *const (&wp)[S][T],
-                                         const AP &ap, uint32_t index)
+template <int T, int S, bool HALF, typename AP>
+__device__ __forceinline__ void nf4_load(Nf4Block<T, S, HALF> &blk, const v4u *const (&wp)[S][T],
+                                         const typename ScaleT<HALF>::type *const (&sp)[S][T],
+                                         const AP &ap, const float *const (&xp)[2],
+                                         uint32_t index)
 {
 #pragma unroll
     for (int st = 0; st < S; ++st)
 #pragma unroll
-        for (int t = 0; t < T; ++t)
+        for (int t = 0; t < T; ++t) {
             blk.w[st][t] = wp[st][t][index * 64];
+            blk.sc[st][t] = sp[st][t][index * 16];
+        }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
         blk.af[ks] = ap.at(index * 4 + ks, 0, 1);
+    blk.xf[0] = xp[0][index];
+    blk.xf[1] = xp[1][index];
 }
 
 template <int T, int S, bool HALF>
-__device__ __forceinline__ void nf4_compute(const Nf4Block<T, S> &blk, float (&accf)[S][T][2],
-                                            const typename ScaleT<HALF>::type *const (&sp)[S][T],
-                                            const float *const (&xp)[2], const uint2 *lut,
-                                            uint32_t g)
+__device__ __forceinline__ void nf4_compute(const Nf4Block<T, S, HALF> &blk,
+                                            float (&accf)[S][T][2], const uint2 *lut)
 {
-    float sc[S][T];
-#pragma unroll
-    for (int st = 0; st < S; ++st)
-#pragma unroll
-        for (int t = 0; t < T; ++t)
-            sc[st][t] = to_f32<HALF>(sp[st][t][g * 16]);
-    const float xf0 = xp[0][g], xf1 = xp[1][g];
     v4f acc[S][T];
 #pragma unroll
     for (int st = 0; st < S; ++st)
@@ -888,8 +897,9 @@ __device__ __forceinline__ void nf4_compute(const Nf4Block<T, S> &blk, float (&a
 #pragma unroll
         for (int t = 0; t < T; ++t) {
             // Rows 4q + {0,1} are batch 2q (hi, lo), rows 4q + {2,3} batch 2q+1.
-            accf[st][t][0] += (acc[st][t].x + acc[st][t].y) * (sc[st][t] * xf0);
-            accf[st][t][1] += (acc[st][t].z + acc[st][t].w) * (sc[st][t] * xf1);
+            const float sc = to_f32<HALF>(blk.sc[st][t]);
+            accf[st][t][0] += (acc[st][t].x + acc[st][t].y) * (sc * blk.xf[0]);
+            accf[st][t][1] += (acc[st][t].z + acc[st][t].w) * (sc * blk.xf[1]);
         }
 }
 
@@ -944,18 +954,18 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
         for (int t = 0; t < T; ++t)
             accf[st][t][0] = accf[st][t][1] = 0.0f;
 
-    Nf4Block<T, S> buf0, buf1;
+    Nf4Block<T, S, HALF> buf0, buf1;
     auto main_loop = [&](const auto &ap) {
         if (nblk > 0)
-            nf4_load(buf0, wp, ap, 0);
+            nf4_load(buf0, wp, sp, ap, xp, 0);
         for (uint32_t i = 0; i < nblk; i += 2) {
             if (i + 1 < nblk)
-                nf4_load(buf1, wp, ap, i + 1);
-            nf4_compute<T, S, HALF>(buf0, accf, sp, xp, lut, i);
+                nf4_load(buf1, wp, sp, ap, xp, i + 1);
+            nf4_compute(buf0, accf, lut);
             if (i + 1 < nblk) {
                 if (i + 2 < nblk)
-                    nf4_load(buf0, wp, ap, i + 2);
-                nf4_compute<T, S, HALF>(buf1, accf, sp, xp, lut, i + 1);
+                    nf4_load(buf0, wp, sp, ap, xp, i + 2);
+                nf4_compute(buf1, accf, lut);
             }
         }
     };
