@@ -605,8 +605,17 @@ __device__ __forceinline__ void i8_load_w(I8Block<F, T, S, NF, HALF> &blk,
 #pragma unroll
         for (int t = 0; t < T; ++t) {
 #pragma unroll
-            for (int l = 0; l < B::LOADS; ++l)
-                blk.w[st][t][l] = wp[st][t][(index * B::LOADS + l) * 64];
+            for (int l = 0; l < B::LOADS; ++l) {
+                // Large INT8 matrices (the 4-tile plan) stream once per
+                // launch: non-temporal loads measured about 10 % faster on
+                // the 65536-row head; ternary, NF4 and small fused shapes
+                // measured the same or slower with them.
+                if constexpr (F == Format::Int8 && T == 4)
+                    blk.w[st][t][l] =
+                        __builtin_nontemporal_load(&wp[st][t][(index * B::LOADS + l) * 64]);
+                else
+                    blk.w[st][t][l] = wp[st][t][(index * B::LOADS + l) * 64];
+            }
 #pragma unroll
             for (int gg = 0; gg < B::GPB; ++gg)
                 blk.sc[st][t][gg] = sp[st][t][(index * B::GPB + gg) * 16];
