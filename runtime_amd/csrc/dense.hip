@@ -469,6 +469,38 @@ __global__ __launch_bounds__(kBlock) void rotary_kernel(float *__restrict__ out,
     }
 }
 
+// One wave: head-local RMS norm of `in` (head_dim values) with `weight`,
+// then the split-half rotation at `position`, into `out` and, when non-null,
+// also `copy` (normalization_rotary.rs:246-369).
+__device__ __forceinline__ void norm_rope_head(const float *__restrict__ in, float *out,
+                                               float *copy, const float *__restrict__ weight,
+                                               uint32_t head_dim, float position, float theta,
+                                               float epsilon)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t half = head_dim / 2;
+    float squares = 0.0f;
+    for (uint32_t c = lane; c < head_dim; c += 64) {
+        const float v = in[c];
+        squares += v * v;
+    }
+    squares = wave_sum(squares);
+    const float reciprocal = 1.0f / sqrtf(squares / float(head_dim) + epsilon);
+    for (uint32_t c = lane; c < half; c += 64) {
+        const float first = (in[c] * reciprocal) * weight[c];
+        const float second = (in[half + c] * reciprocal) * weight[half + c];
+        const Rotation rot = rotation(position, c, head_dim, theta);
+        const float a = first * rot.cosine - second * rot.sine;
+        const float b = second * rot.cosine + first * rot.sine;
+        out[c] = a;
+        out[half + c] = b;
+        if (copy) {
+            copy[c] = a;
+            copy[half + c] = b;
+        }
+    }
+}
+
 // Per-head RMS norm then split-half rotary for query and key heads in one
 // launch (normalization_rotary.rs:246-369): one wave per (token, head),
 // query heads first.
@@ -478,12 +510,9 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(
     const float *__restrict__ key_weight, Positions positions, uint64_t tokens,
     uint32_t query_heads, uint32_t key_heads, uint32_t head_dim, float theta, float epsilon)
 {
-    const int lane = threadIdx.x & 63;
     const uint32_t heads = query_heads + key_heads;
     const uint64_t segments = tokens * heads;
     const uint64_t waves = uint64_t(gridDim.x) * (kBlock / 64);
-    const uint32_t half = head_dim / 2;
-    const float dim_f = float(head_dim);
     for (uint64_t s = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6); s < segments;
          s += waves) {
         const uint64_t token = s / heads;
@@ -492,24 +521,9 @@ __global__ __launch_bounds__(kBlock) void qk_norm_rope_kernel(
         const uint32_t h = is_query ? head : head - query_heads;
         const uint64_t base =
             (token * (is_query ? query_heads : key_heads) + h) * uint64_t(head_dim);
-        const float *in = (is_query ? query : key) + base;
-        float *out = (is_query ? query_out : key_out) + base;
-        const float *weight = is_query ? query_weight : key_weight;
-        float squares = 0.0f;
-        for (uint32_t c = lane; c < head_dim; c += 64) {
-            const float v = in[c];
-            squares += v * v;
-        }
-        squares = wave_sum(squares);
-        const float reciprocal = 1.0f / sqrtf(squares / dim_f + epsilon);
-        const float position = position_of(positions, token);
-        for (uint32_t c = lane; c < half; c += 64) {
-            const float first = (in[c] * reciprocal) * weight[c];
-            const float second = (in[half + c] * reciprocal) * weight[half + c];
-            const Rotation rot = rotation(position, c, head_dim, theta);
-            out[c] = first * rot.cosine - second * rot.sine;
-            out[half + c] = second * rot.cosine + first * rot.sine;
-        }
+        norm_rope_head((is_query ? query : key) + base, (is_query ? query_out : key_out) + base,
+                       nullptr, is_query ? query_weight : key_weight, head_dim,
+                       position_of(positions, token), theta, epsilon);
     }
 }
 
@@ -698,6 +712,9 @@ __global__ __launch_bounds__(kBlock) void gqa_split_kernel(float *__restrict__ p
         for (uint32_t base = 0; base < quads; base += kStage * kBlock) {
             float4 kq[kStage], vq[kStage];
 #pragma unroll
+            for (uint32_t u = 0; u < kStage; ++u)
+                kq[u] = vq[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
             for (uint32_t u = 0; u < kStage; ++u) {
                 const uint32_t i = base + u * kBlock + threadIdx.x;
                 if (i < quads) {
@@ -811,6 +828,171 @@ __global__ __launch_bounds__(kBlock) void gqa_combine_kernel(float *__restrict__
         for (uint32_t pi = 1; pi < parts; ++pi)
             acc += part[pi * head_dim + dim];
         out[uint64_t(blockIdx.x) * head_dim + dim] = acc / denominator;
+    }
+}
+
+// One decode token's qk_norm_rope, key append and split-key attention in
+// one launch (gqa_combine_kernel then merges the ranges).  Block (kv head,
+// range) stages its keys and values with float4 loads, normalises and
+// rotates its group's queries into LDS (the coefficients come from a
+// rotation table, see launch_rotation_table), and -- the block whose range
+// ends at the new key -- that key's row, which it also writes to the cache
+// (the value row is already there).  Each block then stores its (m, l, acc)
+// records as gqa_split_kernel does.  Handing the records to the combine
+// through a kernel boundary measured faster than a last-block combine,
+// whose __threadfence() writes back the L2 of every XCD.
+__device__ __forceinline__ void norm_rope_head_table(const float *__restrict__ in, float *out,
+                                                     float *copy, const float *__restrict__ weight,
+                                                     uint32_t head_dim, const float *cosine,
+                                                     const float *sine, float epsilon)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t half = head_dim / 2;
+    float squares = 0.0f;
+    for (uint32_t c = lane; c < head_dim; c += 64) {
+        const float v = in[c];
+        squares += v * v;
+    }
+    squares = wave_sum(squares);
+    const float reciprocal = 1.0f / sqrtf(squares / float(head_dim) + epsilon);
+    for (uint32_t c = lane; c < half; c += 64) {
+        const float first = (in[c] * reciprocal) * weight[c];
+        const float second = (in[half + c] * reciprocal) * weight[half + c];
+        const float a = first * cosine[c] - second * sine[c];
+        const float b = second * cosine[c] + first * sine[c];
+        out[c] = a;
+        out[half + c] = b;
+        if (copy) {
+            copy[c] = a;
+            copy[half + c] = b;
+        }
+    }
+}
+
+
+__global__ __launch_bounds__(kBlock) void gqa_decode_kernel(DecodeAttention p)
+{
+    extern __shared__ float lds[];
+    const uint32_t d = p.head_dim, group = p.group, splits = p.splits;
+    const uint32_t half = d / 2;
+    float *q = lds;
+    float *kl = q + group * d;
+    float *vl = kl + kSplitKeys * (d + 1);
+    float *pr = vl + kSplitKeys * d;
+    const float *rot = p.rotation + p.position * d;  // cosines [half], sines [half]
+
+    const uint32_t split = blockIdx.x % splits;
+    const uint32_t kv_head = blockIdx.x / splits;
+    const uint64_t kv_width = uint64_t(p.key_value_heads) * d;
+    const uint64_t visible = p.position + 1;
+    const uint64_t begin = uint64_t(split) * kSplitKeys;
+    const uint32_t count =
+        begin >= visible ? 0u : uint32_t(visible - begin < kSplitKeys ? visible - begin : kSplitKeys);
+    const bool holds_new = count > 0 && begin + count == visible;
+    const uint32_t cached = holds_new ? count - 1 : count;  // key rows read from the cache
+    const uint64_t record = uint64_t(d) + 2;
+    const uint32_t head0 = kv_head * group;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+
+    // Keys and values of the range (d % 4 == 0, checked by the launcher).
+    const float *keys = p.key_cache + begin * kv_width + kv_head * uint64_t(d);
+    const float *values = p.value_cache + begin * kv_width + kv_head * uint64_t(d);
+    {
+        constexpr uint32_t kStage = 8;
+        const uint32_t quads = count * d / 4;
+        for (uint32_t base = 0; base < quads; base += kStage * kBlock) {
+            float4 kq[kStage], vq[kStage];
+#pragma unroll
+            for (uint32_t u = 0; u < kStage; ++u)
+                kq[u] = vq[u] = float4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (uint32_t u = 0; u < kStage; ++u) {
+                const uint32_t i = base + u * kBlock + threadIdx.x;
+                if (i < quads) {
+                    const uint32_t key = 4 * i / d, c = 4 * i - key * d;
+                    if (key < cached)
+                        kq[u] = *reinterpret_cast<const float4 *>(keys + key * kv_width + c);
+                    vq[u] = *reinterpret_cast<const float4 *>(values + key * kv_width + c);
+                }
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < kStage; ++u) {
+                const uint32_t i = base + u * kBlock + threadIdx.x;
+                if (i < quads) {
+                    const uint32_t key = 4 * i / d, c = 4 * i - key * d;
+                    if (key < cached) {
+                        float *kr = kl + key * (d + 1) + c;
+                        kr[0] = kq[u].x;
+                        kr[1] = kq[u].y;
+                        kr[2] = kq[u].z;
+                        kr[3] = kq[u].w;
+                    }
+                    reinterpret_cast<float4 *>(vl)[i] = vq[u];
+                }
+            }
+        }
+    }
+    __syncthreads();
+    for (uint32_t h = wave; h < group; h += kBlock / 64)
+        norm_rope_head_table(p.query + (head0 + h) * uint64_t(d), q + h * d, nullptr,
+                             p.query_weight, d, rot, rot + half, p.epsilon);
+    if (holds_new && wave == kBlock / 64 - 1)
+        norm_rope_head_table(p.key + kv_head * uint64_t(d), kl + (count - 1) * (d + 1),
+                             p.key_cache + p.position * kv_width + kv_head * uint64_t(d),
+                             p.key_weight, d, rot, rot + half, p.epsilon);
+    __syncthreads();
+
+    float *out_records = p.partial + (uint64_t(head0) * splits + split) * record;
+    for (uint32_t i = threadIdx.x; i < group * kSplitKeys; i += kBlock) {
+        const uint32_t h = i / kSplitKeys, key = i % kSplitKeys;
+        if (key < count) {
+            const float *qh = q + h * d;
+            const float *kr = kl + key * (d + 1);
+            float dot = 0.0f;
+            for (uint32_t c = 0; c < d; ++c)
+                dot += qh[c] * kr[c];
+            pr[i] = dot * p.scale;
+        }
+    }
+    __syncthreads();
+    for (uint32_t h = wave; h < group; h += kBlock / 64) {
+        const float s = lane < count ? pr[h * kSplitKeys + lane] : -__builtin_inff();
+        const float m = wave_max(s);
+        const float e = lane < count ? expf(s - m) : 0.0f;
+        pr[h * kSplitKeys + lane] = e;
+        const float l = wave_sum(e);
+        if (lane == 0) {
+            out_records[uint64_t(h) * splits * record] = m;
+            out_records[uint64_t(h) * splits * record + 1] = l;
+        }
+    }
+    __syncthreads();
+    for (uint32_t t = threadIdx.x; t < group * d; t += kBlock) {
+        const uint32_t h = t / d, dim = t - h * d;
+        const float *ph = pr + h * kSplitKeys;
+        float acc = 0.0f;
+        for (uint32_t j = 0; j < count; ++j)
+            acc += ph[j] * vl[j * d + dim];
+        out_records[uint64_t(h) * splits * record + 2 + dim] = acc;
+    }
+
+}
+
+// Row t of the table: rotation(t, c) for c < head_dim / 2, cosines then
+// sines (the coefficients the rotary kernels compute inline).
+__global__ __launch_bounds__(kBlock) void rotation_table_kernel(float *__restrict__ table,
+                                                                uint64_t positions,
+                                                                uint32_t head_dim, float theta)
+{
+    const uint32_t half = head_dim / 2;
+    const uint64_t total = positions * half;
+    const uint64_t stride = uint64_t(gridDim.x) * kBlock;
+    for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < total; i += stride) {
+        const uint64_t t = i / half;
+        const uint32_t c = uint32_t(i - t * half);
+        const Rotation r = rotation(float(t), c, head_dim, theta);
+        table[t * head_dim + c] = r.cosine;
+        table[t * head_dim + half + c] = r.sine;
     }
 }
 
@@ -1033,6 +1215,36 @@ void launch_gqa(hipStream_t stream, float *out, const float *query, const float 
     }
     const size_t lds = (size_t(g.head_dim) + kKeyChunk + kBlock) * sizeof(float);
     gqa_kernel<<<unsigned(blocks), kBlock, lds, stream>>>(out, query, key_cache, value_cache, g);
+}
+
+uint32_t gqa_decode_splits(const DecodeAttention &p)
+{
+    const uint64_t splits = (p.position + 1 + kSplitKeys - 1) / kSplitKeys;
+    if (splits > kSplitMaxRanges || p.head_dim % 4 || p.group == 0 ||
+        gqa_split_lds(p.group, p.head_dim) > kSplitMaxLds)
+        return 0;
+    return uint32_t(splits);
+}
+
+size_t gqa_decode_scratch_bytes(const DecodeAttention &p)
+{
+    return size_t(p.query_heads) * gqa_decode_splits(p) * (p.head_dim + 2) * sizeof(float);
+}
+
+void launch_rotation_table(hipStream_t stream, float *table, uint64_t positions,
+                           uint32_t head_dim, float theta)
+{
+    if (positions && head_dim >= 2)
+        rotation_table_kernel<<<grid_for(positions * (head_dim / 2)), kBlock, 0, stream>>>(
+            table, positions, head_dim, theta);
+}
+
+void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p)
+{
+    gqa_decode_kernel<<<p.key_value_heads * p.splits, kBlock,
+                        gqa_split_lds(p.group, p.head_dim), stream>>>(p);
+    gqa_combine_kernel<<<p.query_heads, kBlock, (size_t(p.splits) + kBlock) * sizeof(float),
+                         stream>>>(p.out, p.partial, p.head_dim, p.splits);
 }
 
 void launch_short_conv(hipStream_t stream, float *out, const float *projection,

@@ -43,6 +43,8 @@ struct XForm {
     uint32_t width = 0;        // Conv taps
 };
 
+constexpr uint32_t kMaxSegments = 3;
+
 struct PackedCall {
     Format format = Format::Ternary;
     Epilogue epilogue = Epilogue::Single;
@@ -58,6 +60,14 @@ struct PackedCall {
     bool separate_prologue = false;
     // Matrix-core GEMV only: a transform other than Plain replaces `x`.
     XForm xform;
+    // Matrix-core GEMV, Single epilogue only: when non-zero, the launch
+    // runs `segments` weight streams of one format and width k over the
+    // same activations, seg[i] (seg_n[i] rows) into seg_out[i]; a, n and
+    // out_a are unused.  The scale halves of all segments must agree.
+    uint32_t segments = 0;
+    PackedStream seg[kMaxSegments];
+    float *seg_out[kMaxSegments] = {};
+    uint32_t seg_n[kMaxSegments] = {};
 };
 
 // A matrix-core GEMV (m <= 2; m = 1 for Conv) whose activation prologue
@@ -68,6 +78,13 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
                         uint32_t n, uint32_t k, const mfh_buf *codes_a, const mfh_buf *scales_a,
                         const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
                         float *out_b);
+
+// Like packed_xform with the Single epilogue, over `count` weight streams of
+// one format and width k in one launch (the LFM2 q/k/v projections).
+mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, uint32_t k,
+                                 uint32_t count, const mfh_buf *const *codes,
+                                 const mfh_buf *const *scales, const uint32_t *n,
+                                 float *const *out);
 
 // Decode GEMV for m <= 8 on FP32 FMA units.
 void launch_gemv_fma(hipStream_t stream, const PackedCall &call);
@@ -172,6 +189,33 @@ size_t gqa_scratch_bytes(const GqaShape &g);
 void launch_gqa(hipStream_t stream, float *out, const float *query, const float *key,
                 const float *value, float *key_cache, float *value_cache, const GqaShape &g,
                 float *scratch);
+// One decode token's qk_norm_rope + causal_gqa (no cache append for the
+// value: its row `position` must already hold the new value), as two
+// launches.  Writes the rotated key into the key cache row `position` and
+// the attention output.  `partial` holds gqa_decode_scratch_bytes.
+// gqa_decode_splits gives the key ranges to put in `splits`, or 0 when the
+// shape is outside the kernel.
+struct DecodeAttention {
+    const float *query = nullptr;         // [query_heads * head_dim], raw
+    const float *key = nullptr;           // [key_value_heads * head_dim], raw
+    const float *query_weight = nullptr;  // [head_dim]
+    const float *key_weight = nullptr;    // [head_dim]
+    float *key_cache = nullptr, *value_cache = nullptr;
+    float *partial = nullptr;
+    const float *rotation = nullptr;      // launch_rotation_table rows, >= position + 1
+    float *out = nullptr;                 // [query_heads * head_dim]
+    uint64_t position = 0;                // the new token's row (= cache length before it)
+    uint32_t query_heads = 0, key_value_heads = 0, head_dim = 0, group = 0, splits = 0;
+    float theta = 0.0f, epsilon = 0.0f, scale = 0.0f;
+};
+// table[t * head_dim + c] = cos, table[t * head_dim + head_dim / 2 + c] =
+// sin of the rotation of position t, column c < head_dim / 2, for
+// t < positions: bit for bit what the rotary kernels compute inline.
+void launch_rotation_table(hipStream_t stream, float *table, uint64_t positions,
+                           uint32_t head_dim, float theta);
+uint32_t gqa_decode_splits(const DecodeAttention &p);
+size_t gqa_decode_scratch_bytes(const DecodeAttention &p);
+void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p);
 void launch_short_conv(hipStream_t stream, float *out, const float *projection,
                        const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
                        uint32_t width);

@@ -86,6 +86,7 @@ struct mfl_model {
     uint64_t length = 0;
     std::map<uint64_t, std::unique_ptr<Workspace>> workspaces;
     Owned logits, sampled;
+    Owned rotation;  // [max_tokens, head_dim] rotation coefficients by position
 };
 
 namespace mfh {
@@ -225,9 +226,10 @@ bool fused_decode_ready(const mfl_model *m)
 // activation prologues (see XForm): per convolution block the in
 // projection (residual add + operator norm), the out projection (the
 // convolution) and the gate/up pair (residual add + FFN norm, with SwiGLU in
-// its epilogue); attention blocks write K and V straight into their cache
-// rows.  Same operations and order as append() on one row; only the f32
-// reduction trees of the norms differ.
+// its epilogue).  Attention blocks run q/k/v as one launch (v lands in its
+// cache row) and qk_norm_rope + the key append + attention as two.  Same
+// operations and order as append() on one row; only the f32 reduction trees
+// of the norms and the softmax differ.
 mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_logits)
 {
     mfh_ctx *c = m->ctx;
@@ -280,35 +282,78 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
         } else {
             float *key_row = dev(st.key) + position * kv;
             float *value_row = dev(st.value) + position * kv;
-            if ((s = packed_xform(c, Epilogue::Single, norm_of(lw.operator_norm, block_input_side),
-                                  1, h, h, lw.query.tensor, lw.query.scales, nullptr, nullptr,
-                                  dev(ws->q), nullptr)) ||
-                (s = packed_xform(c, Epilogue::Pair, norm_of(lw.operator_norm, nullptr), 1, kv, h,
-                                  lw.key.tensor, lw.key.scales, lw.value.tensor, lw.value.scales,
-                                  dev(ws->k), value_row)))
-                return s;
-            Positions positions;
-            positions.base = position;
-            launch_qk_norm_rope(c->stream, dev(ws->q_rope), key_row, dev(ws->q), dev(ws->k),
-                                dev(lw.query_norm), dev(lw.key_norm), positions, 1,
-                                cfg.attention_heads, cfg.key_value_heads, cfg.head_dim,
-                                cfg.rope_theta, cfg.block_norm_epsilon);
-            GqaShape g;
-            g.tokens = 1;
-            g.initial_len = st.length;
-            g.query_heads = cfg.attention_heads;
-            g.key_value_heads = cfg.key_value_heads;
-            g.head_dim = cfg.head_dim;
-            g.group = cfg.attention_heads / cfg.key_value_heads;
-            g.scale = 1.0f / std::sqrt(float(cfg.head_dim));
-            float *partials = nullptr;
-            if (const size_t bytes = gqa_scratch_bytes(g)) {
-                partials = static_cast<float *>(work_scratch(c, bytes));
-                if (!partials)
-                    return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+            // q, k and v in one launch when they share a format, else q and
+            // the k/v pair; v lands in its cache row.
+            s = MFH_UNSUPPORTED;
+            if (same_packed_format(lw.query, lw.key) && same_packed_format(lw.key, lw.value)) {
+                const mfh_buf *codes[3] = {lw.query.tensor, lw.key.tensor, lw.value.tensor};
+                const mfh_buf *scales[3] = {lw.query.scales, lw.key.scales, lw.value.scales};
+                const uint32_t rows[3] = {h, kv, kv};
+                float *outs[3] = {dev(ws->q), dev(ws->k), value_row};
+                s = packed_xform_segments(c, norm_of(lw.operator_norm, block_input_side), 1, h, 3,
+                                          codes, scales, rows, outs);
             }
-            launch_gqa(c->stream, dev(ws->attention), dev(ws->q_rope), nullptr, nullptr,
-                       dev(st.key), dev(st.value), g, partials);
+            if (s == MFH_UNSUPPORTED &&
+                !(s = packed_xform(c, Epilogue::Single,
+                                   norm_of(lw.operator_norm, block_input_side), 1, h, h,
+                                   lw.query.tensor, lw.query.scales, nullptr, nullptr, dev(ws->q),
+                                   nullptr)))
+                s = packed_xform(c, Epilogue::Pair, norm_of(lw.operator_norm, nullptr), 1, kv, h,
+                                 lw.key.tensor, lw.key.scales, lw.value.tensor, lw.value.scales,
+                                 dev(ws->k), value_row);
+            if (s)
+                return s;
+            // qk_norm_rope, the key append and split-key attention in one
+            // launch plus the range combine where the shape allows, else
+            // qk_norm_rope (writing the key row) and causal_gqa without an
+            // append.
+            DecodeAttention da;
+            da.query = dev(ws->q);
+            da.key = dev(ws->k);
+            da.query_weight = dev(lw.query_norm);
+            da.key_weight = dev(lw.key_norm);
+            da.key_cache = dev(st.key);
+            da.value_cache = dev(st.value);
+            da.rotation = dev(m->rotation);
+            da.out = dev(ws->attention);
+            da.position = st.length;
+            da.query_heads = cfg.attention_heads;
+            da.key_value_heads = cfg.key_value_heads;
+            da.head_dim = cfg.head_dim;
+            da.group = cfg.attention_heads / cfg.key_value_heads;
+            da.theta = cfg.rope_theta;
+            da.epsilon = cfg.block_norm_epsilon;
+            da.scale = 1.0f / std::sqrt(float(cfg.head_dim));
+            da.splits = gqa_decode_splits(da);
+            if (da.splits) {
+                da.partial = static_cast<float *>(work_scratch(c, gqa_decode_scratch_bytes(da)));
+                if (!da.partial)
+                    return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+                launch_gqa_decode(c->stream, da);
+            } else {
+                Positions positions;
+                positions.base = position;
+                launch_qk_norm_rope(c->stream, dev(ws->q_rope), key_row, dev(ws->q), dev(ws->k),
+                                    dev(lw.query_norm), dev(lw.key_norm), positions, 1,
+                                    cfg.attention_heads, cfg.key_value_heads, cfg.head_dim,
+                                    cfg.rope_theta, cfg.block_norm_epsilon);
+                GqaShape g;
+                g.tokens = 1;
+                g.initial_len = st.length;
+                g.query_heads = cfg.attention_heads;
+                g.key_value_heads = cfg.key_value_heads;
+                g.head_dim = cfg.head_dim;
+                g.group = da.group;
+                g.scale = da.scale;
+                float *partials = nullptr;
+                if (const size_t bytes = gqa_scratch_bytes(g)) {
+                    partials = static_cast<float *>(work_scratch(c, bytes));
+                    if (!partials)
+                        return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+                }
+                launch_gqa(c->stream, dev(ws->attention), dev(ws->q_rope), nullptr, nullptr,
+                           dev(st.key), dev(st.value), g, partials);
+            }
             st.length += 1;
             XForm plain;
             plain.a = dev(ws->attention);
@@ -519,6 +564,12 @@ mfh_status mfl_create(mfh_ctx *ctx, const mfl_config *config, mfl_model **out)
     }
     if (!s)
         s = alloc(ctx, m->logits, 1, c.vocab, MFH_CLASS_CACHE, true);
+    if (!s && (s = alloc(ctx, m->rotation, c.max_tokens, c.head_dim, MFH_CLASS_CACHE, false)) ==
+                  MFH_OK) {
+        DeviceGuard guard(ctx->device);
+        launch_rotation_table(ctx->stream, static_cast<float *>(m->rotation.buf->dev),
+                              c.max_tokens, c.head_dim, c.rope_theta);
+    }
     if (!s) {
         const uint64_t dims[1] = {1};
         s = mfh_alloc_f32(ctx, dims, 1, MFH_CLASS_CACHE, 1, &m->sampled.buf);

@@ -527,15 +527,57 @@ struct MfmaArgs {
     XForm xform;  // activation source of the prologue
     uint32_t m, n, k, k_pad;
     uint32_t ksteps_per_wave;
+    // Segmented launch (one stream, T = 1): blocks [seg_first[i], next) run
+    // weight stream i of seg_n[i] rows into seg_out[i]; 0 segments = off.
+    uint32_t segments;
+    uint32_t seg_first[kMaxSegments];
+    const uint8_t *seg_tiles[kMaxSegments];
+    const void *seg_scales[kMaxSegments];
+    float *seg_out[kMaxSegments];
+    uint32_t seg_n[kMaxSegments];
 };
+
+// The weight streams, output rows and first tile of this block.
+struct Target {
+    uint32_t tile0, n;
+    const uint8_t *tiles[2];
+    const void *scales[2];
+    float *out[2];
+};
+
+template <int T>
+__device__ __forceinline__ Target target_of(const MfmaArgs &a)
+{
+    Target r;
+    uint32_t block = blockIdx.x;
+    r.n = a.n;
+    for (int st = 0; st < 2; ++st) {
+        r.tiles[st] = a.tiles[st];
+        r.scales[st] = a.scales[st];
+        r.out[st] = a.out[st];
+    }
+    if (a.segments) {
+        uint32_t sg = 0;
+        while (sg + 1 < a.segments && block >= a.seg_first[sg + 1])
+            ++sg;
+        block -= a.seg_first[sg];
+        r.tiles[0] = a.seg_tiles[sg];
+        r.scales[0] = a.seg_scales[sg];
+        r.out[0] = a.seg_out[sg];
+        r.n = a.seg_n[sg];
+    }
+    r.tile0 = block * T;
+    return r;
+}
 
 // Fixed-order sum of the wave partials through LDS, then the epilogue.
 // vals[idx] per lane; idx = (st * T + t) * NB + batch-slot-of-lane.
 template <int S, int T, int NB, Epilogue E>
-__device__ __forceinline__ void reduce_and_store(const MfmaArgs &a, float (&vals)[S][T][NB],
-                                                 const uint32_t (&batch)[NB], uint32_t tile0,
-                                                 uint32_t j)
+__device__ __forceinline__ void reduce_and_store(uint32_t m, const Target &tg,
+                                                 float (&vals)[S][T][NB],
+                                                 const uint32_t (&batch)[NB], uint32_t j)
 {
+    const uint32_t tile0 = tg.tile0;
     extern __shared__ float red[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, waves = blockDim.x >> 6;
     constexpr int V = S * T * NB;
@@ -559,15 +601,15 @@ __device__ __forceinline__ void reduce_and_store(const MfmaArgs &a, float (&vals
         }
         const uint32_t b = batch[nb];
         const uint32_t row = (tile0 + t) * 16 + j;
-        if (b < a.m && row < a.n) {
-            const size_t o = size_t(b) * a.n + row;
+        if (b < m && row < tg.n) {
+            const size_t o = size_t(b) * tg.n + row;
             if constexpr (E == Epilogue::Single) {
-                a.out[0][o] = v[0];
+                tg.out[0][o] = v[0];
             } else if constexpr (E == Epilogue::Pair) {
-                a.out[0][o] = v[0];
-                a.out[1][o] = v[S - 1];
+                tg.out[0][o] = v[0];
+                tg.out[1][o] = v[S - 1];
             } else {
-                a.out[0][o] = silu_mul(v[0], v[S - 1]);
+                tg.out[0][o] = silu_mul(v[0], v[S - 1]);
             }
         }
     }
@@ -742,7 +784,8 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
     constexpr int KPL = Geo<F>::kpl;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t tile0 = blockIdx.x * T;
+    const Target tg = target_of<T>(a);
+    const uint32_t tile0 = tg.tile0;
     const uint32_t groups = a.k_pad / 128;
     const uint32_t s_begin = wave * a.ksteps_per_wave;
     const uint32_t nblk = a.ksteps_per_wave / B::LB;
@@ -755,9 +798,9 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
     for (int st = 0; st < S; ++st)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            wp[st][t] = reinterpret_cast<const v4u *>(a.tiles[st]) + (tile0 + t) * tile_vecs +
+            wp[st][t] = reinterpret_cast<const v4u *>(tg.tiles[st]) + (tile0 + t) * tile_vecs +
                         (s_begin / KPL) * 64 + lane;
-            sp[st][t] = reinterpret_cast<const ST *>(a.scales[st]) +
+            sp[st][t] = reinterpret_cast<const ST *>(tg.scales[st]) +
                         (size_t(tile0 + t) * groups + g_begin) * 16 + j;
         }
     const GlobalFrag<v4i> ap{reinterpret_cast<const v4i *>(a.afrag) + size_t(s_begin) * NF * 64 +
@@ -832,7 +875,7 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
 #pragma unroll
     for (int f = 0; f < NF; ++f)
         batch[f] = 4 * f + q;
-    reduce_and_store<S, T, NF, E>(a, accf, batch, tile0, j);
+    reduce_and_store<S, T, NF, E>(a.m, tg, accf, batch, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -936,7 +979,8 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t tile0 = blockIdx.x * T;
+    const Target tg = target_of<T>(a);
+    const uint32_t tile0 = tg.tile0;
     const uint32_t groups = a.k_pad / 128;
     const uint32_t s_begin = wave * a.ksteps_per_wave;  // 32-wide ksteps
     const uint32_t nblk = a.ksteps_per_wave / 4;
@@ -949,9 +993,9 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
     for (int st = 0; st < S; ++st)
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            wp[st][t] = reinterpret_cast<const v4u *>(a.tiles[st]) + (tile0 + t) * tile_vecs +
+            wp[st][t] = reinterpret_cast<const v4u *>(tg.tiles[st]) + (tile0 + t) * tile_vecs +
                         g_begin * 64 + lane;
-            sp[st][t] = reinterpret_cast<const ST *>(a.scales[st]) +
+            sp[st][t] = reinterpret_cast<const ST *>(tg.scales[st]) +
                         (size_t(tile0 + t) * groups + g_begin) * 16 + j;
         }
     const float *xp[2] = {a.xf + (2 * q) * groups + g_begin, a.xf + (2 * q + 1) * groups + g_begin};
@@ -1003,7 +1047,7 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
                                   lane});
     }
     const uint32_t batch[2] = {2 * q, 2 * q + 1};
-    reduce_and_store<S, T, 2, E>(a, accf, batch, tile0, j);
+    reduce_and_store<S, T, 2, E>(a.m, tg, accf, batch, j);
 }
 
 // ---------------------------------------------------------------------------
@@ -1256,12 +1300,38 @@ Scratch carve(void *scratch, uint32_t k_pad)
 // Largest grid that takes the in-kernel prologue (see gemv_i8_format).
 constexpr unsigned kFusedMaxBlocks = 512;
 
+// Tiles of the call: one stream's, or every segment's (each padded to 64
+// rows as repacked).  Segment first-block table for T = 1.
+uint32_t call_tiles(const PackedCall &call)
+{
+    if (!call.segments)
+        return pad_to(call.n, 64) / 16;
+    uint32_t tiles = 0;
+    for (uint32_t i = 0; i < call.segments; ++i)
+        tiles += pad_to(call.seg_n[i], 64) / 16;
+    return tiles;
+}
+
+void set_segments(MfmaArgs &args, const PackedCall &call)
+{
+    args.segments = call.segments;
+    uint32_t first = 0;
+    for (uint32_t i = 0; i < call.segments; ++i) {
+        args.seg_first[i] = first;
+        args.seg_tiles[i] = call.seg[i].tiles;
+        args.seg_scales[i] = call.seg[i].tiled_scales;
+        args.seg_out[i] = call.seg_out[i];
+        args.seg_n[i] = call.seg_n[i];
+        first += pad_to(call.seg_n[i], 64) / 16;
+    }
+}
+
 template <Format F>
 void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
 {
     const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
     const uint32_t groups = k_pad / 128;
-    const uint32_t n_tiles = pad_to(call.n, 64) / 16;
+    const uint32_t n_tiles = call_tiles(call);
     const int nf = call.m <= 4 ? 1 : 2;
     Scratch sc = carve(scratch, k_pad);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
@@ -1285,9 +1355,11 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
                n_tiles / t <= kFusedMaxBlocks && share <= kFusedGroupsPerWave &&
                share <= held_groups(xform.kind) && fused_kind_served(call.epilogue, xform.kind);
     };
-    Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1, false);
+    // Segmented launches keep one tile per block.
+    const int max_t = streams == 1 && !call.segments ? 4 : 1;
+    Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, false);
     if (!fusable(plan)) {
-        const Plan wide = plan_for(n_tiles, ksteps, Geo<F>::lb, streams == 1 ? 4 : 1, true);
+        const Plan wide = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, true);
         if (fusable(wide))
             plan = wide;
     }
@@ -1315,6 +1387,7 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     args.n = call.n;
     args.k_pad = k_pad;
     args.ksteps_per_wave = ksteps / plan.waves;
+    set_segments(args, call);
     const unsigned blocks = n_tiles / plan.tiles_per_block;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {
@@ -1331,7 +1404,7 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
 {
     const uint32_t k_pad = pad_to(call.k, 128);
     const uint32_t groups = k_pad / 128;
-    const uint32_t n_tiles = pad_to(call.n, 64) / 16;
+    const uint32_t n_tiles = call_tiles(call);
     Scratch sc = carve(scratch, k_pad);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const uint32_t ksteps = k_pad / 32;
@@ -1347,9 +1420,10 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
                n_tiles / p.tiles_per_block <= kFusedMaxBlocks && share <= kFusedGroupsPerWave &&
                share <= held_groups(xform.kind) && fused_kind_served(call.epilogue, xform.kind);
     };
-    Plan plan = plan_for(n_tiles, ksteps, 4, streams == 1 ? 2 : 1, false);
+    const int max_t = streams == 1 && !call.segments ? 2 : 1;
+    Plan plan = plan_for(n_tiles, ksteps, 4, max_t, false);
     if (!fusable(plan)) {
-        const Plan wide = plan_for(n_tiles, ksteps, 4, streams == 1 ? 2 : 1, true);
+        const Plan wide = plan_for(n_tiles, ksteps, 4, max_t, true);
         if (fusable(wide))
             plan = wide;
     }
@@ -1374,6 +1448,7 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     args.n = call.n;
     args.k_pad = k_pad;
     args.ksteps_per_wave = ksteps / plan.waves;
+    set_segments(args, call);
     const unsigned blocks = n_tiles / plan.tiles_per_block;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {

@@ -208,6 +208,62 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
 }
 
+mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, uint32_t k,
+                                 uint32_t count, const mfh_buf *const *codes,
+                                 const mfh_buf *const *scales, const uint32_t *n,
+                                 float *const *out)
+{
+    if (count == 0 || count > kMaxSegments || m == 0 || m > 2 || xform.kind == XKind::Conv ||
+        !xform.a || (xform.kind == XKind::AddRms && !xform.w) ||
+        (xform.kind == XKind::Swiglu && !xform.b))
+        return fail(ctx, MFH_UNSUPPORTED, "fused decode product needs the matrix-core GEMV");
+    PackedCall call;
+    call.epilogue = Epilogue::Single;
+    call.m = m;
+    call.k = k;
+    call.xform = xform;
+    if (xform.kind == XKind::Plain)
+        call.x = xform.a;
+    call.segments = count;
+    Packed first;
+    for (uint32_t i = 0; i < count; ++i) {
+        Packed p;
+        mfh_status s = check_packed(ctx, codes[i], scales[i], &p);
+        if (s)
+            return s;
+        if (i == 0)
+            first = p;
+        if (p.format != first.format || p.inner != k || p.rows != n[i] || !out[i])
+            return fail(ctx, MFH_INVALID_SHAPE,
+                        "packed linear input width differs from weight width");
+        call.seg[i] = stream_of(codes[i], scales[i]);
+        call.seg_out[i] = out[i];
+        call.seg_n[i] = n[i];
+    }
+    call.format = first.format;
+    call.n = n[0];
+    if (!use_mfma_gemv(ctx, call))
+        return fail(ctx, MFH_UNSUPPORTED, "fused decode product needs the matrix-core GEMV");
+    DeviceGuard guard(ctx->device);
+    for (uint32_t i = 0; i < count; ++i) {
+        Packed p{n[i], k, first.format};
+        mfh_status s = prepare_tiles(ctx, codes[i], scales[i], p, &call.seg[i]);
+        if (s)
+            return s;
+        if (call.seg[i].tiled_half != call.seg[0].tiled_half)
+            return fail(ctx, MFH_UNSUPPORTED, "segment scales differ in width");
+    }
+    call.a.tiled_half = call.seg[0].tiled_half;
+    void *scratch = digits_scratch(ctx, gemv_mfma_scratch_bytes(call));
+    if (!scratch)
+        return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+    call.separate_prologue = ctx->kernel_path == 2;
+    launch_gemv_mfma(ctx->stream, call, scratch);
+    if (hipGetLastError() != hipSuccess)
+        return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
+    return MFH_OK;
+}
+
 }  // namespace mfh
 
 using namespace mfh;

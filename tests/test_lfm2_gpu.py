@@ -78,6 +78,24 @@ def test_prefill_then_teacher_forced_decode(backend, path, mix):
     model.close()
 
 
+@pytest.mark.parametrize("mix", ["mixed", "ternary"])
+def test_decode_past_several_key_ranges(backend, path, mix):
+    # 140 cached keys: the one-launch decode attention splits them into
+    # three 64-key ranges whose records the last block combines; its arrival
+    # counters are reused by every attention layer and step.
+    say("lfm2 long decode", mix, path)
+    cfg, model, ref = build(backend, mix)
+    prompt = convert.token_ids(140, 0x7043_0004, cfg.vocab)
+    model.append(prompt)
+    check_logits(backend.read(model.logits), ref.append(prompt))
+    for _ in range(4):
+        model.sample()
+        token = backend.read(model.sampled)[0]
+        model.append(model.sampled)
+        check_logits(backend.read(model.logits), ref.append([int(token)]))
+    model.close()
+
+
 @pytest.mark.parametrize("mix", ["mixed", "dense-conv-int8"])
 def test_fused_ffn_prefill(backend, mix):
     # >= 96 rows with a packed FFN takes packed_swiglu_pair + packed_linear
