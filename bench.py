@@ -201,6 +201,19 @@ def profile_only(backend, args) -> int:
     if args.profile.startswith("lfm2-"):
         log(json.dumps(lfm2_decode(backend, args.profile[5:])))
         return 0
+    if args.profile == "gemm":
+        n, k, m = 8192, 2048, 2048
+        codes, scales16 = convert.packed_weights(n, k, "ternary", 0x5EED0101)
+        scales = convert.f16_to_f32(scales16)
+        cb = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
+        sb = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
+        xb = backend.upload_f32((m, k), convert.normal((m, k), 0xAC70101 + m))
+        out = backend.allocate_f32((m, n))
+        for _ in range(6):
+            backend.packed_linear(out, xb, cb, sb)
+        backend.synchronize()
+        log(f"gemm ternary M={m} {n}x{k} x 6")
+        return 0
     if args.profile == "copy":
         count = 64 << 20
         src = backend.allocate_f32((count,))
@@ -241,9 +254,11 @@ def main() -> int:
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM cases")
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
-    ap.add_argument("--profile", choices=["dominant", "copy", "lfm2-350m", "lfm2-1.2b"],
+    ap.add_argument("--profile", choices=["dominant", "copy", "lfm2-350m", "lfm2-1.2b", "gemm"],
                     help="run only the dominant operation (or a 256 MiB device copy, the "
-                         "counter calibration) for rocprofv3, and print no JSON line")
+                         "counter calibration, an LFM2 decode, or the ternary "
+                         "M=2048 x 8192x2048 prefill GEMM) for rocprofv3, and print no "
+                         "JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the packed GEMV path on a "
@@ -311,6 +326,7 @@ def main() -> int:
     t0 = time.perf_counter()
     for step in range(args.steps):
         enqueue(0, len(launches), step % args.copies)
+    enqueue_s = time.perf_counter() - t0
     stop.record(stream)
     stop.synchronize()
     wall_s = time.perf_counter() - t0
@@ -377,6 +393,7 @@ def main() -> int:
             "weight_copies": args.copies,
             "bytes_per_step": step_bytes,
             "host_wall_s": round(wall_s, 4),
+            "host_enqueue_ms_per_step": round(enqueue_s * 1e3 / args.steps, 4),
         },
         "roofline": {
             "bound": "hbm",

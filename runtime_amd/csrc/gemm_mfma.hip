@@ -126,25 +126,41 @@ template <Format F> struct Planes {
     static constexpr int value = F == Format::Nf4 ? 2 : 1;
 };
 
-// Decode the 16 codes of one (n, 16-k) chunk to binary16 levels.
+// The 16 codes of one (n, 16-k) chunk as loaded: INT8 16 bytes, ternary 4,
+// NF4 8.
+template <Format F> struct Codes16;
+template <> struct Codes16<Format::Int8> { typedef uint4 type; };
+template <> struct Codes16<Format::Ternary> { typedef unsigned type; };
+template <> struct Codes16<Format::Nf4> { typedef uint2 type; };
+
+// Load one chunk, or the codes of level 0 for a row past n.
 template <Format F>
-__device__ __forceinline__ void decode16(const uint8_t *src, bool live, const _Float16 (*nf)[16],
-                                         v8h (&hi)[2], v8h (&lo)[2])
+__device__ __forceinline__ typename Codes16<F>::type load_codes16(const uint8_t *src, bool live)
+{
+    if constexpr (F == Format::Int8)
+        return live ? *reinterpret_cast<const uint4 *>(src) : uint4{0, 0, 0, 0};
+    else if constexpr (F == Format::Ternary)
+        return live ? *reinterpret_cast<const unsigned *>(src) : 0x55555555u;
+    else
+        return live ? *reinterpret_cast<const uint2 *>(src) : uint2{0x77777777u, 0x77777777u};
+}
+
+// Decode a chunk to binary16 levels (NF4: hi and lo planes).
+template <Format F>
+__device__ __forceinline__ void decode16(const typename Codes16<F>::type &c,
+                                         const _Float16 (*nf)[16], v8h (&hi)[2], v8h (&lo)[2])
 {
     if constexpr (F == Format::Int8) {
-        uint4 w = live ? *reinterpret_cast<const uint4 *>(src) : uint4{0, 0, 0, 0};
-        const unsigned words[4] = {w.x, w.y, w.z, w.w};
+        const unsigned words[4] = {c.x, c.y, c.z, c.w};
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             hi[i / 8][i % 8] = _Float16(float(int8_t(words[i / 4] >> (8 * (i % 4)))));
     } else if constexpr (F == Format::Ternary) {
-        const unsigned w = live ? *reinterpret_cast<const unsigned *>(src) : 0x55555555u;
 #pragma unroll
         for (int i = 0; i < 16; ++i)
-            hi[i / 8][i % 8] = _Float16(float(int((w >> (2 * i)) & 3u) - 1));
+            hi[i / 8][i % 8] = _Float16(float(int((c >> (2 * i)) & 3u) - 1));
     } else {
-        uint2 w = live ? *reinterpret_cast<const uint2 *>(src) : uint2{0x77777777u, 0x77777777u};
-        const unsigned words[2] = {w.x, w.y};
+        const unsigned words[2] = {c.x, c.y};
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const unsigned code = (words[i / 8] >> (4 * (i % 8))) & 15u;
@@ -203,29 +219,37 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
     const _Float16 *a_hi = g.xh + size_t(a_live ? m0 + a_row : 0) * g.k;
     const _Float16 *a_lo = g.xl + size_t(a_live ? m0 + a_row : 0) * g.k;
 
-    v8h a_reg[2][2], b_hi[2], b_lo[2];
-    auto fetch = [&](uint32_t s) {
+    // One stage of this thread's operands as loaded from global memory:
+    // the activation halves and the undecoded codes.  Two such sets are in
+    // flight: stage s + 2 loads while stage s computes from LDS and stage
+    // s + 1 waits in registers to be decoded into LDS.
+    struct Raw {
+        v8h a[2][2];
+        typename Codes16<F>::type b;
+    };
+    auto fetch = [&](uint32_t s, Raw &r) {
         const uint32_t k0 = s * kBK + a_k;
         if (a_live) {
             const v8h *ph = reinterpret_cast<const v8h *>(a_hi + k0);
             const v8h *pl = reinterpret_cast<const v8h *>(a_lo + k0);
-            a_reg[0][0] = ph[0];
-            a_reg[0][1] = ph[1];
-            a_reg[1][0] = pl[0];
-            a_reg[1][1] = pl[1];
+            r.a[0][0] = ph[0];
+            r.a[0][1] = ph[1];
+            r.a[1][0] = pl[0];
+            r.a[1][1] = pl[1];
         } else {
             const v8h z = {};
-            a_reg[0][0] = a_reg[0][1] = a_reg[1][0] = a_reg[1][1] = z;
+            r.a[0][0] = r.a[0][1] = r.a[1][0] = r.a[1][1] = z;
         }
-        decode16<F>(b_src + size_t(s * kBK + b_k) / weights_per_byte(F), b_live, nf, b_hi,
-                    b_lo);
+        r.b = load_codes16<F>(b_src + size_t(s * kBK + b_k) / weights_per_byte(F), b_live);
     };
-    auto store = [&](int buf) {
+    auto store = [&](int buf, const Raw &r) {
 #pragma unroll
         for (int p = 0; p < 2; ++p) {
-            *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k]) = a_reg[p][0];
-            *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k + 8]) = a_reg[p][1];
+            *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k]) = r.a[p][0];
+            *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k + 8]) = r.a[p][1];
         }
+        v8h b_hi[2], b_lo[2];
+        decode16<F>(r.b, nf, b_hi, b_lo);
         *reinterpret_cast<v8h *>(&Bs[buf][b_st][0][b_n][b_k]) = b_hi[0];
         *reinterpret_cast<v8h *>(&Bs[buf][b_st][0][b_n][b_k + 8]) = b_hi[1];
         if constexpr (P == 2) {
@@ -247,13 +271,34 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
 
     const int li = lane & 15, lq = lane >> 4;
     const int row_base = wm * (kBM / 4), col_base = wn * (BNS / 2);
-    fetch(s_begin);
-    store(0);
-    __syncthreads();
-    for (uint32_t s = s_begin; s < s_end; ++s) {
+    // The group's constants, loaded when the group starts and applied when
+    // it ends: 2^e per activation row and the weight scale per column.
+    float gfx[TI][4], gsc[S][TJ];
+    auto load_group_constants = [&](uint32_t grp) {
+#pragma unroll
+        for (int i = 0; i < TI; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const uint32_t mm = m0 + row_base + i * 16 + lq * 4 + r;
+                gfx[i][r] = mm < g.m ? g.factor[size_t(mm) * groups + grp] : 0.0f;
+            }
+#pragma unroll
+        for (int st = 0; st < S; ++st)
+#pragma unroll
+            for (int j = 0; j < TJ; ++j) {
+                const uint32_t nn = n0 + col_base + j * 16 + li;
+                gsc[st][j] = nn < g.n ? g.scales[st][size_t(nn) * groups + grp] : 0.0f;
+            }
+    };
+
+    // One stage: `next` holds stage s + 1 (loaded a stage ago), `freed`
+    // held stage s (already in LDS) and receives stage s + 2.
+    auto step = [&](uint32_t s, Raw &next, Raw &freed) {
         const int buf = (s - s_begin) & 1;
-        if (s + 1 < s_end)
-            fetch(s + 1);
+        if (s + 2 < s_end)
+            fetch(s + 2, freed);
+        if (s % SPG == 0)
+            load_group_constants(s / SPG);
 #pragma unroll
         for (int kb = 0; kb < KB; ++kb) {
             v8h ah[TI], al[TI];
@@ -287,33 +332,33 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
         }
         if (s % SPG == SPG - 1) {
             // Group epilogue: total += group_sum * (2^e[m] * scale[n]).
-            const uint32_t grp = s / SPG;
-            float fx[TI][4];
-#pragma unroll
-            for (int i = 0; i < TI; ++i)
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const uint32_t mm = m0 + row_base + i * 16 + lq * 4 + r;
-                    fx[i][r] = mm < g.m ? g.factor[size_t(mm) * groups + grp] : 0.0f;
-                }
 #pragma unroll
             for (int st = 0; st < S; ++st)
 #pragma unroll
-                for (int j = 0; j < TJ; ++j) {
-                    const uint32_t nn = n0 + col_base + j * 16 + li;
-                    const float sc = nn < g.n ? g.scales[st][size_t(nn) * groups + grp] : 0.0f;
+                for (int j = 0; j < TJ; ++j)
 #pragma unroll
                     for (int i = 0; i < TI; ++i) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
-                            total[st][i][j][r] += acc[st][i][j][r] * (fx[i][r] * sc);
+                            total[st][i][j][r] += acc[st][i][j][r] * (gfx[i][r] * gsc[st][j]);
                         acc[st][i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
                     }
-                }
         }
         if (s + 1 < s_end)
-            store(buf ^ 1);
+            store(buf ^ 1, next);
         __syncthreads();
+    };
+
+    Raw r0, r1;
+    fetch(s_begin, r0);
+    if (s_begin + 1 < s_end)
+        fetch(s_begin + 1, r1);
+    store(0, r0);
+    __syncthreads();
+    for (uint32_t s = s_begin; s < s_end; s += 2) {
+        step(s, r1, r0);
+        if (s + 1 < s_end)
+            step(s + 1, r0, r1);
     }
 
 #pragma unroll
