@@ -8,8 +8,11 @@
 // does.  Reductions the reference runs sequentially (sums of squares, softmax
 // denominators, attention-weighted sums) run here as fixed-shape trees, so
 // results are deterministic run to run and agree with the reference within
-// f32 reassociation error.  Attention scores keep the reference's sequential
-// dot order per key and are bit-identical to it.
+// f32 reassociation error.  The per-row attention kernels keep the
+// reference's sequential dot order per key, so their scores are
+// bit-identical to it; the prefill kernel on fp32 matrix cores sums each
+// score in matrix-core order and takes the online softmax form, also
+// within f32 reassociation error.
 //
 // Unlike the reference's CPU backend, a non-finite intermediate does not
 // raise an error: device work is deferred, so NaN/Inf propagate to the
@@ -648,6 +651,212 @@ __global__ __launch_bounds__(kBlock) void gqa_kernel(float *__restrict__ out,
     }
 }
 
+// ---- prefill attention on fp32 matrix cores ------------------------------
+//
+// Flash-style causal GQA for many (token, query head) pairs.  A block of
+// kFlashWaves waves serves one key/value head and kFlashRows query rows:
+// `tile_tokens` consecutive tokens times the group's query heads (row r is
+// token t0 + r / group, query head r % group of the key/value head).  Key
+// and value rows stream through LDS in kFlashKeys-key tiles that every row
+// of the block shares; each wave owns 16 rows.
+//
+// Per tile, S^T = K Q^T on v_mfma_f32_16x16x4f32 leaves row j of a wave in
+// lane column j: lane 16q + j holds the scores of keys 16c + 4q + r in
+// register r of column block c.  The running maximum, the exponent sum and
+// the output rescale therefore stay in the row's own four lanes (reduced
+// over the lane blocks q).  The output accumulates as O^T = V^T P^T, whose B
+// operand at step (c, r) is the lane's own probability register, and whose
+// result lane 16q + j holds dimensions 16t + 4q + r of row j.
+//
+// Numerics: every score is the exact products summed in matrix-core order,
+// and the softmax takes the online (running maximum) form of the
+// reference's three passes (attention_convolution.rs:90-170); results agree
+// within f32 reassociation error.  A key the causal mask hides gets
+// probability zero, so a non-finite value row later in the same tile still
+// reaches the earlier rows (0 * NaN), where the reference skips it.
+constexpr int kFlashWaves = 4;
+constexpr uint32_t kFlashRows = 16 * kFlashWaves;
+constexpr uint32_t kFlashKeys = 64;
+// Widest head of the fp32 matrix-core path: its key and transposed value
+// tiles stay within 64 KB of LDS.
+constexpr uint32_t kFlashMaxDim = 112;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// K tile [keys][D + 4], then V^T tile [D][keys + 4] (pads keep 16-byte rows
+// and spread the lane blocks over banks).
+template <int D>
+constexpr size_t flash_lds_bytes()
+{
+    return (size_t(kFlashKeys) * (D + 4) + size_t(D) * (kFlashKeys + 4)) * sizeof(float);
+}
+
+template <int D>
+__global__ __launch_bounds__(64 * kFlashWaves) void gqa_flash_kernel(
+    float *__restrict__ out, const float *__restrict__ query, const float *__restrict__ key_cache,
+    const float *__restrict__ value_cache, GqaShape g, uint32_t tile_tokens, uint32_t token_tiles)
+{
+    static_assert(D % 16 == 0 && D <= int(kFlashMaxDim), "head width of the flash path");
+    constexpr uint32_t KS = D + 4, VS = kFlashKeys + 4;
+    constexpr int U = D / 16;                  // 16-wide dimension blocks
+    constexpr int C = kFlashKeys / 16;         // 16-key column blocks
+    constexpr uint32_t QUADS = kFlashKeys * D / 4;  // float4s per tile and matrix
+    constexpr int PER = QUADS / (64 * kFlashWaves);
+    static_assert(QUADS % (64 * kFlashWaves) == 0, "staging shape");
+    extern __shared__ float lds[];
+    float *kl = lds;
+    float *vt = lds + kFlashKeys * KS;
+
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t kv_heads = g.key_value_heads;
+    const uint32_t kv_head = blockIdx.x % kv_heads;
+    // Longest token tiles (most keys) first.
+    const uint32_t tile = token_tiles - 1 - blockIdx.x / kv_heads;
+    const uint64_t t0 = uint64_t(tile) * tile_tokens;
+    const uint64_t t_end = t0 + tile_tokens < g.tokens ? t0 + tile_tokens : g.tokens;
+    const uint64_t k_end = g.initial_len + t_end;  // keys [0, k_end) reach some row
+    const uint64_t kv_width = uint64_t(kv_heads) * D;
+
+    // The lane's row.  Rows past the tile (or past the last token) compute
+    // over every staged key and store nothing.
+    const uint32_t row = 16 * wave + j;
+    const uint32_t group = g.group;
+    const uint64_t token = t0 + row / group;
+    const uint32_t head = kv_head * group + row % group;
+    const bool valid = row < tile_tokens * group && token < g.tokens;
+    const uint64_t last = valid ? g.initial_len + token : k_end - 1;  // last visible key
+
+    // Q^T operand: dimensions 16u + 4q + e of the row at step 4u + e.
+    v4f qv[U];
+    const float *qrow = query + (token * g.query_heads + head) * uint64_t(D);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        qv[u] = valid ? *reinterpret_cast<const v4f *>(qrow + 16 * u + 4 * q) : v4f{0, 0, 0, 0};
+
+    v4f kr[PER], vr[PER];
+    auto stage_load = [&](uint32_t n) {
+        const uint64_t k0 = uint64_t(n) * kFlashKeys;
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const uint32_t f = threadIdx.x + p * 64 * kFlashWaves;
+            const uint32_t key = f / (D / 4), c4 = f % (D / 4);
+            kr[p] = vr[p] = v4f{0, 0, 0, 0};
+            if (k0 + key < k_end) {
+                const size_t at = (k0 + key) * kv_width + uint64_t(kv_head) * D + 4 * c4;
+                kr[p] = *reinterpret_cast<const v4f *>(key_cache + at);
+                vr[p] = *reinterpret_cast<const v4f *>(value_cache + at);
+            }
+        }
+    };
+    auto stage_store = [&]() {
+#pragma unroll
+        for (int p = 0; p < PER; ++p) {
+            const uint32_t f = threadIdx.x + p * 64 * kFlashWaves;
+            const uint32_t key = f / (D / 4), c4 = f % (D / 4);
+            *reinterpret_cast<v4f *>(kl + key * KS + 4 * c4) = kr[p];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                vt[(4 * c4 + e) * VS + key] = vr[p][e];
+        }
+    };
+
+    v4f o[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+        o[u] = v4f{0, 0, 0, 0};
+    float m = -__builtin_inff(), l = 0.0f;
+    const uint32_t tiles = uint32_t((k_end + kFlashKeys - 1) / kFlashKeys);
+    stage_load(0);
+    stage_store();
+    __syncthreads();
+    for (uint32_t n = 0; n < tiles; ++n) {
+        if (n + 1 < tiles)
+            stage_load(n + 1);  // in flight behind this tile's arithmetic
+        // S^T = K Q^T.  A operand of lane (q, i): key 16c + i, dimensions
+        // 16u + 4q + e.
+        v4f s[C];
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+            s[c] = v4f{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            v4f kk[C];
+#pragma unroll
+            for (int c = 0; c < C; ++c)
+                kk[c] = *reinterpret_cast<const v4f *>(kl + (16 * c + j) * KS + 16 * u + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+#pragma unroll
+                for (int c = 0; c < C; ++c)
+                    s[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(kk[c][e], qv[u][e], s[c], 0, 0, 0);
+        }
+        // Scale, causal mask, online softmax over the row's four lanes.
+        const uint64_t k0 = uint64_t(n) * kFlashKeys;
+        float mx = -__builtin_inff();
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float v = s[c][r] * g.scale;
+                if (k0 + 16 * c + 4 * q + r > last)
+                    v = -__builtin_inff();
+                s[c][r] = v;
+                mx = fmaxf(mx, v);
+            }
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float m_new = fmaxf(m, mx);
+        const float alpha = expf(m - m_new);
+        float sum = 0.0f;
+#pragma unroll
+        for (int c = 0; c < C; ++c)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float p = expf(s[c][r] - m_new);
+                s[c][r] = p;
+                sum += p;
+            }
+        sum += __shfl_xor(sum, 16, 64);
+        sum += __shfl_xor(sum, 32, 64);
+        l = l * alpha + sum;
+        m = m_new;
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+            o[u] *= alpha;
+        // O^T += V^T P^T.  A operand of lane (q, i) at step (c, r): V^T row
+        // 16t + i, key 16c + 4q + r.
+#pragma unroll
+        for (int c = 0; c < C; ++c) {
+            v4f vv[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+                vv[u] = *reinterpret_cast<const v4f *>(vt + (16 * u + j) * VS + 16 * c + 4 * q);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+#pragma unroll
+                for (int u = 0; u < U; ++u)
+                    o[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[u][r], s[c][r], o[u], 0, 0, 0);
+        }
+        if (n + 1 < tiles) {
+            __syncthreads();
+            stage_store();
+            __syncthreads();
+        }
+    }
+    if (!valid)
+        return;
+    float *orow = out + (token * g.query_heads + head) * uint64_t(D);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        v4f r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            r[e] = o[u][e] / l;
+        *reinterpret_cast<v4f *>(orow + 16 * u + 4 * q) = r;
+    }
+}
+
 // Split-key attention for few (token, head) pairs (decode): the visible keys
 // of one (token, key/value head) are cut into kSplitKeys-wide ranges, one
 // block per range serving every query head of the group.  The block stages
@@ -1182,6 +1391,43 @@ uint32_t gqa_splits(const GqaShape &g)
     return uint32_t(splits);
 }
 
+// The fp32 matrix-core prefill kernel serves heads of 16..kFlashMaxDim
+// dimensions in steps of 16, groups of at most kFlashRows query heads, and
+// 16-byte aligned operands (its float4 loads and stores).
+bool flash_served(const GqaShape &g, const float *out, const float *query, const float *key_cache,
+                  const float *value_cache)
+{
+    auto aligned = [](const float *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    return g.head_dim && g.head_dim % 16 == 0 && g.head_dim <= kFlashMaxDim && g.group >= 1 &&
+           g.group <= kFlashRows && aligned(out) && aligned(query) && aligned(key_cache) &&
+           aligned(value_cache);
+}
+
+template <int D>
+void launch_flash_d(hipStream_t stream, float *out, const float *query, const float *key_cache,
+                    const float *value_cache, const GqaShape &g)
+{
+    const uint32_t tile_tokens = kFlashRows / g.group;
+    const uint64_t token_tiles = (g.tokens + tile_tokens - 1) / tile_tokens;
+    gqa_flash_kernel<D><<<unsigned(token_tiles * g.key_value_heads), 64 * kFlashWaves,
+                          flash_lds_bytes<D>(), stream>>>(out, query, key_cache, value_cache, g,
+                                                          tile_tokens, uint32_t(token_tiles));
+}
+
+void launch_flash(hipStream_t stream, float *out, const float *query, const float *key_cache,
+                  const float *value_cache, const GqaShape &g)
+{
+    switch (g.head_dim) {
+    case 16: return launch_flash_d<16>(stream, out, query, key_cache, value_cache, g);
+    case 32: return launch_flash_d<32>(stream, out, query, key_cache, value_cache, g);
+    case 48: return launch_flash_d<48>(stream, out, query, key_cache, value_cache, g);
+    case 64: return launch_flash_d<64>(stream, out, query, key_cache, value_cache, g);
+    case 80: return launch_flash_d<80>(stream, out, query, key_cache, value_cache, g);
+    case 96: return launch_flash_d<96>(stream, out, query, key_cache, value_cache, g);
+    default: return launch_flash_d<112>(stream, out, query, key_cache, value_cache, g);
+    }
+}
+
 }  // namespace
 
 size_t gqa_scratch_bytes(const GqaShape &g)
@@ -1213,6 +1459,8 @@ void launch_gqa(hipStream_t stream, float *out, const float *query, const float 
             out, scratch, g.head_dim, splits);
         return;
     }
+    if (flash_served(g, out, query, key_cache, value_cache))
+        return launch_flash(stream, out, query, key_cache, value_cache, g);
     const size_t lds = (size_t(g.head_dim) + kKeyChunk + kBlock) * sizeof(float);
     gqa_kernel<<<unsigned(blocks), kBlock, lds, stream>>>(out, query, key_cache, value_cache, g);
 }

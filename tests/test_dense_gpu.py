@@ -248,6 +248,15 @@ GQA_CASES = [
     (1, 200, 256, 16, 8, 64),        # ragged last range
     (3, 130, 256, 8, 2, 96),         # group of four, 96-wide heads
     (1, 2500, 2561, 32, 8, 64),      # decode at the end of a 2048-token prefill
+    # prefill on the fp32 matrix-core kernel (64-row tiles, 64-key tiles)
+    (130, 0, 256, 32, 8, 64),        # ragged last token tile and key tile
+    (300, 50, 512, 16, 8, 64),       # cached prefix, tiles straddling it
+    (64, 0, 64, 2, 1, 112),          # widest head of the path, one key tile
+    (200, 7, 256, 6, 2, 16),         # group of three: 64-row tiles hold 21 tokens
+    (130, 1000, 1200, 8, 8, 32),     # group of one over a long cached prefix
+    (40, 3, 64, 20, 4, 48),          # group of five
+    (33, 0, 40, 64, 1, 80),          # group of 64: one token per block
+    (512, 0, 512, 32, 8, 64),        # the LFM2-1.2B head layout
 ]
 
 
