@@ -1246,6 +1246,65 @@ __global__ __launch_bounds__(kBlock) void short_conv_kernel(float *__restrict__ 
         history[uint64_t(r) * hidden + channel] = u_at(int64_t(tokens) - history_rows + r);
 }
 
+// The same convolution for many tokens, one thread per (token, channel)
+// output, with the same per-output tap order (bit-identical results).  The
+// history is only read here; conv_roll_kernel rolls it afterwards.
+__global__ __launch_bounds__(kBlock) void conv_tokens_kernel(float *__restrict__ out,
+                                                             const float *__restrict__ projection,
+                                                             const float *__restrict__ kernel,
+                                                             const float *__restrict__ history,
+                                                             uint64_t tokens, uint32_t hidden,
+                                                             uint32_t width)
+{
+    const uint64_t pw = uint64_t(hidden) * 3;
+    const int64_t history_rows = int64_t(width) - 1;
+    const uint64_t count = tokens * hidden, stride = uint64_t(gridDim.x) * kBlock;
+    for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < count; i += stride) {
+        const uint64_t t = i / hidden;
+        const uint32_t channel = uint32_t(i - t * hidden);
+        const float *taps = kernel + uint64_t(channel) * width;
+        float total = 0.0f;
+        for (uint32_t tap = 0; tap < width; ++tap) {
+            const int64_t relative = int64_t(t) + int64_t(tap) - history_rows;
+            float u;
+            if (relative < 0) {
+                u = history[uint64_t(relative + history_rows) * hidden + channel];
+            } else {
+                const float *p = projection + uint64_t(relative) * pw + channel;
+                u = p[0] * p[2 * uint64_t(hidden)];
+            }
+            total += taps[tap] * u;
+        }
+        out[t * hidden + channel] = total * projection[t * pw + hidden + channel];
+    }
+}
+
+// The history roll of short_conv_kernel on its own, one thread per channel.
+__global__ __launch_bounds__(kBlock) void conv_roll_kernel(const float *__restrict__ projection,
+                                                           float *__restrict__ history,
+                                                           uint64_t tokens, uint32_t hidden,
+                                                           uint32_t width)
+{
+    const uint32_t channel = blockIdx.x * kBlock + threadIdx.x;
+    if (channel >= hidden)
+        return;
+    const uint64_t pw = uint64_t(hidden) * 3;
+    const int64_t history_rows = int64_t(width) - 1;
+    for (int64_t r = 0; r < history_rows; ++r) {
+        const int64_t relative = int64_t(tokens) - history_rows + r;
+        float u;
+        if (relative < 0) {
+            // An old row strictly below the one written: read before it is
+            // overwritten, as in short_conv_kernel.
+            u = history[uint64_t(relative + history_rows) * hidden + channel];
+        } else {
+            const float *p = projection + uint64_t(relative) * pw + channel;
+            u = p[0] * p[2 * uint64_t(hidden)];
+        }
+        history[uint64_t(r) * hidden + channel] = u;
+    }
+}
+
 }  // namespace
 
 // ---- launches ----------------------------------------------------------
@@ -1499,8 +1558,18 @@ void launch_short_conv(hipStream_t stream, float *out, const float *projection,
                        const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
                        uint32_t width)
 {
-    short_conv_kernel<<<(hidden + kBlock - 1) / kBlock, kBlock, 0, stream>>>(
+    // A channel walk over few tokens is one launch; many tokens spread over
+    // (token, channel) threads, then the history rolls in a second launch.
+    constexpr uint64_t kWalkTokens = 16;
+    if (tokens <= kWalkTokens) {
+        short_conv_kernel<<<(hidden + kBlock - 1) / kBlock, kBlock, 0, stream>>>(
+            out, projection, kernel, history, tokens, hidden, width);
+        return;
+    }
+    conv_tokens_kernel<<<grid_for(tokens * hidden), kBlock, 0, stream>>>(
         out, projection, kernel, history, tokens, hidden, width);
+    conv_roll_kernel<<<(hidden + kBlock - 1) / kBlock, kBlock, 0, stream>>>(projection, history,
+                                                                           tokens, hidden, width);
 }
 
 }  // namespace mfh

@@ -275,7 +275,10 @@ def test_causal_gqa(backend, tokens, start, cap, qh, kvh, d):
 
 
 @pytest.mark.parametrize("tokens,hidden,width", [(1, 1024, 3), (1, 2048, 3), (7, 2053, 3),
-                                                 (1, 64, 1), (2, 100, 4), (5, 16, 2), (1, 1, 3)])
+                                                 (1, 64, 1), (2, 100, 4), (5, 16, 2), (1, 1, 3),
+                                                 # (token, channel) threads + separate roll
+                                                 (17, 2048, 3), (300, 1000, 3), (2048, 2048, 3),
+                                                 (20, 33, 25), (40, 7, 1)])
 def test_gated_short_convolution_bitwise(backend, tokens, hidden, width):
     say("gated_short_convolution", tokens, hidden, width)
     projection = rng_f32(60 + tokens, (tokens, 3 * hidden))
