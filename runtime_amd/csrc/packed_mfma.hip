@@ -757,6 +757,169 @@ __device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF, HALF> &blk
     }
 }
 
+// ---------------------------------------------------------------------------
+// Register prologue (m <= 4, activations as stored).  Each wave forms the
+// digit fragments of its own loop blocks, one block ahead of the MFMAs,
+// from the raw activations: no LDS, no barrier, no separate kernel.
+// Lane 16q + 4b + p loads x[b][64s + 16q + 4p + t] (t = 0..3) of every
+// kstep s, and it supplies digit row p of batch b in the MFMA A operand.
+// Per group, the exponent and the ternary correction reduce over the 16
+// lanes that hold the batch (lane quad, lane blocks); the quad then shares
+// its 16 offset values and each lane packs digit p of all of them.  The
+// arithmetic is emit_group's value for value, so the fragments, factors and
+// corrections are the bytes digits_kernel would write.
+// ---------------------------------------------------------------------------
+constexpr int kRegPro = 16;
+
+template <int LB>
+struct RegX {
+    v4f v[LB];
+};
+
+// Quad lane exchanges (DPP quad_perm): the value of lane l ^ 1, l ^ 2.
+__device__ __forceinline__ unsigned quad_xor1(unsigned v)
+{
+    return unsigned(__builtin_amdgcn_mov_dpp(int(v), 0xB1, 0xF, 0xF, false));
+}
+__device__ __forceinline__ unsigned quad_xor2(unsigned v)
+{
+    return unsigned(__builtin_amdgcn_mov_dpp(int(v), 0x4E, 0xF, 0xF, false));
+}
+
+// 4 x 4 byte transpose: r[i] byte j = w[j] byte (REV ? 3 - i : i).
+// v_perm_b32 selector bytes 0-3 pick bytes of its second operand, 4-7 of
+// its first.
+template <bool REV>
+__device__ __forceinline__ void byte_transpose(const unsigned (&w)[4], unsigned (&r)[4])
+{
+    // Pairs of rows: (w0.b_i, w1.b_i) for two i per dword.
+    const unsigned sa = REV ? 0x06020703u : 0x05010400u;  // i = 0, 1 (REV: bytes 3, 2)
+    const unsigned sb = REV ? 0x04000501u : 0x07030602u;  // i = 2, 3 (REV: bytes 1, 0)
+    const unsigned a01 = __builtin_amdgcn_perm(w[1], w[0], sa);
+    const unsigned b01 = __builtin_amdgcn_perm(w[1], w[0], sb);
+    const unsigned a23 = __builtin_amdgcn_perm(w[3], w[2], sa);
+    const unsigned b23 = __builtin_amdgcn_perm(w[3], w[2], sb);
+    r[0] = __builtin_amdgcn_perm(a23, a01, 0x05040100u);
+    r[1] = __builtin_amdgcn_perm(a23, a01, 0x07060302u);
+    r[2] = __builtin_amdgcn_perm(b23, b01, 0x05040100u);
+    r[3] = __builtin_amdgcn_perm(b23, b01, 0x07060302u);
+}
+
+// 4 x 4 transpose across a lane quad: lane p ends with r[P] = register p of
+// quad lane P (two butterfly stages).
+__device__ __forceinline__ void quad_transpose(unsigned (&r)[4], uint32_t p)
+{
+    unsigned m[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned other = quad_xor1(r[i ^ 1]);
+        m[i] = (p & 1) == unsigned(i & 1) ? r[i] : other;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const unsigned other = quad_xor2(m[i ^ 2]);
+        r[i] = (p & 2) == unsigned(i & 2) ? m[i] : other;
+    }
+}
+
+// Loop block `index` of this lane's activation values (zeros past k or for
+// batch slots at or beyond m).
+template <int LB>
+__device__ __forceinline__ void reg_load(RegX<LB> &rx, const float *xrow, bool live, uint32_t k,
+                                         uint32_t s0, uint32_t index)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t off = 16 * (lane >> 4) + 4 * (lane & 3);
+#pragma unroll
+    for (int kk = 0; kk < LB; ++kk) {
+        const uint32_t kx = 64 * (s0 + index * LB + kk) + off;
+        rx.v[kk] = live && kx < k ? *reinterpret_cast<const v4f *>(xrow + kx)
+                                  : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+template <Format F, int T, int S, bool HALF>
+__device__ __forceinline__ void reg_digits(const RegX<Geo<F>::lb> &rx,
+                                           I8Block<F, T, S, 1, HALF> &blk)
+{
+    using B = I8Block<F, T, S, 1, HALF>;
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t p = lane & 3, q = lane >> 4;
+    const unsigned flip = p ? 0x80808080u : 0u;
+#pragma unroll
+    for (int gg = 0; gg < B::GPB; ++gg) {
+        // Largest magnitude as bits: |x| orders like its bit pattern, and a
+        // pattern at or above infinity's marks a non-finite group.
+        unsigned mb = 0;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                mb = max(mb, __float_as_uint(rx.v[2 * gg + kk][t]) & 0x7FFFFFFFu);
+        mb = max(mb, quad_xor1(mb));
+        mb = max(mb, quad_xor2(mb));
+        mb = max(mb, unsigned(__shfl_xor(int(mb), 16, 64)));
+        mb = max(mb, unsigned(__shfl_xor(int(mb), 32, 64)));
+        const bool bad = mb >= 0x7F800000u;
+        int e = 0;
+        if (!bad && mb)
+            frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+        const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
+        long long corr = 0;
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int ks = 2 * gg + kk;
+            unsigned vp[4];
+            int u_prev = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                int val = bad ? 0 : int(rintf(ldexpf(rx.v[ks][t], 30 - e)));
+                if constexpr (F == Format::Ternary) {
+                    // Field t of the nested masks (see the operand-field note).
+                    const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
+                    val = t == 0 ? u : u - u_prev;
+                    u_prev = u;
+                    corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
+                                  : -(static_cast<long long>(u) << 6);
+                }
+                vp[t] = unsigned(val + 0x808080);
+            }
+            // d[D] byte t = digit D of value t (digit D is byte 3 - D of the
+            // offset form); after the quad transpose d[P] byte t = digit p of
+            // quad lane P's value t, i.e. of lane-block value c = 4P + t.
+            unsigned d[4];
+            byte_transpose<true>(vp, d);
+            quad_transpose(d, p);
+            unsigned w[4];
+            if constexpr (F == Format::Ternary) {
+                byte_transpose<false>(d, w);  // ternary byte 4t + P: dword t, byte P
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    w[i] = d[i];             // INT8 byte c = 4P + t: dword P, byte t
+            }
+            blk.af[ks][0] = v4i{int(w[0] ^ flip), int(w[1] ^ flip), int(w[2] ^ flip),
+                                int(w[3] ^ flip)};
+        }
+        // Lane (q, j) applies batch q's constants: lane 4q holds them.
+        blk.xf[gg][0] = __shfl(factor, int(4 * q), 64);
+        if constexpr (F == Format::Ternary) {
+            corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
+                    (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
+            corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
+                    (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
+            corr += __shfl_xor(corr, 16, 64);
+            corr += __shfl_xor(corr, 32, 64);
+            // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
+            const long long lo = ((corr + 32768) & 65535) - 32768;
+            const int hi = int((corr - lo) >> 16);
+            blk.cv[gg][0] = int2{__shfl(hi, int(4 * q), 64), __shfl(int(lo), int(4 * q), 64)};
+        } else {
+            blk.cv[gg][0] = int2{0, 0};
+        }
+    }
+}
+
 // Bytes of dynamic LDS past the reduction area that the in-kernel prologue
 // uses: the live rows (4 per batch row) of the digit fragments of all of K,
 // then 4 slots of group factors and corrections.
@@ -835,7 +998,35 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
             }
         }
     };
-    if constexpr (PRO >= 0) {
+    if constexpr (PRO == kRegPro) {
+        static_assert(NF == 1, "the register prologue serves m <= 4");
+        // Activation loads go out ahead of the same block's weights, so a
+        // block's digits can form while its weights are still arriving.
+        const uint32_t b = (lane >> 2) & 3;
+        const float *xrow = a.xform.a + size_t(b < a.m ? b : 0) * a.k;
+        const bool live = b < a.m;
+        RegX<B::LB> rx0, rx1;
+        if (nblk > 0) {
+            reg_load(rx0, xrow, live, a.k, s_begin, 0);
+            i8_load_w(buf0, wp, sp, 0);
+        }
+        for (uint32_t i = 0; i < nblk; i += 2) {
+            if (i + 1 < nblk) {
+                reg_load(rx1, xrow, live, a.k, s_begin, i + 1);
+                i8_load_w(buf1, wp, sp, i + 1);
+            }
+            reg_digits(rx0, buf0);
+            i8_compute(buf0, accf);
+            if (i + 1 < nblk) {
+                if (i + 2 < nblk) {
+                    reg_load(rx0, xrow, live, a.k, s_begin, i + 2);
+                    i8_load_w(buf0, wp, sp, i + 2);
+                }
+                reg_digits(rx1, buf1);
+                i8_compute(buf1, accf);
+            }
+        }
+    } else if constexpr (PRO >= 0) {
         static_assert(NF == 1, "the in-kernel prologue serves m <= 2");
         extern __shared__ float lds_dyn[];
         __shared__ float rms_scratch[8];
@@ -1168,7 +1359,7 @@ template <Format F, int T, int S, int NF, bool HALF, Epilogue E, int PRO>
 void launch_i8_kernel(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves)
 {
     size_t lds = reduce_lds_bytes<S, NF>(waves, T);
-    if constexpr (PRO >= 0)
+    if constexpr (PRO >= 0 && PRO != kRegPro)
         lds += fused_bytes(args.k_pad, args.m);
     gemv_i8_kernel<F, T, S, NF, HALF, E, PRO><<<blocks, 64 * waves, lds, stream>>>(args);
 }
@@ -1178,6 +1369,8 @@ void launch_i8_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, in
 {
     if constexpr (NF == 1) {
         switch (pro) {
+        case kRegPro:
+            return launch_i8_kernel<F, T, S, NF, HALF, E, kRegPro>(stream, args, blocks, waves);
         case int(XKind::Plain):
             return launch_i8_kernel<F, T, S, NF, HALF, E, 0>(stream, args, blocks, waves);
         case int(XKind::AddRms):
@@ -1365,8 +1558,17 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     }
     plan.tiles_per_block = tiles_of(plan);
     const bool fused = fusable(plan);
-    const int pro = fused ? int(xform.kind) : -1;
-    if (!fused)
+    // Otherwise plain activations of at most four rows form their digits in
+    // the GEMV's registers (16-byte aligned rows for its float4 loads).
+    // Ternary operands cost more arithmetic per group (the field telescoping
+    // and the correction): past two groups per wave the separate prologue
+    // kernel measured faster (65536 x 2048: 13.3 against 14.4 us).
+    const uint32_t wave_groups = ksteps / plan.waves / 2;
+    const bool reg = !fused && !call.separate_prologue && xform.kind == XKind::Plain &&
+                     call.m <= 4 && reinterpret_cast<uintptr_t>(xform.a) % 16 == 0 &&
+                     (F != Format::Ternary || wave_groups <= 2);
+    const int pro = fused ? int(xform.kind) : reg ? kRegPro : -1;
+    if (!fused && !reg)
         digits_kernel<F>
             <<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 4 * nf), 64 * kPrologueWaves,
                0, stream>>>(xform, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag),

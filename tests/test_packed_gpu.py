@@ -109,6 +109,25 @@ def test_decode_gemv_sweep_shapes(backend, path, scheme, m, n, k):
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("n,k", [(16384, 2048), (4608, 1024), (1024, 1024), (2048, 8192)])
+def test_non_finite_activations_poison_their_rows(backend, path, scheme, n, k):
+    """A NaN or infinity in an activation row makes that row's outputs
+    non-finite (device backends surface it through argmax rather than a
+    per-op check, inference.rs:125-131); the other rows are unaffected."""
+    say("non-finite rows", scheme, path, n, k)
+    m = 4
+    codes, scales = make_weights(n, k, scheme, 0x5EED0300 + n + k)
+    x = convert.normal((m, k), 0xAC70300 + k)
+    x[1, 300] = np.nan
+    x[2, 5] = np.inf
+    x[3, k - 1] = -np.inf
+    got = run_linear(backend, x, codes, scales)
+    assert not np.isfinite(got[1:]).any()
+    want = oracle.packed_linear_threaded(x[:1], codes, scales)
+    assert_close(got[:1], want, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
 def test_lm_head_shape(backend, scheme):
     say("lm head", scheme)
     n, k, m = 65536, 2048, 2
