@@ -15,10 +15,10 @@ from HBM rather than the 256 MB Infinity Cache.
 steps (HIP events on the backend's stream), where a launch's bytes are
 N*K*b/8 + (N*K/128)*2 + B*K*4 + B*N*4 (codes at b = 2/4/8 bits, scales at
 their stored FP16 width, activations, outputs).  The roofline object is for
-the dominant operation (the 65536x2048 INT8 head at B=1, an activation
-prologue kernel plus the GEMV kernel): its bytes over its average duration
-across back-to-back launches on rotating copies, against the 8 TB/s HBM
-peak.
+the dominant operation (the 65536x2048 INT8 head at B=1, one GEMV kernel
+that forms its activation digits in registers): its bytes over its average
+duration across back-to-back launches on rotating copies, against the
+8 TB/s HBM peak.
 """
 from __future__ import annotations
 
@@ -36,10 +36,10 @@ SHAPES = [(1024, 1024), (4608, 1024), (2048, 2048), (8192, 2048), (2048, 8192), 
 BATCHES = [1, 2, 4, 8]
 HBM_PEAK_GBS = 8000.0
 DOMINANT = ("int8", (65536, 2048), 1)
-# HBM bytes per dominant launch (prologue + GEMV) from rocprofv3 FETCH_SIZE
+# HBM bytes per dominant launch (one GEMV kernel) from rocprofv3 FETCH_SIZE
 # and WRITE_SIZE runs of `--profile dominant`, scaled by the same counters
 # over `--profile copy` (profiles/int8_gemv_65536x2048_b1.md).
-DOMINANT_TRAFFIC_BYTES = 137_163_747
+DOMINANT_TRAFFIC_BYTES = 136_726_339
 
 
 def algorithmic_bytes(n: int, k: int, b: int, fmt: str) -> int:
@@ -334,8 +334,7 @@ def main() -> int:
 
     # Dominant operation: back-to-back launches over rotating weight copies
     # (each launch streams its matrix from HBM), bracketed by one event pair
-    # on the backend's stream.  One launch is the activation prologue kernel
-    # plus the GEMV kernel.
+    # on the backend's stream.  One launch is one GEMV kernel.
     di = launches.index(DOMINANT)
     dom_reps = 8 * args.copies
     for r in range(args.copies):
