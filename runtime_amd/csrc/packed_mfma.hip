@@ -770,6 +770,10 @@ __device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF, HALF> &blk
 // corrections are the bytes digits_kernel would write.
 // ---------------------------------------------------------------------------
 constexpr int kRegPro = 16;
+// Largest K range per wave (in 64-wide ksteps) of the register prologue of
+// the add + RMS norm, which holds the whole range while the row's squares
+// reduce.
+constexpr int kRegNormSteps = 4;
 
 template <int LB>
 struct RegX {
@@ -1023,6 +1027,76 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
                     i8_load_w(buf0, wp, sp, i + 2);
                 }
                 reg_digits(rx1, buf1);
+                i8_compute(buf1, accf);
+            }
+        }
+    } else if constexpr (PRO == kRegPro + int(XKind::AddRms)) {
+        static_assert(NF == 1, "the register prologue serves m <= 4");
+        // s = a + b over the wave's whole K range (at most kRegNormSteps
+        // ksteps), every wave's squares summed per batch row, then
+        // x = (s * reciprocal) * weight as in the separate prologue.
+        constexpr int KS = kRegNormSteps;
+        constexpr int NB = KS / B::LB;  // loop blocks held
+        __shared__ float rms_part[8][4];  // [wave][batch slot]
+        const XForm &t = a.xform;
+        const uint32_t b = (lane >> 2) & 3;
+        const bool live = b < a.m;
+        const size_t row = size_t(live ? b : 0) * a.k;
+        const uint32_t steps = a.ksteps_per_wave;
+        const uint32_t off = 16 * (lane >> 4) + 4 * (lane & 3);
+        auto at = [&](int ks) { return 64 * (s_begin + ks) + off; };
+        v4f xs[KS], ys[KS], ws[KS];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const bool in = uint32_t(ks) < steps && at(ks) < a.k;
+            xs[ks] = ys[ks] = ws[ks] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            if (in && live)
+                xs[ks] = *reinterpret_cast<const v4f *>(t.a + row + at(ks));
+            if (in && live && t.b)
+                ys[ks] = *reinterpret_cast<const v4f *>(t.b + row + at(ks));
+            if (in)
+                ws[ks] = *reinterpret_cast<const v4f *>(t.w + at(ks));
+        }
+        if (nblk > 0)
+            i8_load_w(buf0, wp, sp, 0);
+        if (nblk > 1)
+            i8_load_w(buf1, wp, sp, 1);
+        float squares = 0.0f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (t.b)
+                xs[ks] = xs[ks] + ys[ks];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                squares += xs[ks][e] * xs[ks][e];
+        }
+        squares += __shfl_xor(squares, 1, 64);
+        squares += __shfl_xor(squares, 2, 64);
+        squares += __shfl_xor(squares, 16, 64);
+        squares += __shfl_xor(squares, 32, 64);
+        if ((lane & 0x33) == 0)  // lane 4b: one per batch slot
+            rms_part[wave][b] = squares;
+        __syncthreads();
+        float total = 0.0f;
+        for (uint32_t w = 0; w < blockDim.x / 64; ++w)
+            total += rms_part[w][b];
+        const float reciprocal = rms_reciprocal(total, a.k, t.epsilon);
+        RegX<B::LB> rx[NB];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            if (blockIdx.x == 0 && t.side && live && uint32_t(ks) < steps && at(ks) < a.k)
+                *reinterpret_cast<v4f *>(t.side + row + at(ks)) = xs[ks];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                rx[ks / B::LB].v[ks % B::LB][e] = (xs[ks][e] * reciprocal) * ws[ks][e];
+        }
+        if (nblk > 0) {
+            reg_digits(rx[0], buf0);
+            i8_compute(buf0, accf);
+        }
+        if constexpr (NB > 1) {
+            if (nblk > 1) {
+                reg_digits(rx[1], buf1);
                 i8_compute(buf1, accf);
             }
         }
@@ -1359,7 +1433,7 @@ template <Format F, int T, int S, int NF, bool HALF, Epilogue E, int PRO>
 void launch_i8_kernel(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves)
 {
     size_t lds = reduce_lds_bytes<S, NF>(waves, T);
-    if constexpr (PRO >= 0 && PRO != kRegPro)
+    if constexpr (PRO >= 0 && PRO < kRegPro)
         lds += fused_bytes(args.k_pad, args.m);
     gemv_i8_kernel<F, T, S, NF, HALF, E, PRO><<<blocks, 64 * waves, lds, stream>>>(args);
 }
@@ -1371,6 +1445,9 @@ void launch_i8_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, in
         switch (pro) {
         case kRegPro:
             return launch_i8_kernel<F, T, S, NF, HALF, E, kRegPro>(stream, args, blocks, waves);
+        case kRegPro + int(XKind::AddRms):
+            return launch_i8_kernel<F, T, S, NF, HALF, E, kRegPro + int(XKind::AddRms)>(
+                stream, args, blocks, waves);
         case int(XKind::Plain):
             return launch_i8_kernel<F, T, S, NF, HALF, E, 0>(stream, args, blocks, waves);
         case int(XKind::AddRms):
@@ -1550,25 +1627,46 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     };
     // Segmented launches keep one tile per block.
     const int max_t = streams == 1 && !call.segments ? 4 : 1;
-    Plan plan = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, false);
-    if (!fusable(plan)) {
-        const Plan wide = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, true);
-        if (fusable(wide))
-            plan = wide;
+    const Plan narrow = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, false);
+    const Plan wide = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, true);
+    // The register prologue serves plain activations, and the add + RMS norm
+    // when each wave's K range is at most kRegNormSteps ksteps (it holds them
+    // all while the row's squares reduce), for at most four rows with 16-byte
+    // aligned operands.  Ternary operands cost more arithmetic per group
+    // (the field telescoping and the correction): past two groups per wave
+    // the separate prologue kernel measured faster (65536 x 2048: 13.3
+    // against 14.4 us).
+    auto aligned = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    auto reg_ok = [&](Plan p) {
+        const uint32_t per_wave = ksteps / p.waves;
+        if (call.separate_prologue || call.m > 4 || (F == Format::Ternary && per_wave / 2 > 2))
+            return false;
+        if (xform.kind == XKind::Plain)
+            return aligned(xform.a);
+        if (xform.kind == XKind::AddRms)
+            return per_wave <= uint32_t(kRegNormSteps) && aligned(xform.a) && aligned(xform.b) &&
+                   aligned(xform.w) && aligned(xform.side);
+        return false;
+    };
+    // Preference: the register prologue for the norm, then the LDS one,
+    // then the register prologue for plain activations, then the separate
+    // prologue kernel.  The 8-wave plan takes the norm only with one tile per
+    // block: the 4-tile norm kernel holds two waves per SIMD, too few for the
+    // LM head's 8-wave blocks (1.2B-shape decode 1389 -> 1355 tok/s).
+    Plan plan = narrow;
+    int pro = -1;
+    const bool reg_wide = reg_ok(wide) && tiles_of(wide) == 1;
+    if (xform.kind == XKind::AddRms && (reg_ok(narrow) || reg_wide)) {
+        plan = reg_ok(narrow) ? narrow : wide;
+        pro = kRegPro + int(XKind::AddRms);
+    } else if (fusable(narrow) || fusable(wide)) {
+        plan = fusable(narrow) ? narrow : wide;
+        pro = int(xform.kind);
+    } else if (reg_ok(narrow)) {
+        pro = kRegPro;
     }
     plan.tiles_per_block = tiles_of(plan);
-    const bool fused = fusable(plan);
-    // Otherwise plain activations of at most four rows form their digits in
-    // the GEMV's registers (16-byte aligned rows for its float4 loads).
-    // Ternary operands cost more arithmetic per group (the field telescoping
-    // and the correction): past two groups per wave the separate prologue
-    // kernel measured faster (65536 x 2048: 13.3 against 14.4 us).
-    const uint32_t wave_groups = ksteps / plan.waves / 2;
-    const bool reg = !fused && !call.separate_prologue && xform.kind == XKind::Plain &&
-                     call.m <= 4 && reinterpret_cast<uintptr_t>(xform.a) % 16 == 0 &&
-                     (F != Format::Ternary || wave_groups <= 2);
-    const int pro = fused ? int(xform.kind) : reg ? kRegPro : -1;
-    if (!fused && !reg)
+    if (pro < 0)
         digits_kernel<F>
             <<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 4 * nf), 64 * kPrologueWaves,
                0, stream>>>(xform, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag),
