@@ -1220,6 +1220,97 @@ __device__ __forceinline__ void nf4_compute(const Nf4Block<T, S, HALF> &blk,
         }
 }
 
+// Weights and group scales of NF4 loop block `index`.
+template <int T, int S, bool HALF>
+__device__ __forceinline__ void nf4_load_w(Nf4Block<T, S, HALF> &blk,
+                                           const v4u *const (&wp)[S][T],
+                                           const typename ScaleT<HALF>::type *const (&sp)[S][T],
+                                           uint32_t index)
+{
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            blk.w[st][t] = wp[st][t][index * 64];
+            blk.sc[st][t] = sp[st][t][index * 16];
+        }
+}
+
+// NF4 register prologue (m <= 4).  Lane 16q + 2b + h supplies half h (0:
+// hi, 1: lo) of batch b in the f16 A operand, eight values
+// k = 32s + 8q + 0..7 per 32-wide kstep s.  The lane pair splits them:
+// lane h loads values 4h..4h+3 (k offset nf4_reg_offset), splits them
+// into binary16 hi and lo, keeps its own half and sends its partner the
+// other (DPP).  The group exponent reduces over the batch's eight lanes
+// (the pair and the lane blocks).  The arithmetic is halves_kernel's value
+// for value.
+__device__ __forceinline__ uint32_t nf4_reg_offset()
+{
+    const uint32_t lane = threadIdx.x & 63;
+    return 8 * (lane >> 4) + 4 * (lane & 1);
+}
+
+__device__ __forceinline__ void nf4_reg_load(RegX<4> &rx, const float *xrow, bool live,
+                                             uint32_t k, uint32_t s0, uint32_t index)
+{
+    const uint32_t off = nf4_reg_offset();
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        const uint32_t kx = 32 * (s0 + index * 4 + kk) + off;
+        rx.v[kk] = live && kx < k ? *reinterpret_cast<const v4f *>(xrow + kx)
+                                  : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
+__device__ __forceinline__ unsigned pack_halves(_Float16 lo_k, _Float16 hi_k)
+{
+    return unsigned(__builtin_bit_cast(unsigned short, lo_k)) |
+           (unsigned(__builtin_bit_cast(unsigned short, hi_k)) << 16);
+}
+
+template <int T, int S, bool HALF>
+__device__ __forceinline__ void nf4_reg_halves(const RegX<4> &rx, Nf4Block<T, S, HALF> &blk)
+{
+    const uint32_t lane = threadIdx.x & 63;
+    const uint32_t h = lane & 1, q = lane >> 4;
+    unsigned mb = 0;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            mb = max(mb, __float_as_uint(rx.v[kk][t]) & 0x7FFFFFFFu);
+    mb = max(mb, quad_xor1(mb));
+    mb = max(mb, unsigned(__shfl_xor(int(mb), 16, 64)));
+    mb = max(mb, unsigned(__shfl_xor(int(mb), 32, 64)));
+    const bool bad = mb >= 0x7F800000u;
+    int e = 0;
+    if (!bad && mb)
+        frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+    const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+        unsigned mine[2], recv[2];
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+            const float v0 = bad ? 0.0f : ldexpf(rx.v[kk][2 * pr], -e);
+            const float v1 = bad ? 0.0f : ldexpf(rx.v[kk][2 * pr + 1], -e);
+            const _Float16 h0 = _Float16(v0), h1 = _Float16(v1);
+            const _Float16 l0 = _Float16(v0 - float(h0)), l1 = _Float16(v1 - float(h1));
+            const unsigned hi_pair = pack_halves(h0, h1), lo_pair = pack_halves(l0, l1);
+            mine[pr] = h ? lo_pair : hi_pair;
+            recv[pr] = quad_xor1(h ? hi_pair : lo_pair);  // the partner's half h
+        }
+        // Values 0..3 of the lane block come from lane h = 0, 4..7 from h = 1.
+        const v4u d = h ? v4u{recv[0], recv[1], mine[0], mine[1]}
+                        : v4u{mine[0], mine[1], recv[0], recv[1]};
+        blk.af[kk] = __builtin_bit_cast(v8h, d);
+    }
+    // Lane (q, j) applies the factors of batches 2q and 2q + 1: lanes 4q and
+    // 4q + 2 hold them.
+    blk.xf[0] = __shfl(factor, int(4 * q), 64);
+    blk.xf[1] = __shfl(factor, int(4 * q + 2), 64);
+}
+
 template <int T, int S, bool HALF, Epilogue E, int PRO>
 __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
 {
@@ -1272,10 +1363,9 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
         for (int t = 0; t < T; ++t)
             accf[st][t][0] = accf[st][t][1] = 0.0f;
 
+    // buf0 holds loop block 0 on entry.
     Nf4Block<T, S, HALF> buf0, buf1;
     auto main_loop = [&](const auto &ap) {
-        if (nblk > 0)
-            nf4_load(buf0, wp, sp, ap, xp, 0);
         for (uint32_t i = 0; i < nblk; i += 2) {
             if (i + 1 < nblk)
                 nf4_load(buf1, wp, sp, ap, xp, i + 1);
@@ -1287,7 +1377,32 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
             }
         }
     };
-    if constexpr (PRO >= 0) {
+    if constexpr (PRO == kRegPro) {
+        const uint32_t b = (lane >> 1) & 7;
+        const bool live = b < a.m;
+        const float *xrow = a.xform.a + size_t(live ? b : 0) * a.k;
+        RegX<4> rx0, rx1;
+        if (nblk > 0) {
+            nf4_reg_load(rx0, xrow, live, a.k, s_begin, 0);
+            nf4_load_w(buf0, wp, sp, 0);
+        }
+        for (uint32_t i = 0; i < nblk; i += 2) {
+            if (i + 1 < nblk) {
+                nf4_reg_load(rx1, xrow, live, a.k, s_begin, i + 1);
+                nf4_load_w(buf1, wp, sp, i + 1);
+            }
+            nf4_reg_halves(rx0, buf0);
+            nf4_compute(buf0, accf, lut);
+            if (i + 1 < nblk) {
+                if (i + 2 < nblk) {
+                    nf4_reg_load(rx0, xrow, live, a.k, s_begin, i + 2);
+                    nf4_load_w(buf0, wp, sp, i + 2);
+                }
+                nf4_reg_halves(rx1, buf1);
+                nf4_compute(buf1, accf, lut);
+            }
+        }
+    } else if constexpr (PRO >= 0) {
         extern __shared__ float lds_dyn[];
         __shared__ float rms_scratch[8];
         const uint32_t waves = blockDim.x >> 6;
@@ -1304,12 +1419,18 @@ __global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
         __syncthreads();
         xp[0] = fxf + (2 * q) * groups + g_begin;
         xp[1] = fxf + (2 * q + 1) * groups + g_begin;
-        main_loop(LdsFrag<v8h>{reinterpret_cast<const v8h *>(frag) + (size_t(s_begin) * 4 + q) * rp +
+        const LdsFrag<v8h> lap{reinterpret_cast<const v8h *>(frag) + (size_t(s_begin) * 4 + q) * rp +
                                    j,
-                               4 * rp, j < rp});
+                               4 * rp, j < rp};
+        if (nblk > 0)
+            nf4_load(buf0, wp, sp, lap, xp, 0);
+        main_loop(lap);
     } else {
-        main_loop(GlobalFrag<v8h>{reinterpret_cast<const v8h *>(a.afrag) + size_t(s_begin) * 64 +
-                                  lane});
+        const GlobalFrag<v8h> gap{reinterpret_cast<const v8h *>(a.afrag) + size_t(s_begin) * 64 +
+                                  lane};
+        if (nblk > 0)
+            nf4_load(buf0, wp, sp, gap, xp, 0);
+        main_loop(gap);
     }
     const uint32_t batch[2] = {2 * q, 2 * q + 1};
     reduce_and_store<S, T, 2, E>(a.m, tg, accf, batch, j);
@@ -1501,7 +1622,7 @@ template <int T, int S, bool HALF, Epilogue E, int PRO>
 void launch_nf4_kernel(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves)
 {
     size_t lds = reduce_lds_bytes<S, 2>(waves, T);
-    if constexpr (PRO >= 0)
+    if constexpr (PRO >= 0 && PRO < kRegPro)
         lds += fused_bytes_nf4(args.k_pad, args.m);
     gemv_nf4_kernel<T, S, HALF, E, PRO><<<blocks, 64 * waves, lds, stream>>>(args);
 }
@@ -1510,6 +1631,8 @@ template <int T, int S, bool HALF, Epilogue E>
 void launch_nf4_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, int waves, int pro)
 {
     switch (pro) {
+    case kRegPro:
+        return launch_nf4_kernel<T, S, HALF, E, kRegPro>(stream, args, blocks, waves);
     case int(XKind::Plain):
         return launch_nf4_kernel<T, S, HALF, E, 0>(stream, args, blocks, waves);
     case int(XKind::AddRms):
@@ -1721,15 +1844,23 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
                share <= held_groups(xform.kind) && fused_kind_served(call.epilogue, xform.kind);
     };
     const int max_t = streams == 1 && !call.segments ? 2 : 1;
-    Plan plan = plan_for(n_tiles, ksteps, 4, max_t, false);
-    if (!fusable(plan)) {
-        const Plan wide = plan_for(n_tiles, ksteps, 4, max_t, true);
-        if (fusable(wide))
-            plan = wide;
+    const Plan narrow = plan_for(n_tiles, ksteps, 4, max_t, false);
+    const Plan wide = plan_for(n_tiles, ksteps, 4, max_t, true);
+    // Register prologue for plain activations of at most four rows (16-byte
+    // aligned) over at most 256 k per wave.  NF4 forms twice the operand
+    // values per k of the integer formats next to its table decode, and past
+    // that share (the 65536 x 2048 head, K = 8192), at eight rows, or for the
+    // add + RMS norm the separate or LDS prologue measured faster.
+    Plan plan = narrow;
+    int pro = -1;
+    if (fusable(narrow) || fusable(wide)) {
+        plan = fusable(narrow) ? narrow : wide;
+        pro = int(xform.kind);
+    } else if (!call.separate_prologue && xform.kind == XKind::Plain && call.m <= 4 &&
+               ksteps / narrow.waves <= 8 && reinterpret_cast<uintptr_t>(xform.a) % 16 == 0) {
+        pro = kRegPro;
     }
-    const bool fused = fusable(plan);
-    const int pro = fused ? int(xform.kind) : -1;
-    if (!fused)
+    if (pro < 0)
         halves_kernel<<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 8),
                         64 * kPrologueWaves, 0, stream>>>(xform, call.m, call.k, groups,
                                                           static_cast<_Float16 *>(sc.afrag), sc.xf);
