@@ -15,12 +15,22 @@
 //   power of two, so this equals the reference's scale * dot.  NF4 drops
 //   the lo * lo product, which is below 2^-22 of each term.
 //
-// Tiling.  A 512-lane block computes a 128 (m) x 128 (n) output tile, split
-// over S weight streams of 128 / S columns each.  Eight waves (4 x 2) own
-// 32 x 64 (S = 1) or 32 x 32-per-stream (S = 2) pieces.  K advances in
-// kBK-wide stages: the activation halves and the decoded weight levels are
-// staged through LDS, double buffered.  The load of stage s + 1 runs from
-// global memory while stage s feeds the MFMAs.
+// Operands.  B (the weights) is read straight from the decode GEMV's
+// repacked tiles: 16 rows x K per tile, one 16-byte load per lane covering
+// 64 (INT8), 128 (NF4) or 256 (ternary) k, already in the MFMA lane order.
+// Each wave decodes its tiles to binary16 in registers (INT8 and ternary by
+// placing the code under a binary16 exponent of 1024 and subtracting, NF4
+// through a 256-entry LDS table of level halves), so weights never pass
+// through LDS.  A, the activation halves, is staged through LDS, double
+// buffered, one stage ahead in registers.  Within a 64-wide stage, MFMA
+// half h takes k = 16q + 8h + 0..7 of lane block q (INT8, ternary: the
+// tiles' byte order) or k = 32h + 8q + 0..7 (NF4: its 32-wide kstep).
+//
+// Tiling.  A 256-lane block (2 x 2 waves) computes a 128 (m) x 128 (n)
+// output tile, split over S weight streams of 128 / S columns each; a wave
+// owns 64 x 64 (4 x 4 MFMA tiles, 4 / S column tiles per stream), with a
+// group accumulator and a running total per MFMA tile.  The 74 KB of LDS
+// lets two blocks share a CU.
 //
 // Grid mapping.  Workgroups are dealt round-robin to the 8 XCDs.  Block b
 // computes tile (b % 8) * (tiles / 8) + b / 8, so each XCD's L2 holds a
@@ -36,18 +46,19 @@ namespace mfh {
 namespace {
 
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v2h __attribute__((ext_vector_type(2)));
 typedef float v4f __attribute__((ext_vector_type(4)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
-#ifndef MFH_GEMM_KBK
-#define MFH_GEMM_KBK 64
-#endif
-constexpr int kThreads = 512;     // 8 waves: 4 (m) x 2 (n)
-constexpr int kBM = 128;          // rows per block tile
-constexpr int kBN = 128;          // columns per block tile (all streams)
-constexpr int kBK = MFH_GEMM_KBK; // k per stage (32 or 64: whole MFMA k-blocks)
-// LDS row pitch in halves: kBK + 8 (80 or 144 bytes) puts the 16 rows read
-// by one lane group on distinct banks.
+constexpr int kThreads = 256;  // 4 waves: 2 (m) x 2 (n)
+constexpr int kBM = 128;       // rows per block tile
+constexpr int kBN = 128;       // columns per block tile (all streams)
+constexpr int kBK = 64;        // k per stage
+// LDS row pitch in halves: kBK + 8 (144 bytes) puts the 16 rows read by one
+// lane group on distinct banks.
 constexpr int kRow = kBK + 8;
+constexpr int kTI = 4;  // 16-row MFMA tiles per wave
+constexpr int kTJ = 4;  // 16-column MFMA tiles per wave, all streams
 
 __constant__ float kLevels[16] = {
     -1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f,
@@ -111,86 +122,105 @@ __global__ __launch_bounds__(64) void split_kernel(const float *__restrict__ x, 
 
 struct GemmArgs {
     const _Float16 *xh, *xl;
-    const float *factor;  // [m, k / 128]
-    const uint8_t *codes[2];
-    const float *scales[2];
+    const float *factor;       // [m, k / 128]
+    const uint8_t *wtiles[2];  // repacked codes per stream
+    const void *scales[2];     // tiled scales per stream: [tile][groups_pad][16]
     float *out[2];
-    float *partial;       // split-K: [chunk][stream][m][n] raw sums
+    float *partial;            // split-K: [chunk][stream][m][n] raw sums
     uint32_t m, n, k;
-    uint32_t tiles_n, tiles;
-    uint32_t chunks;      // K split into `chunks` runs of whole groups
+    uint32_t n_tiles;          // 16-row tiles of each repacked stream
+    uint32_t tile_vecs;        // 16-byte lane loads per tile (of 64 lanes)
+    uint32_t groups_pad;       // tiled scale groups per tile
+    uint32_t tiles_n, tiles;   // output block tiles along n, and in all
+    uint32_t chunks;           // K split into `chunks` runs of whole groups
 };
 
-// Level planes of one weight stream: NF4 needs hi and lo.
-template <Format F> struct Planes {
-    static constexpr int value = F == Format::Nf4 ? 2 : 1;
+// 64-wide stages covered by one 16-byte lane load of a tile.
+template <Format F> struct Chunk {
+    static constexpr int stages = F == Format::Int8 ? 1 : F == Format::Nf4 ? 2 : 4;
 };
 
-// The 16 codes of one (n, 16-k) chunk as loaded: INT8 16 bytes, ternary 4,
-// NF4 8.
-template <Format F> struct Codes16;
-template <> struct Codes16<Format::Int8> { typedef uint4 type; };
-template <> struct Codes16<Format::Ternary> { typedef unsigned type; };
-template <> struct Codes16<Format::Nf4> { typedef uint2 type; };
-
-// Load one chunk, or the codes of level 0 for a row past n.
-template <Format F>
-__device__ __forceinline__ typename Codes16<F>::type load_codes16(const uint8_t *src, bool live)
+template <bool HALF>
+__device__ __forceinline__ float scale_at(const void *p, size_t i)
 {
-    if constexpr (F == Format::Int8)
-        return live ? *reinterpret_cast<const uint4 *>(src) : uint4{0, 0, 0, 0};
-    else if constexpr (F == Format::Ternary)
-        return live ? *reinterpret_cast<const unsigned *>(src) : 0x55555555u;
+    if constexpr (HALF)
+        return __half2float(static_cast<const __half *>(p)[i]);
     else
-        return live ? *reinterpret_cast<const uint2 *>(src) : uint2{0x77777777u, 0x77777777u};
+        return static_cast<const float *>(p)[i];
 }
 
-// Decode a chunk to binary16 levels (NF4: hi and lo planes).
-template <Format F>
-__device__ __forceinline__ void decode16(const typename Codes16<F>::type &c,
-                                         const _Float16 (*nf)[16], v8h (&hi)[2], v8h (&lo)[2])
+// INT8 bytes 8h..8h+7 of the lane's 16 (k = 16q + 8h + 0..7): binary16
+// 1024 + (b ^ 0x80) is exact, and subtracting 1152 leaves the signed code.
+__device__ __forceinline__ v8h decode_i8(const v4u &raw, int h)
 {
-    if constexpr (F == Format::Int8) {
-        const unsigned words[4] = {c.x, c.y, c.z, c.w};
+    const v2h bias = {_Float16(-1152.0f), _Float16(-1152.0f)};
+    v8h out;
 #pragma unroll
-        for (int i = 0; i < 16; ++i)
-            hi[i / 8][i % 8] = _Float16(float(int8_t(words[i / 4] >> (8 * (i % 4)))));
-    } else if constexpr (F == Format::Ternary) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i)
-            hi[i / 8][i % 8] = _Float16(float(int((c >> (2 * i)) & 3u) - 1));
-    } else {
-        const unsigned words[2] = {c.x, c.y};
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const unsigned code = (words[i / 8] >> (4 * (i % 8))) & 15u;
-            hi[i / 8][i % 8] = nf[0][code];
-            lo[i / 8][i % 8] = nf[1][code];
-        }
+    for (int d = 0; d < 2; ++d) {
+        const unsigned x = raw[2 * h + d] ^ 0x80808080u;
+        // v_perm_b32 selector bytes 0-3 pick bytes of its second operand, 4-7
+        // of its first: [x.b0, 0x64, x.b1, 0x64] and [x.b2, 0x64, x.b3, 0x64].
+        const v2h a = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, x, 0x04010400u)) +
+                      bias;
+        const v2h b = __builtin_bit_cast(v2h, __builtin_amdgcn_perm(0x64646464u, x, 0x04030402u)) +
+                      bias;
+        out[4 * d] = a[0];
+        out[4 * d + 1] = a[1];
+        out[4 * d + 2] = b[0];
+        out[4 * d + 3] = b[1];
     }
+    return out;
 }
 
-template <Format F, int S, Epilogue E>
-__global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
+// Ternary tile dword (16 codes, k = 16q + 4e + f at byte e, field f; field 3
+// stored as (c + 2) mod 4), bytes 2h and 2h + 1: binary16 1024 + c minus
+// 1025 is c - 1.
+__device__ __forceinline__ v8h decode_ternary(unsigned w, int h)
 {
-    constexpr int P = Planes<F>::value;
-    constexpr int BNS = kBN / S;       // columns per stream
-    constexpr int TI = kBM / 4 / 16;   // 16-row tiles per wave (4 wave rows)
-    constexpr int TJ = BNS / 2 / 16;   // 16-column tiles per stream per wave (2 wave columns)
-    constexpr int KB = kBK / 32;       // MFMA k-blocks per stage
-    constexpr int SPG = 128 / kBK;     // stages per 128-group
-    __shared__ _Float16 As[2][2][kBM][kRow];          // [stage][hi, lo][row][k]
-    __shared__ _Float16 Bs[2][S][P][BNS][kRow];       // [stage][stream][plane][n][k]
-    __shared__ _Float16 nf[2][16];
+    const v2h bias = {_Float16(-1025.0f), _Float16(-1025.0f)};
+    w ^= 0x80808080u;                              // canonical codes
+    const unsigned even = w & 0x33333333u;         // fields 0, 2 of each byte
+    const unsigned odd = (w >> 2) & 0x33333333u;   // fields 1, 3
+    v8h out;
+#pragma unroll
+    for (int e2 = 0; e2 < 2; ++e2) {
+        const unsigned e = unsigned(2 * h + e2);
+        // [even.b_e, even.b_e, odd.b_e, odd.b_e]: each 16-bit lane's low
+        // byte carries (field f, field f + 2) of one parity.
+        const unsigned d = __builtin_amdgcn_perm(odd, even, e | (e << 8) | ((4 + e) << 16) |
+                                                                ((4 + e) << 24));
+        const v2h a = __builtin_bit_cast(v2h, (d & 0x00030003u) | 0x64006400u) + bias;
+        const v2h b = __builtin_bit_cast(v2h, ((d >> 4) & 0x00030003u) | 0x64006400u) + bias;
+        out[4 * e2] = a[0];      // field 0
+        out[4 * e2 + 1] = a[1];  // field 1
+        out[4 * e2 + 2] = b[0];  // field 2
+        out[4 * e2 + 3] = b[1];  // field 3
+    }
+    return out;
+}
+
+template <Format F, int S, Epilogue E, bool HALF>
+__global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
+{
+    constexpr int P = F == Format::Nf4 ? 2 : 1;  // weight level planes
+    constexpr int TJS = kTJ / S;                 // column tiles per stream per wave
+    constexpr int BNS = kBN / S;                 // block columns per stream
+    constexpr int SPC = Chunk<F>::stages;
+    __shared__ _Float16 As[2][2][kBM][kRow];  // [stage][hi, lo][row][k]
+    __shared__ float fac[2][kBM];                // 2^e per row, by group parity
+    __shared__ uint2 lut[F == Format::Nf4 ? 256 : 1];
 
     if constexpr (F == Format::Nf4) {
-        if (threadIdx.x < 16) {
-            const float l = kLevels[threadIdx.x];
-            const _Float16 h = _Float16(l);
-            nf[0][threadIdx.x] = h;
-            nf[1][threadIdx.x] = _Float16(l - float(h));
-        }
-        __syncthreads();
+        // Entry for one code byte: x = hi halves of (low nibble, high nibble),
+        // y = lo halves, each a packed binary16 pair for consecutive k.
+        const uint32_t e = threadIdx.x;
+        const float l0 = kLevels[e & 15], l1 = kLevels[e >> 4];
+        const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
+        const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
+        lut[e] = uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
+                           (unsigned(__builtin_bit_cast(unsigned short, h1)) << 16),
+                       unsigned(__builtin_bit_cast(unsigned short, r0)) |
+                           (unsigned(__builtin_bit_cast(unsigned short, r1)) << 16)};
     }
 
     // XCD-aware tile order over (chunk, tile) blocks.
@@ -200,177 +230,173 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
         block = (blockIdx.x % 8) * (blocks / 8) + blockIdx.x / 8;
     const uint32_t chunk = block / g.tiles, tile = block % g.tiles;
     const uint32_t m0 = (tile / g.tiles_n) * kBM, n0 = (tile % g.tiles_n) * BNS;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // Wave-uniform, so the tile addresses live in scalar registers.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
+    const int li = lane & 15, lq = lane >> 4;
     const uint32_t groups = g.k / 128;
     const uint32_t chunk_stages = g.k / kBK / g.chunks;
     const uint32_t s_begin = chunk * chunk_stages, s_end = s_begin + chunk_stages;
-    const size_t row_bytes = size_t(g.k) / weights_per_byte(F);
 
-    // Global -> register staging, 16 consecutive k per thread and operand:
-    // A = (row, k part) of both halves; B = (stream, n, k part).
-    constexpr int APR = kBK / 16;  // A threads per row
-    const uint32_t a_row = tid / APR, a_k = (tid % APR) * 16;
+    // A staging: thread -> (row, 32-wide k half) of both activation halves.
+    const uint32_t a_row = tid >> 1, a_k = (tid & 1) * 32;
     const bool a_live = m0 + a_row < g.m;
-    const uint32_t b_st = tid / (kThreads / S), b_local = tid % (kThreads / S);
-    const uint32_t b_n = b_local / APR, b_k = (b_local % APR) * 16;
-    const bool b_live = n0 + b_n < g.n;
-    const uint8_t *b_src = g.codes[b_st] + size_t(b_live ? n0 + b_n : 0) * row_bytes;
-    const _Float16 *a_hi = g.xh + size_t(a_live ? m0 + a_row : 0) * g.k;
-    const _Float16 *a_lo = g.xl + size_t(a_live ? m0 + a_row : 0) * g.k;
-
-    // One stage of this thread's operands as loaded from global memory:
-    // the activation halves and the undecoded codes.  Two such sets are in
-    // flight: stage s + 2 loads while stage s computes from LDS and stage
-    // s + 1 waits in registers to be decoded into LDS.
-    struct Raw {
-        v8h a[2][2];
-        typename Codes16<F>::type b;
+    const _Float16 *a_src[2] = {g.xh + size_t(a_live ? m0 + a_row : 0) * g.k + a_k,
+                                g.xl + size_t(a_live ? m0 + a_row : 0) * g.k + a_k};
+    struct ARaw {
+        v8h v[2][4];
     };
-    auto fetch = [&](uint32_t s, Raw &r) {
-        const uint32_t k0 = s * kBK + a_k;
-        if (a_live) {
-            const v8h *ph = reinterpret_cast<const v8h *>(a_hi + k0);
-            const v8h *pl = reinterpret_cast<const v8h *>(a_lo + k0);
-            r.a[0][0] = ph[0];
-            r.a[0][1] = ph[1];
-            r.a[1][0] = pl[0];
-            r.a[1][1] = pl[1];
-        } else {
-            const v8h z = {};
-            r.a[0][0] = r.a[0][1] = r.a[1][0] = r.a[1][1] = z;
-        }
-        r.b = load_codes16<F>(b_src + size_t(s * kBK + b_k) / weights_per_byte(F), b_live);
-    };
-    auto store = [&](int buf, const Raw &r) {
+    auto fetch_a = [&](uint32_t s, ARaw &r) {
 #pragma unroll
-        for (int p = 0; p < 2; ++p) {
-            *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k]) = r.a[p][0];
-            *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k + 8]) = r.a[p][1];
-        }
-        v8h b_hi[2], b_lo[2];
-        decode16<F>(r.b, nf, b_hi, b_lo);
-        *reinterpret_cast<v8h *>(&Bs[buf][b_st][0][b_n][b_k]) = b_hi[0];
-        *reinterpret_cast<v8h *>(&Bs[buf][b_st][0][b_n][b_k + 8]) = b_hi[1];
-        if constexpr (P == 2) {
-            *reinterpret_cast<v8h *>(&Bs[buf][b_st][1][b_n][b_k]) = b_lo[0];
-            *reinterpret_cast<v8h *>(&Bs[buf][b_st][1][b_n][b_k + 8]) = b_lo[1];
-        }
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                r.v[p][u] = a_live ? *reinterpret_cast<const v8h *>(a_src[p] + s * kBK + 8 * u)
+                                   : v8h{};
+    };
+    auto store_a = [&](int buf, const ARaw &r) {
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k + 8 * u]) = r.v[p][u];
     };
 
-    v4f acc[S][TI][TJ], total[S][TI][TJ];
+    // The wave's weight tiles: column tile jt is tile tt of stream jt / TJS.
+    const v4u *wptr[kTJ];
+    const void *sptr[kTJ];
+    bool wlive[kTJ];
 #pragma unroll
-    for (int st = 0; st < S; ++st)
+    for (int jt = 0; jt < kTJ; ++jt) {
+        const int st = jt / TJS, tt = jt % TJS;
+        const uint32_t t = n0 / 16 + wn * TJS + tt;
+        wlive[jt] = t < g.n_tiles;
+        wptr[jt] = reinterpret_cast<const v4u *>(g.wtiles[st]) +
+                   size_t(wlive[jt] ? t : 0) * g.tile_vecs + lane;
+        sptr[jt] = HALF ? static_cast<const void *>(static_cast<const __half *>(g.scales[st]) +
+                                                    size_t(wlive[jt] ? t : 0) * g.groups_pad * 16 +
+                                                    li)
+                        : static_cast<const void *>(static_cast<const float *>(g.scales[st]) +
+                                                    size_t(wlive[jt] ? t : 0) * g.groups_pad * 16 +
+                                                    li);
+    }
+    v4u cur[kTJ];
+    auto load_chunk = [&](uint32_t c, v4u (&dst)[kTJ]) {
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                acc[st][i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                total[st][i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            }
+        for (int jt = 0; jt < kTJ; ++jt)
+            dst[jt] = wlive[jt] ? wptr[jt][size_t(c) * 64] : v4u{0u, 0u, 0u, 0u};
+    };
 
-    const int li = lane & 15, lq = lane >> 4;
-    const int row_base = wm * (kBM / 4), col_base = wn * (BNS / 2);
-    // The group's constants, loaded when the group starts and applied when
-    // it ends: 2^e per activation row and the weight scale per column.
-    float gfx[TI][4], gsc[S][TJ];
+    v4f acc[kTI][kTJ], total[kTI][kTJ];
+#pragma unroll
+    for (int i = 0; i < kTI; ++i)
+#pragma unroll
+        for (int jt = 0; jt < kTJ; ++jt) {
+            acc[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            total[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+
+    // Group constants: the block's 2^e per activation row go to LDS when the
+    // group starts (read at its end, two barriers later); each lane loads
+    // the weight scale of its columns.
+    float gsc[kTJ];
     auto load_group_constants = [&](uint32_t grp) {
+        if (tid < kBM) {
+            const uint32_t mm = m0 + tid;
+            fac[grp & 1][tid] = mm < g.m ? g.factor[size_t(mm) * groups + grp] : 0.0f;
+        }
 #pragma unroll
-        for (int i = 0; i < TI; ++i)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const uint32_t mm = m0 + row_base + i * 16 + lq * 4 + r;
-                gfx[i][r] = mm < g.m ? g.factor[size_t(mm) * groups + grp] : 0.0f;
-            }
-#pragma unroll
-        for (int st = 0; st < S; ++st)
-#pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const uint32_t nn = n0 + col_base + j * 16 + li;
-                gsc[st][j] = nn < g.n ? g.scales[st][size_t(nn) * groups + grp] : 0.0f;
-            }
+        for (int jt = 0; jt < kTJ; ++jt)
+            gsc[jt] = scale_at<HALF>(sptr[jt], size_t(grp) * 16);
     };
 
-    // One stage: `next` holds stage s + 1 (loaded a stage ago), `freed`
-    // held stage s (already in LDS) and receives stage s + 2.
-    auto step = [&](uint32_t s, Raw &next, Raw &freed) {
+    ARaw ra;
+    fetch_a(s_begin, ra);
+    load_chunk(s_begin / SPC, cur);
+    store_a(0, ra);
+    load_group_constants(s_begin / 2);
+    __syncthreads();
+
+    for (uint32_t s = s_begin; s < s_end; ++s) {
         const int buf = (s - s_begin) & 1;
-        if (s + 2 < s_end)
-            fetch(s + 2, freed);
-        if (s % SPG == 0)
-            load_group_constants(s / SPG);
+        if (s + 1 < s_end)
+            fetch_a(s + 1, ra);
+        if (s % 2 == 0 && s != s_begin)
+            load_group_constants(s / 2);
 #pragma unroll
-        for (int kb = 0; kb < KB; ++kb) {
-            v8h ah[TI], al[TI];
+        for (int h = 0; h < 2; ++h) {
+            v8h bh[kTJ], bl[kTJ];
 #pragma unroll
-            for (int i = 0; i < TI; ++i) {
-                const int row = row_base + i * 16 + li;
-                ah[i] = *reinterpret_cast<const v8h *>(&As[buf][0][row][kb * 32 + lq * 8]);
-                al[i] = *reinterpret_cast<const v8h *>(&As[buf][1][row][kb * 32 + lq * 8]);
-            }
+            for (int jt = 0; jt < kTJ; ++jt) {
+                if constexpr (F == Format::Int8) {
+                    bh[jt] = decode_i8(cur[jt], h);
+                } else if constexpr (F == Format::Ternary) {
+                    bh[jt] = decode_ternary(cur[jt][s % 4], h);
+                } else {
+                    const unsigned word = cur[jt][2 * (s % 2) + h];
+                    v4u hi, lo;
 #pragma unroll
-            for (int st = 0; st < S; ++st)
-#pragma unroll
-                for (int j = 0; j < TJ; ++j) {
-                    const int nrow = col_base + j * 16 + li;
-                    const v8h bh =
-                        *reinterpret_cast<const v8h *>(&Bs[buf][st][0][nrow][kb * 32 + lq * 8]);
-                    v8h bl;
-                    if constexpr (P == 2)
-                        bl = *reinterpret_cast<const v8h *>(
-                            &Bs[buf][st][1][nrow][kb * 32 + lq * 8]);
-#pragma unroll
-                    for (int i = 0; i < TI; ++i) {
-                        v4f c = acc[st][i][j];
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bh, c, 0, 0, 0);
-                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al[i], bh, c, 0, 0, 0);
-                        if constexpr (P == 2)
-                            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah[i], bl, c, 0, 0, 0);
-                        acc[st][i][j] = c;
+                    for (int p = 0; p < 4; ++p) {
+                        const uint2 e = lut[(word >> (8 * p)) & 255u];
+                        hi[p] = e.x;
+                        lo[p] = e.y;
                     }
+                    bh[jt] = __builtin_bit_cast(v8h, hi);
+                    bl[jt] = __builtin_bit_cast(v8h, lo);
                 }
+            }
+            // The chunk's last decode: its registers take the next chunk,
+            // in flight behind this half's MFMAs.
+            if (h == 1 && (s + 1) % SPC == 0 && s + 1 < s_end)
+                load_chunk((s + 1) / SPC, cur);
+            const int koff = F == Format::Nf4 ? 32 * h + 8 * lq : 16 * lq + 8 * h;
+#pragma unroll
+            for (int i = 0; i < kTI; ++i) {
+                const int row = wm * 64 + i * 16 + li;
+                const v8h ah = *reinterpret_cast<const v8h *>(&As[buf][0][row][koff]);
+                const v8h al = *reinterpret_cast<const v8h *>(&As[buf][1][row][koff]);
+#pragma unroll
+                for (int jt = 0; jt < kTJ; ++jt) {
+                    v4f c = acc[i][jt];
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[jt], c, 0, 0, 0);
+                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[jt], c, 0, 0, 0);
+                    if constexpr (P == 2)
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[jt], c, 0, 0, 0);
+                    acc[i][jt] = c;
+                }
+            }
         }
-        if (s % SPG == SPG - 1) {
+        if (s % 2 == 1) {
             // Group epilogue: total += group_sum * (2^e[m] * scale[n]).
 #pragma unroll
-            for (int st = 0; st < S; ++st)
+            for (int i = 0; i < kTI; ++i) {
+                const v4f gfx =
+                    *reinterpret_cast<const v4f *>(&fac[(s / 2) & 1][wm * 64 + i * 16 + lq * 4]);
 #pragma unroll
-                for (int j = 0; j < TJ; ++j)
+                for (int jt = 0; jt < kTJ; ++jt) {
 #pragma unroll
-                    for (int i = 0; i < TI; ++i) {
-#pragma unroll
-                        for (int r = 0; r < 4; ++r)
-                            total[st][i][j][r] += acc[st][i][j][r] * (gfx[i][r] * gsc[st][j]);
-                        acc[st][i][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                    }
+                    for (int r = 0; r < 4; ++r)
+                        total[i][jt][r] += acc[i][jt][r] * (gfx[r] * gsc[jt]);
+                    acc[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
         }
         if (s + 1 < s_end)
-            store(buf ^ 1, next);
+            store_a(buf ^ 1, ra);
         __syncthreads();
-    };
-
-    Raw r0, r1;
-    fetch(s_begin, r0);
-    if (s_begin + 1 < s_end)
-        fetch(s_begin + 1, r1);
-    store(0, r0);
-    __syncthreads();
-    for (uint32_t s = s_begin; s < s_end; s += 2) {
-        step(s, r1, r0);
-        if (s + 1 < s_end)
-            step(s + 1, r0, r1);
     }
 
 #pragma unroll
-    for (int i = 0; i < TI; ++i)
+    for (int i = 0; i < kTI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t mm = m0 + row_base + i * 16 + lq * 4 + r;
+            const uint32_t mm = m0 + wm * 64 + i * 16 + lq * 4 + r;
             if (mm >= g.m)
                 continue;
 #pragma unroll
-            for (int j = 0; j < TJ; ++j) {
-                const uint32_t nn = n0 + col_base + j * 16 + li;
+            for (int tt = 0; tt < TJS; ++tt) {
+                const uint32_t nn = n0 + (wn * TJS + tt) * 16 + li;
                 if (nn >= g.n)
                     continue;
                 const size_t o = size_t(mm) * g.n + nn;
@@ -379,16 +405,17 @@ __global__ __launch_bounds__(kThreads) void gemm_mfma_kernel(GemmArgs g)
                     const size_t plane = size_t(g.m) * g.n;
 #pragma unroll
                     for (int st = 0; st < S; ++st)
-                        g.partial[(size_t(chunk) * S + st) * plane + o] = total[st][i][j][r];
+                        g.partial[(size_t(chunk) * S + st) * plane + o] =
+                            total[i][st * TJS + tt][r];
                     continue;
                 }
                 if constexpr (E == Epilogue::Single) {
-                    g.out[0][o] = total[0][i][j][r];
+                    g.out[0][o] = total[i][tt][r];
                 } else if constexpr (E == Epilogue::Pair) {
-                    g.out[0][o] = total[0][i][j][r];
-                    g.out[1][o] = total[S - 1][i][j][r];
+                    g.out[0][o] = total[i][tt][r];
+                    g.out[1][o] = total[i][(S - 1) * TJS + tt][r];
                 } else {
-                    g.out[0][o] = silu_mul(total[0][i][j][r], total[S - 1][i][j][r]);
+                    g.out[0][o] = silu_mul(total[i][tt][r], total[i][(S - 1) * TJS + tt][r]);
                 }
             }
         }
@@ -422,47 +449,44 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(float *__restrict__ 
     }
 }
 
-template <Format F>
-void launch_format(hipStream_t stream, const PackedCall &call, const GemmArgs &args)
+template <Format F, int S, Epilogue E>
+void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half)
 {
     const unsigned grid = args.tiles * args.chunks;
-    const size_t plane = size_t(args.m) * args.n;
-    const unsigned rgrid = unsigned(std::min<size_t>((plane + 255) / 256, 65536));
-    switch (call.epilogue) {
-    case Epilogue::Single:
-        gemm_mfma_kernel<F, 1, Epilogue::Single><<<grid, kThreads, 0, stream>>>(args);
-        if (args.chunks > 1)
-            splitk_reduce_kernel<1, Epilogue::Single><<<rgrid, 256, 0, stream>>>(
-                args.out[0], args.out[1], args.partial, plane, args.chunks);
-        break;
-    case Epilogue::Pair:
-        gemm_mfma_kernel<F, 2, Epilogue::Pair><<<grid, kThreads, 0, stream>>>(args);
-        if (args.chunks > 1)
-            splitk_reduce_kernel<2, Epilogue::Pair><<<rgrid, 256, 0, stream>>>(
-                args.out[0], args.out[1], args.partial, plane, args.chunks);
-        break;
-    case Epilogue::SwigluPair:
-        gemm_mfma_kernel<F, 2, Epilogue::SwigluPair><<<grid, kThreads, 0, stream>>>(args);
-        if (args.chunks > 1)
-            splitk_reduce_kernel<2, Epilogue::SwigluPair><<<rgrid, 256, 0, stream>>>(
-                args.out[0], args.out[1], args.partial, plane, args.chunks);
-        break;
+    if (half)
+        gemm_mfma_kernel<F, S, E, true><<<grid, kThreads, 0, stream>>>(args);
+    else
+        gemm_mfma_kernel<F, S, E, false><<<grid, kThreads, 0, stream>>>(args);
+    if (args.chunks > 1) {
+        const size_t plane = size_t(args.m) * args.n;
+        const unsigned rgrid = unsigned(std::min<size_t>((plane + 255) / 256, 65536));
+        splitk_reduce_kernel<S, E><<<rgrid, 256, 0, stream>>>(args.out[0], args.out[1],
+                                                              args.partial, plane, args.chunks);
     }
 }
 
-// K chunks for a grid of `tiles` output tiles: enough to give every CU a
-// block, in whole groups, each chunk at least 4 groups deep.
+template <Format F>
+void launch_format(hipStream_t stream, const PackedCall &call, const GemmArgs &args, bool half)
+{
+    switch (call.epilogue) {
+    case Epilogue::Single:
+        return launch_epilogue<F, 1, Epilogue::Single>(stream, args, half);
+    case Epilogue::Pair:
+        return launch_epilogue<F, 2, Epilogue::Pair>(stream, args, half);
+    case Epilogue::SwigluPair:
+        return launch_epilogue<F, 2, Epilogue::SwigluPair>(stream, args, half);
+    }
+}
+
+// K chunks for a grid of `tiles` output tiles: enough to give every CU two
+// blocks, in whole groups, each chunk at least 4 groups deep.
 uint32_t split_chunks(uint32_t tiles, uint32_t groups)
 {
     uint32_t chunks = 1;
-    while (tiles * chunks * 2 <= 256 && groups % (chunks * 2) == 0 && groups / (chunks * 2) >= 4)
+    while (tiles * chunks * 2 <= 512 && groups % (chunks * 2) == 0 && groups / (chunks * 2) >= 4)
         chunks *= 2;
     return chunks;
 }
-
-}  // namespace
-
-namespace {
 
 uint32_t tiles_of(const PackedCall &call, uint32_t *tiles_n)
 {
@@ -491,26 +515,37 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     _Float16 *xl = xh + size_t(call.m) * call.k;
     float *factor = reinterpret_cast<float *>(xl + size_t(call.m) * call.k);
     split_kernel<<<dim3(groups, call.m), 64, 0, stream>>>(call.x, call.m, call.k, xh, xl, factor);
+    // The repacked tiles pad K to 256 (ternary) or 128; one 16-byte lane load
+    // covers 64 (INT8), 128 (NF4) or 256 (ternary) k.
+    const uint32_t align = call.format == Format::Ternary ? 256 : 128;
+    const uint32_t k_pad = (call.k + align - 1) / align * align;
+    const uint32_t chunk_k =
+        call.format == Format::Int8 ? 64 : call.format == Format::Nf4 ? 128 : 256;
     GemmArgs args{};
     args.xh = xh;
     args.xl = xl;
     args.factor = factor;
-    args.codes[0] = call.a.codes;
-    args.codes[1] = call.b.codes;
-    args.scales[0] = call.a.scales;
-    args.scales[1] = call.b.scales;
+    args.wtiles[0] = call.a.tiles;
+    args.wtiles[1] = call.b.tiles;
+    args.scales[0] = call.a.tiled_scales;
+    args.scales[1] = call.b.tiled_scales;
     args.out[0] = call.out_a;
     args.out[1] = call.out_b;
     args.m = call.m;
     args.n = call.n;
     args.k = call.k;
+    args.n_tiles = (call.n + 63) / 64 * 4;
+    args.tile_vecs = k_pad / chunk_k * 64;
+    args.groups_pad = k_pad / 128;
     args.tiles = tiles_of(call, &args.tiles_n);
     args.chunks = split_chunks(args.tiles, groups);
     args.partial = factor + size_t(call.m) * groups;
+    const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
+    const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     switch (call.format) {
-    case Format::Ternary: launch_format<Format::Ternary>(stream, call, args); break;
-    case Format::Nf4: launch_format<Format::Nf4>(stream, call, args); break;
-    case Format::Int8: launch_format<Format::Int8>(stream, call, args); break;
+    case Format::Ternary: launch_format<Format::Ternary>(stream, call, args, half); break;
+    case Format::Nf4: launch_format<Format::Nf4>(stream, call, args, half); break;
+    case Format::Int8: launch_format<Format::Int8>(stream, call, args, half); break;
     }
 }
 

@@ -140,6 +140,13 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
     } else if (call.m <= 8) {
         launch_gemv_fma(stream, call);
     } else if (ctx->kernel_path != 1) {
+        // The GEMM reads the same repacked tiles as the decode GEMV.
+        Packed p{call.n, call.k, call.format};
+        mfh_status s = prepare_tiles(ctx, codes_a, scales_a, p, &call.a);
+        if (!s && codes_b)
+            s = prepare_tiles(ctx, codes_b, scales_b, p, &call.b);
+        if (s)
+            return s;
         void *scratch = digits_scratch(ctx, gemm_mfma_scratch_bytes(call));
         if (!scratch)
             return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
