@@ -36,6 +36,7 @@
 // computes tile (b % 8) * (tiles / 8) + b / 8, so each XCD's L2 holds a
 // contiguous run of tiles: neighbouring n-tiles of the same m rows.
 #include <algorithm>
+#include <type_traits>
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -140,15 +141,6 @@ template <Format F> struct Chunk {
     static constexpr int stages = F == Format::Int8 ? 1 : F == Format::Nf4 ? 2 : 4;
 };
 
-template <bool HALF>
-__device__ __forceinline__ float scale_at(const void *p, size_t i)
-{
-    if constexpr (HALF)
-        return __half2float(static_cast<const __half *>(p)[i]);
-    else
-        return static_cast<const float *>(p)[i];
-}
-
 // INT8 bytes 8h..8h+7 of the lane's 16 (k = 16q + 8h + 0..7): binary16
 // 1024 + (b ^ 0x80) is exact, and subtracting 1152 leaves the signed code.
 __device__ __forceinline__ v8h decode_i8(const v4u &raw, int h)
@@ -240,6 +232,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     const uint32_t s_begin = chunk * chunk_stages, s_end = s_begin + chunk_stages;
 
     // A staging: thread -> (row, 32-wide k half) of both activation halves.
+    // Rows past m load row 0 (their outputs are never stored), so every
+    // load is unconditional and nothing waits to clear a destination.
     const uint32_t a_row = tid >> 1, a_k = (tid & 1) * 32;
     const bool a_live = m0 + a_row < g.m;
     const _Float16 *a_src[2] = {g.xh + size_t(a_live ? m0 + a_row : 0) * g.k + a_k,
@@ -252,8 +246,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
         for (int p = 0; p < 2; ++p)
 #pragma unroll
             for (int u = 0; u < 4; ++u)
-                r.v[p][u] = a_live ? *reinterpret_cast<const v8h *>(a_src[p] + s * kBK + 8 * u)
-                                   : v8h{};
+                r.v[p][u] = *reinterpret_cast<const v8h *>(a_src[p] + s * kBK + 8 * u);
     };
     auto store_a = [&](int buf, const ARaw &r) {
 #pragma unroll
@@ -282,10 +275,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                                                     li);
     }
     v4u cur[kTJ];
+    // Tiles past n read tile 0 (their columns are never stored).
     auto load_chunk = [&](uint32_t c, v4u (&dst)[kTJ]) {
 #pragma unroll
         for (int jt = 0; jt < kTJ; ++jt)
-            dst[jt] = wlive[jt] ? wptr[jt][size_t(c) * 64] : v4u{0u, 0u, 0u, 0u};
+            dst[jt] = wptr[jt][size_t(c) * 64];
     };
 
     v4f acc[kTI][kTJ], total[kTI][kTJ];
@@ -297,31 +291,38 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
             total[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
 
-    // Group constants: the block's 2^e per activation row go to LDS when the
-    // group starts (read at its end, two barriers later); each lane loads
-    // the weight scale of its columns.
-    float gsc[kTJ];
+    // Group constants, loaded when the group starts and used at its end (so
+    // the in-order load counter never makes an early instruction wait for
+    // them): each lane's weight scales, kept in their stored form, and the
+    // block's 2^e per activation row (threads < kBM), which reach LDS at the
+    // end of the group's first stage, a barrier before they are read.
+    typename std::conditional<HALF, unsigned short, float>::type gsc_raw[kTJ];
+    float fac_raw = 0.0f;
+    const uint32_t fac_row = m0 + (tid & (kBM - 1)) < g.m ? m0 + (tid & (kBM - 1)) : 0;
     auto load_group_constants = [&](uint32_t grp) {
-        if (tid < kBM) {
-            const uint32_t mm = m0 + tid;
-            fac[grp & 1][tid] = mm < g.m ? g.factor[size_t(mm) * groups + grp] : 0.0f;
-        }
+        fac_raw = g.factor[size_t(fac_row) * groups + grp];
 #pragma unroll
-        for (int jt = 0; jt < kTJ; ++jt)
-            gsc[jt] = scale_at<HALF>(sptr[jt], size_t(grp) * 16);
+        for (int jt = 0; jt < kTJ; ++jt) {
+            if constexpr (HALF)
+                gsc_raw[jt] = static_cast<const unsigned short *>(sptr[jt])[size_t(grp) * 16];
+            else
+                gsc_raw[jt] = static_cast<const float *>(sptr[jt])[size_t(grp) * 16];
+        }
     };
 
-    ARaw ra;
-    fetch_a(s_begin, ra);
+    ARaw next;
+    fetch_a(s_begin, next);
     load_chunk(s_begin / SPC, cur);
-    store_a(0, ra);
     load_group_constants(s_begin / 2);
+    store_a(0, next);
     __syncthreads();
 
     for (uint32_t s = s_begin; s < s_end; ++s) {
         const int buf = (s - s_begin) & 1;
-        if (s + 1 < s_end)
-            fetch_a(s + 1, ra);
+        // The last stage re-fetches itself and stores to the idle buffer:
+        // with no conditional fetch, no path leaves a load pending at the
+        // loop's back edge.
+        fetch_a(s + 1 < s_end ? s + 1 : s, next);
         if (s % 2 == 0 && s != s_begin)
             load_group_constants(s / 2);
 #pragma unroll
@@ -369,6 +370,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
         }
         if (s % 2 == 1) {
             // Group epilogue: total += group_sum * (2^e[m] * scale[n]).
+            float gsc[kTJ];
+#pragma unroll
+            for (int jt = 0; jt < kTJ; ++jt) {
+                if constexpr (HALF)
+                    gsc[jt] = __half2float(__ushort_as_half(gsc_raw[jt]));
+                else
+                    gsc[jt] = gsc_raw[jt];
+            }
 #pragma unroll
             for (int i = 0; i < kTI; ++i) {
                 const v4f gfx =
@@ -382,8 +391,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                 }
             }
         }
-        if (s + 1 < s_end)
-            store_a(buf ^ 1, ra);
+        store_a(buf ^ 1, next);
+        if (s % 2 == 0 && tid < kBM)
+            fac[(s / 2) & 1][tid] = fac_raw;
         __syncthreads();
     }
 
