@@ -82,15 +82,22 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// One wave per (128-group, row): factor[m, g] = 2^e (NaN for a group with a
-// non-finite value) and the binary16 halves of x * 2^-e.
-__global__ __launch_bounds__(64) void split_kernel(const float *__restrict__ x, uint32_t m,
-                                                   uint32_t k, _Float16 *__restrict__ xh,
-                                                   _Float16 *__restrict__ xl,
-                                                   float *__restrict__ factor)
+// One wave per (128-group, row), kSplitWaves groups of a row per block:
+// factor[m, g] = 2^e (NaN for a group with a non-finite value) and the
+// binary16 halves of x * 2^-e.
+constexpr int kSplitWaves = 4;
+
+__global__ __launch_bounds__(64 * kSplitWaves) void split_kernel(const float *__restrict__ x,
+                                                                 uint32_t m, uint32_t k,
+                                                                 _Float16 *__restrict__ xh,
+                                                                 _Float16 *__restrict__ xl,
+                                                                 float *__restrict__ factor)
 {
-    const uint32_t g = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+    const uint32_t g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6), row = blockIdx.y;
+    const uint32_t lane = threadIdx.x & 63;
     const uint32_t groups = k / 128;
+    if (g >= groups)
+        return;
     const float *src = x + size_t(row) * k + g * 128;
     float v[2];
     bool bad = false;
@@ -524,7 +531,8 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     _Float16 *xh = reinterpret_cast<_Float16 *>(p);
     _Float16 *xl = xh + size_t(call.m) * call.k;
     float *factor = reinterpret_cast<float *>(xl + size_t(call.m) * call.k);
-    split_kernel<<<dim3(groups, call.m), 64, 0, stream>>>(call.x, call.m, call.k, xh, xl, factor);
+    split_kernel<<<dim3((groups + kSplitWaves - 1) / kSplitWaves, call.m), 64 * kSplitWaves, 0,
+                   stream>>>(call.x, call.m, call.k, xh, xl, factor);
     // The repacked tiles pad K to 256 (ternary) or 128; one 16-byte lane load
     // covers 64 (INT8), 128 (NF4) or 256 (ternary) k.
     const uint32_t align = call.format == Format::Ternary ? 256 : 128;
