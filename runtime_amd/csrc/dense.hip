@@ -1189,6 +1189,34 @@ __global__ __launch_bounds__(kBlock) void gqa_decode_kernel(DecodeAttention p)
 
 // Row t of the table: rotation(t, c) for c < head_dim / 2, cosines then
 // sines (the coefficients the rotary kernels compute inline).
+// qk_norm_rope_kernel for the consecutive positions first, first + 1, ...,
+// with the coefficients read from a rotation table (launch_rotation_table)
+// rather than computed per element: the same values bit for bit.
+__global__ __launch_bounds__(kBlock) void qk_norm_rope_table_kernel(
+    float *__restrict__ query_out, float *__restrict__ key_out, const float *__restrict__ query,
+    const float *__restrict__ key, const float *__restrict__ query_weight,
+    const float *__restrict__ key_weight, const float *__restrict__ table, uint64_t first,
+    uint64_t tokens, uint32_t query_heads, uint32_t key_heads, uint32_t head_dim, float epsilon)
+{
+    const uint32_t heads = query_heads + key_heads;
+    const uint64_t segments = tokens * heads;
+    const uint64_t waves = uint64_t(gridDim.x) * (kBlock / 64);
+    for (uint64_t s = uint64_t(blockIdx.x) * (kBlock / 64) + (threadIdx.x >> 6); s < segments;
+         s += waves) {
+        const uint64_t token = s / heads;
+        const uint32_t head = uint32_t(s - token * heads);
+        const bool is_query = head < query_heads;
+        const uint32_t h = is_query ? head : head - query_heads;
+        const uint64_t base =
+            (token * (is_query ? query_heads : key_heads) + h) * uint64_t(head_dim);
+        const float *row = table + (first + token) * head_dim;
+        norm_rope_head_table((is_query ? query : key) + base,
+                             (is_query ? query_out : key_out) + base, nullptr,
+                             is_query ? query_weight : key_weight, head_dim, row,
+                             row + head_dim / 2, epsilon);
+    }
+}
+
 __global__ __launch_bounds__(kBlock) void rotation_table_kernel(float *__restrict__ table,
                                                                 uint64_t positions,
                                                                 uint32_t head_dim, float theta)
@@ -1419,6 +1447,19 @@ void launch_rotary(hipStream_t stream, float *out, const float *in, const Positi
     if (total)
         rotary_kernel<<<grid_for(total), kBlock, 0, stream>>>(out, in, positions, tokens, heads,
                                                                head_dim, theta);
+}
+
+void launch_qk_norm_rope_table(hipStream_t stream, float *query_out, float *key_out,
+                               const float *query, const float *key, const float *query_weight,
+                               const float *key_weight, const float *table, uint64_t first,
+                               uint64_t tokens, uint32_t query_heads, uint32_t key_heads,
+                               uint32_t head_dim, float epsilon)
+{
+    const uint64_t segments = tokens * (query_heads + key_heads);
+    if (segments)
+        qk_norm_rope_table_kernel<<<grid_for(segments, kBlock / 64), kBlock, 0, stream>>>(
+            query_out, key_out, query, key, query_weight, key_weight, table, first, tokens,
+            query_heads, key_heads, head_dim, epsilon);
 }
 
 void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, const float *query,

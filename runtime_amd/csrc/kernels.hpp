@@ -177,6 +177,13 @@ struct Positions {
 };
 void launch_rotary(hipStream_t stream, float *out, const float *in, const Positions &positions,
                    uint64_t tokens, uint32_t heads, uint32_t head_dim, float theta);
+// The same for the consecutive positions first .. first + tokens - 1, with
+// the coefficients from a launch_rotation_table table (bit-identical).
+void launch_qk_norm_rope_table(hipStream_t stream, float *query_out, float *key_out,
+                               const float *query, const float *key, const float *query_weight,
+                               const float *key_weight, const float *table, uint64_t first,
+                               uint64_t tokens, uint32_t query_heads, uint32_t key_heads,
+                               uint32_t head_dim, float epsilon);
 void launch_qk_norm_rope(hipStream_t stream, float *query_out, float *key_out, const float *query,
                          const float *key, const float *query_weight, const float *key_weight,
                          const Positions &positions, uint64_t tokens, uint32_t query_heads,

@@ -467,12 +467,25 @@ mfh_status append(mfl_model *m, const uint32_t *tokens, size_t count, const mfh_
                 s = weight_linear(c, ws->v.buf, u, lw.value);
             if (s)
                 return s;
-            if ((s = need(c, lw.query_norm)) || (s = need(c, lw.key_norm)) ||
-                (s = mfh_qk_norm_rope(c, ws->q_rope.buf, ws->k_rope.buf, ws->q.buf, ws->k.buf,
-                                      lw.query_norm.tensor, lw.key_norm.tensor, positions.data(),
-                                      rows, cfg.attention_heads, cfg.head_dim, cfg.rope_theta,
-                                      cfg.key_value_heads, cfg.head_dim, cfg.block_norm_epsilon)) ||
-                (s = mfh_causal_gqa(c, ws->attention.buf, ws->q_rope.buf, ws->k_rope.buf,
+            if ((s = need(c, lw.query_norm)) || (s = need(c, lw.key_norm)))
+                return s;
+            if (cfg.head_dim >= 2 && cfg.head_dim % 2 == 0) {
+                // Positions length .. length + rows - 1 are rows of the
+                // model's rotation table (the coefficients qk_norm_rope
+                // would compute, bit for bit).
+                launch_qk_norm_rope_table(c->stream, dev(ws->q_rope), dev(ws->k_rope), dev(ws->q),
+                                          dev(ws->k), dev(lw.query_norm), dev(lw.key_norm),
+                                          dev(m->rotation), m->length, rows, cfg.attention_heads,
+                                          cfg.key_value_heads, cfg.head_dim,
+                                          cfg.block_norm_epsilon);
+            } else if ((s = mfh_qk_norm_rope(c, ws->q_rope.buf, ws->k_rope.buf, ws->q.buf,
+                                             ws->k.buf, lw.query_norm.tensor, lw.key_norm.tensor,
+                                             positions.data(), rows, cfg.attention_heads,
+                                             cfg.head_dim, cfg.rope_theta, cfg.key_value_heads,
+                                             cfg.head_dim, cfg.block_norm_epsilon))) {
+                return s;
+            }
+            if ((s = mfh_causal_gqa(c, ws->attention.buf, ws->q_rope.buf, ws->k_rope.buf,
                                     ws->v.buf, st.key.buf, st.value.buf, &st.length,
                                     cfg.attention_heads, cfg.key_value_heads, cfg.head_dim)) ||
                 (s = weight_linear(c, ws->op.buf, ws->attention.buf, lw.output)))
