@@ -152,6 +152,30 @@ def test_prefill_gemm(backend, path, scheme, m):
     assert_close(got, want, 1e-4, 1e-4)
 
 
+# Ragged prefill shapes: partial 128-row and 64-column output tiles, K that
+# ends inside a 256-wide ternary chunk, a single group, and shapes where the
+# contraction is split across workgroups.
+GEMM_EDGE_SHAPES = [(9, 37, 384), (130, 200, 640), (257, 70, 1152), (33, 1000, 128),
+                    (129, 4608, 1024), (12, 64, 4096)]
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m,n,k", GEMM_EDGE_SHAPES)
+def test_prefill_gemm_ragged_shapes(backend, path, scheme, m, n, k):
+    say("prefill gemm ragged", scheme, path, m, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0310 + n + k)
+    x = convert.normal((m, k), 0xAC70310 + m)
+    x[m // 2, k // 3] = np.nan
+    x[m - 1, 0] = np.inf
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear_threaded(x, codes, scales)
+    bad = np.zeros(m, dtype=bool)
+    bad[[m // 2, m - 1]] = True
+    assert not np.isfinite(got[bad]).any()
+    assert max_rel_err(got[~bad], want[~bad]) <= 1e-3
+    assert_close(got[~bad], want[~bad], 1e-4, 1e-4)
+
+
 # --- pair / SwiGLU variants -----------------------------------------------------------
 
 @pytest.mark.parametrize("scheme", SCHEMES)
