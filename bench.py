@@ -357,10 +357,16 @@ def main() -> int:
     # Per-launch table (outside the timed region): each operation launched
     # back to back over the rotating copies between one event pair.  Matrices
     # far smaller than the 256 MB Infinity Cache stay resident in it here.
+    # Eight dominant launches (about 200 us of device work) go first, so the
+    # host has enqueued the timed launches before the device reaches them: a
+    # two-kernel launch of a small matrix takes less device time than its
+    # host-side enqueue.
     log("per-launch table")
     repeats = 4 * args.copies
     detail = {}
     for i, (fmt_i, (n_i, k_i), b_i) in enumerate(launches):
+        for r in range(8):
+            launch(di, r)
         e0, e1 = hiptime.Event(), hiptime.Event()
         e0.record(stream)
         for r in range(repeats):

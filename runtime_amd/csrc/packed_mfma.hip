@@ -758,11 +758,12 @@ __device__ __forceinline__ void i8_compute(const I8Block<F, T, S, NF, HALF> &blk
 }
 
 // ---------------------------------------------------------------------------
-// Register prologue (m <= 4, activations as stored).  Each wave forms the
+// Register prologue (m <= 8, activations as stored).  Each wave forms the
 // digit fragments of its own loop blocks, one block ahead of the MFMAs,
 // from the raw activations: no LDS, no barrier, no separate kernel.
-// Lane 16q + 4b + p loads x[b][64s + 16q + 4p + t] (t = 0..3) of every
-// kstep s, and it supplies digit row p of batch b in the MFMA A operand.
+// Lane 16q + 4b + p loads x[4f + b][64s + 16q + 4p + t] (t = 0..3) of every
+// kstep s for each fragment f, and it supplies digit row p of batch 4f + b
+// in fragment f's MFMA A operand.
 // Per group, the exponent and the ternary correction reduce over the 16
 // lanes that hold the batch (lane quad, lane blocks); the quad then shares
 // its 16 offset values and each lane packs digit p of all of them.  The
@@ -774,6 +775,8 @@ constexpr int kRegPro = 16;
 // the add + RMS norm, which holds the whole range while the row's squares
 // reduce.
 constexpr int kRegNormSteps = 4;
+// Largest grid for the two-fragment (m > 4) ternary register prologue.
+constexpr uint32_t kRegPairBlocks = 320;
 
 template <int LB>
 struct RegX {
@@ -842,11 +845,12 @@ __device__ __forceinline__ void reg_load(RegX<LB> &rx, const float *xrow, bool l
     }
 }
 
-template <Format F, int T, int S, bool HALF>
+// Fragment f (batch rows 4f..4f+3) of a loop block from this lane's values.
+template <Format F, int T, int S, int NF, bool HALF>
 __device__ __forceinline__ void reg_digits(const RegX<Geo<F>::lb> &rx,
-                                           I8Block<F, T, S, 1, HALF> &blk)
+                                           I8Block<F, T, S, NF, HALF> &blk, int f)
 {
-    using B = I8Block<F, T, S, 1, HALF>;
+    using B = I8Block<F, T, S, NF, HALF>;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t p = lane & 3, q = lane >> 4;
     const unsigned flip = p ? 0x80808080u : 0u;
@@ -902,11 +906,11 @@ __device__ __forceinline__ void reg_digits(const RegX<Geo<F>::lb> &rx,
                 for (int i = 0; i < 4; ++i)
                     w[i] = d[i];             // INT8 byte c = 4P + t: dword P, byte t
             }
-            blk.af[ks][0] = v4i{int(w[0] ^ flip), int(w[1] ^ flip), int(w[2] ^ flip),
+            blk.af[ks][f] = v4i{int(w[0] ^ flip), int(w[1] ^ flip), int(w[2] ^ flip),
                                 int(w[3] ^ flip)};
         }
         // Lane (q, j) applies batch q's constants: lane 4q holds them.
-        blk.xf[gg][0] = __shfl(factor, int(4 * q), 64);
+        blk.xf[gg][f] = __shfl(factor, int(4 * q), 64);
         if constexpr (F == Format::Ternary) {
             corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
                     (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
@@ -917,9 +921,9 @@ __device__ __forceinline__ void reg_digits(const RegX<Geo<F>::lb> &rx,
             // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
             const long long lo = ((corr + 32768) & 65535) - 32768;
             const int hi = int((corr - lo) >> 16);
-            blk.cv[gg][0] = int2{__shfl(hi, int(4 * q), 64), __shfl(int(lo), int(4 * q), 64)};
+            blk.cv[gg][f] = int2{__shfl(hi, int(4 * q), 64), __shfl(int(lo), int(4 * q), 64)};
         } else {
-            blk.cv[gg][0] = int2{0, 0};
+            blk.cv[gg][f] = int2{0, 0};
         }
     }
 }
@@ -939,12 +943,17 @@ __host__ __device__ constexpr size_t fused_bytes_nf4(uint32_t k_pad, uint32_t m)
 }
 
 // At most 8 waves per block: two per SIMD leaves 256 VGPRs per wave for the
-// double-buffered loop blocks.  PRO < 0: digits_kernel wrote the activation
-// fragments to global scratch.  Otherwise the block first forms them in LDS
-// with the in-kernel prologue of transform XKind(PRO) (block_prologue) while
-// each wave's first weights are in flight.
+// double-buffered loop blocks.  One-tile, one-stream, one-fragment kernels
+// with the separate or register prologue (at most 110 VGPRs) also run 16
+// waves, for the small-N plan (kDeepWaves).  PRO < 0: digits_kernel wrote
+// the activation fragments to global scratch.  PRO == kRegPro(+AddRms):
+// each lane forms its own fragments in registers.  Otherwise the block first
+// forms them in LDS with the in-kernel prologue of transform XKind(PRO)
+// (block_prologue) while each wave's first weights are in flight.
 template <Format F, int T, int S, int NF, bool HALF, Epilogue E, int PRO>
-__global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
+__global__ __launch_bounds__(T == 1 && S == 1 && NF == 1 && (PRO < 0 || PRO == kRegPro) ? 1024
+                                                                                          : 512)
+void gemv_i8_kernel(MfmaArgs a)
 {
     using B = I8Block<F, T, S, NF, HALF>;
     using ST = typename ScaleT<HALF>::type;
@@ -1003,30 +1012,44 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
         }
     };
     if constexpr (PRO == kRegPro) {
-        static_assert(NF == 1, "the register prologue serves m <= 4");
         // Activation loads go out ahead of the same block's weights, so a
         // block's digits can form while its weights are still arriving.
         const uint32_t b = (lane >> 2) & 3;
-        const float *xrow = a.xform.a + size_t(b < a.m ? b : 0) * a.k;
-        const bool live = b < a.m;
-        RegX<B::LB> rx0, rx1;
+        const float *xrow[NF];
+        bool live[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            live[f] = 4 * f + b < a.m;
+            xrow[f] = a.xform.a + size_t(live[f] ? 4 * f + b : 0) * a.k;
+        }
+        RegX<B::LB> rx0[NF], rx1[NF];
+        auto load_x = [&](RegX<B::LB>(&rx)[NF], uint32_t index) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                reg_load(rx[f], xrow[f], live[f], a.k, s_begin, index);
+        };
+        auto digits = [&](const RegX<B::LB>(&rx)[NF], B &blk) {
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                reg_digits(rx[f], blk, f);
+        };
         if (nblk > 0) {
-            reg_load(rx0, xrow, live, a.k, s_begin, 0);
+            load_x(rx0, 0);
             i8_load_w(buf0, wp, sp, 0);
         }
         for (uint32_t i = 0; i < nblk; i += 2) {
             if (i + 1 < nblk) {
-                reg_load(rx1, xrow, live, a.k, s_begin, i + 1);
+                load_x(rx1, i + 1);
                 i8_load_w(buf1, wp, sp, i + 1);
             }
-            reg_digits(rx0, buf0);
+            digits(rx0, buf0);
             i8_compute(buf0, accf);
             if (i + 1 < nblk) {
                 if (i + 2 < nblk) {
-                    reg_load(rx0, xrow, live, a.k, s_begin, i + 2);
+                    load_x(rx0, i + 2);
                     i8_load_w(buf0, wp, sp, i + 2);
                 }
-                reg_digits(rx1, buf1);
+                digits(rx1, buf1);
                 i8_compute(buf1, accf);
             }
         }
@@ -1091,12 +1114,12 @@ __global__ __launch_bounds__(512) void gemv_i8_kernel(MfmaArgs a)
                 rx[ks / B::LB].v[ks % B::LB][e] = (xs[ks][e] * reciprocal) * ws[ks][e];
         }
         if (nblk > 0) {
-            reg_digits(rx[0], buf0);
+            reg_digits(rx[0], buf0, 0);
             i8_compute(buf0, accf);
         }
         if constexpr (NB > 1) {
             if (nblk > 1) {
-                reg_digits(rx[1], buf1);
+                reg_digits(rx[1], buf1, 0);
                 i8_compute(buf1, accf);
             }
         }
@@ -1311,8 +1334,11 @@ __device__ __forceinline__ void nf4_reg_halves(const RegX<4> &rx, Nf4Block<T, S,
     blk.xf[1] = __shfl(factor, int(4 * q + 2), 64);
 }
 
+// Block shapes as gemv_i8_kernel's; one-tile single-stream kernels with the
+// separate or register prologue (at most 116 VGPRs) also run 16 waves.
 template <int T, int S, bool HALF, Epilogue E, int PRO>
-__global__ __launch_bounds__(512) void gemv_nf4_kernel(MfmaArgs a)
+__global__ __launch_bounds__(T == 1 && S == 1 && (PRO < 0 || PRO == kRegPro) ? 1024 : 512)
+void gemv_nf4_kernel(MfmaArgs a)
 {
     using ST = typename ScaleT<HALF>::type;
     // kLutCopies interleaved copies of the 256-entry table; lane l reads copy
@@ -1535,6 +1561,21 @@ Plan plan_for(uint32_t n_tiles, uint32_t ksteps, uint32_t lb, int max_t, bool wi
     return Plan{1, 1};
 }
 
+// Small-N shapes fall back to one tile per block and 8 waves over K with too
+// few waves to fill the chip (n_tiles * 8 < 2048): there 16 waves per block
+// halve every wave's K range (2048 x 8192 INT8 at one row: 9.48 -> 8.13 us;
+// 2048 x 2048 NF4: 5.13 -> 4.63 us).  Only kernels declared for 1024 lanes
+// take it (one tile, one stream, one fragment; separate or register
+// prologue).
+constexpr int kDeepWaves = 16;
+Plan deepen(Plan p, uint32_t n_tiles, uint32_t ksteps, uint32_t lb)
+{
+    if (p.tiles_per_block == 1 && p.waves == 8 && uint64_t(n_tiles) * 8 < 2048 &&
+        ksteps % (kDeepWaves * lb) == 0)
+        p.waves = kDeepWaves;
+    return p;
+}
+
 template <int S, int NB>
 size_t reduce_lds_bytes(int waves, int t)
 {
@@ -1584,6 +1625,11 @@ void launch_i8_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, in
         default:
             break;
         }
+    } else if constexpr (S == 1) {
+        // Two fragments: gemv_i8_format picks the register prologue only for
+        // single products, else the separate one (pro < 0).
+        if (pro == kRegPro)
+            return launch_i8_kernel<F, T, S, NF, HALF, E, kRegPro>(stream, args, blocks, waves);
     }
     launch_i8_kernel<F, T, S, NF, HALF, E, -1>(stream, args, blocks, waves);
 }
@@ -1610,11 +1656,12 @@ void launch_i8_nf(hipStream_t stream, const MfmaArgs &args, Epilogue e, unsigned
         else
             launch_i8<F, T, S, 1, false>(stream, args, e, blocks, waves, pro);
     } else {
-        // The in-kernel prologue serves m <= 2 (one fragment) only.
+        // Two fragments: the separate prologue or the plain register one
+        // (the LDS and norm prologues serve one fragment only).
         if (half)
-            launch_i8<F, T, S, 2, true>(stream, args, e, blocks, waves, -1);
+            launch_i8<F, T, S, 2, true>(stream, args, e, blocks, waves, pro);
         else
-            launch_i8<F, T, S, 2, false>(stream, args, e, blocks, waves, -1);
+            launch_i8<F, T, S, 2, false>(stream, args, e, blocks, waves, pro);
     }
 }
 
@@ -1752,9 +1799,10 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const int max_t = streams == 1 && !call.segments ? 4 : 1;
     const Plan narrow = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, false);
     const Plan wide = plan_for(n_tiles, ksteps, Geo<F>::lb, max_t, true);
-    // The register prologue serves plain activations, and the add + RMS norm
-    // when each wave's K range is at most kRegNormSteps ksteps (it holds them
-    // all while the row's squares reduce), for at most four rows with 16-byte
+    // The register prologue serves plain activations (up to eight rows for
+    // single products, four for two-stream ones), and the add + RMS norm of
+    // at most four rows when each wave's K range is at most kRegNormSteps
+    // ksteps (it holds them all while the row's squares reduce), with 16-byte
     // aligned operands.  Ternary operands cost more arithmetic per group
     // (the field telescoping and the correction): past two groups per wave
     // the separate prologue kernel measured faster (65536 x 2048: 13.3
@@ -1762,33 +1810,50 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     auto aligned = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
     auto reg_ok = [&](Plan p) {
         const uint32_t per_wave = ksteps / p.waves;
-        if (call.separate_prologue || call.m > 4 || (F == Format::Ternary && per_wave / 2 > 2))
+        if (call.separate_prologue || (F == Format::Ternary && per_wave / 2 > 2))
             return false;
+        if (xform.kind == XKind::Plain && call.m > 4) {
+            // Two fragments double each lane's prologue arithmetic, which
+            // every block repeats for its K range: it stays ahead of the
+            // separate kernel for INT8 up to 8 ksteps per wave (2048 x 8192
+            // at 16: 12.7 -> 13.9 us) and for ternary up to kRegPairBlocks
+            // blocks (8192 x 2048 at 512 blocks: 8.0 -> 10.7 us; 4608 x 1024
+            // at 288: 6.3 -> 6.0 us).
+            if (streams != 1 || (F == Format::Int8 && per_wave > 8) ||
+                (F == Format::Ternary && n_tiles / tiles_of(p) > kRegPairBlocks))
+                return false;
+        }
         if (xform.kind == XKind::Plain)
             return aligned(xform.a);
+        if (call.m > 4)
+            return false;
         if (xform.kind == XKind::AddRms)
             return per_wave <= uint32_t(kRegNormSteps) && aligned(xform.a) && aligned(xform.b) &&
                    aligned(xform.w) && aligned(xform.side);
         return false;
     };
-    // Preference: the register prologue for the norm, then the LDS one,
-    // then the register prologue for plain activations, then the separate
-    // prologue kernel.  The 8-wave plan takes the norm only with one tile per
-    // block: the 4-tile norm kernel holds two waves per SIMD, too few for the
-    // LM head's 8-wave blocks (1.2B-shape decode 1389 -> 1355 tok/s).
+    // Preference: the register prologue (norm or plain), then the LDS one,
+    // then the separate prologue kernel.  For plain activations the register
+    // prologue measured 13-46 % faster than the LDS one wherever both apply
+    // (4608 x 1024 at two rows: ternary 7.49 -> 4.01 us, INT8 5.52 -> 3.61).
+    // The 8-wave plan takes the norm only with one tile per block: the 4-tile
+    // norm kernel holds two waves per SIMD, too few for the LM head's 8-wave
+    // blocks (1.2B-shape decode 1389 -> 1355 tok/s).
     Plan plan = narrow;
     int pro = -1;
     const bool reg_wide = reg_ok(wide) && tiles_of(wide) == 1;
     if (xform.kind == XKind::AddRms && (reg_ok(narrow) || reg_wide)) {
         plan = reg_ok(narrow) ? narrow : wide;
         pro = kRegPro + int(XKind::AddRms);
+    } else if (xform.kind == XKind::Plain && reg_ok(narrow)) {
+        pro = kRegPro;
     } else if (fusable(narrow) || fusable(wide)) {
         plan = fusable(narrow) ? narrow : wide;
         pro = int(xform.kind);
-    } else if (reg_ok(narrow)) {
-        pro = kRegPro;
     }
     plan.tiles_per_block = tiles_of(plan);
+    if ((pro < 0 || pro == kRegPro) && streams == 1 && nf == 1)
+        plan = deepen(plan, n_tiles, ksteps, Geo<F>::lb);
     if (pro < 0)
         digits_kernel<F>
             <<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 4 * nf), 64 * kPrologueWaves,
@@ -1851,15 +1916,19 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     // values per k of the integer formats next to its table decode, and past
     // that share (the 65536 x 2048 head, K = 8192), at eight rows, or for the
     // add + RMS norm the separate or LDS prologue measured faster.
+    // It is preferred to the LDS prologue (1024 x 1024 at two rows: 5.01 ->
+    // 3.72 us).
     Plan plan = narrow;
     int pro = -1;
-    if (fusable(narrow) || fusable(wide)) {
+    if (!call.separate_prologue && xform.kind == XKind::Plain && call.m <= 4 &&
+        ksteps / narrow.waves <= 8 && reinterpret_cast<uintptr_t>(xform.a) % 16 == 0) {
+        pro = kRegPro;
+    } else if (fusable(narrow) || fusable(wide)) {
         plan = fusable(narrow) ? narrow : wide;
         pro = int(xform.kind);
-    } else if (!call.separate_prologue && xform.kind == XKind::Plain && call.m <= 4 &&
-               ksteps / narrow.waves <= 8 && reinterpret_cast<uintptr_t>(xform.a) % 16 == 0) {
-        pro = kRegPro;
     }
+    if ((pro < 0 || pro == kRegPro) && streams == 1)
+        plan = deepen(plan, n_tiles, ksteps, 4);
     if (pro < 0)
         halves_kernel<<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 8),
                         64 * kPrologueWaves, 0, stream>>>(xform, call.m, call.k, groups,
