@@ -1259,7 +1259,7 @@ __device__ __forceinline__ void nf4_load_w(Nf4Block<T, S, HALF> &blk,
         }
 }
 
-// NF4 register prologue (m <= 4).  Lane 16q + 2b + h supplies half h (0:
+// NF4 register prologue (m <= 8).  Lane 16q + 2b + h supplies half h (0:
 // hi, 1: lo) of batch b in the f16 A operand, eight values
 // k = 32s + 8q + 0..7 per 32-wide kstep s.  The lane pair splits them:
 // lane h loads values 4h..4h+3 (k offset nf4_reg_offset), splits them
@@ -1911,16 +1911,17 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const int max_t = streams == 1 && !call.segments ? 2 : 1;
     const Plan narrow = plan_for(n_tiles, ksteps, 4, max_t, false);
     const Plan wide = plan_for(n_tiles, ksteps, 4, max_t, true);
-    // Register prologue for plain activations of at most four rows (16-byte
+    // Register prologue for plain activations (up to eight rows, 16-byte
     // aligned) over at most 256 k per wave.  NF4 forms twice the operand
     // values per k of the integer formats next to its table decode, and past
-    // that share (the 65536 x 2048 head, K = 8192), at eight rows, or for the
-    // add + RMS norm the separate or LDS prologue measured faster.
-    // It is preferred to the LDS prologue (1024 x 1024 at two rows: 5.01 ->
-    // 3.72 us).
+    // that share (the 65536 x 2048 head, K = 8192) or for the add + RMS norm
+    // the separate or LDS prologue measured faster.  It is preferred to the
+    // LDS prologue (1024 x 1024 at two rows: 5.01 -> 3.72 us) and to the
+    // separate one at five to eight rows (1024 x 1024 at eight: 6.49 ->
+    // 3.85 us; 8192 x 2048: 8.08 -> 6.87 us).
     Plan plan = narrow;
     int pro = -1;
-    if (!call.separate_prologue && xform.kind == XKind::Plain && call.m <= 4 &&
+    if (!call.separate_prologue && xform.kind == XKind::Plain && call.m <= 8 &&
         ksteps / narrow.waves <= 8 && reinterpret_cast<uintptr_t>(xform.a) % 16 == 0) {
         pro = kRegPro;
     } else if (fusable(narrow) || fusable(wide)) {
