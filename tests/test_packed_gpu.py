@@ -115,16 +115,22 @@ def test_non_finite_activations_poison_their_rows(backend, path, scheme, n, k):
     non-finite (device backends surface it through argmax rather than a
     per-op check, inference.rs:125-131); the other rows are unaffected."""
     say("non-finite rows", scheme, path, n, k)
-    m = 4
-    codes, scales = make_weights(n, k, scheme, 0x5EED0300 + n + k)
-    x = convert.normal((m, k), 0xAC70300 + k)
-    x[1, 300] = np.nan
-    x[2, 5] = np.inf
-    x[3, k - 1] = -np.inf
-    got = run_linear(backend, x, codes, scales)
-    assert not np.isfinite(got[1:]).any()
-    want = oracle.packed_linear_threaded(x[:1], codes, scales)
-    assert_close(got[:1], want, 1e-4, 1e-4)
+    for m in (4, 7):  # one activation fragment, and two (rows 4-7)
+        codes, scales = make_weights(n, k, scheme, 0x5EED0300 + n + k)
+        x = convert.normal((m, k), 0xAC70300 + k + m)
+        x[1, 300] = np.nan
+        x[2, 5] = np.inf
+        x[3, k - 1] = -np.inf
+        bad = [1, 2, 3]
+        if m > 4:
+            x[5, 77] = np.nan
+            x[6, k // 2] = -np.inf
+            bad += [5, 6]
+        good = [r for r in range(m) if r not in bad]
+        got = run_linear(backend, x, codes, scales)
+        assert not np.isfinite(got[bad]).any()
+        want = oracle.packed_linear_threaded(x[good], codes, scales)
+        assert_close(got[good], want, 1e-4, 1e-4)
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
