@@ -1307,6 +1307,34 @@ __global__ __launch_bounds__(kBlock) void conv_tokens_kernel(float *__restrict__
     }
 }
 
+// One decode token of the gated short convolution, reading the history
+// from `history` and writing the rolled history to `next` (the two-buffer
+// layout of the decode step), one thread per channel.  The arithmetic is
+// short_conv_kernel's at one token, term for term.
+__global__ __launch_bounds__(kBlock) void conv_step_kernel(float *__restrict__ out,
+                                                           const float *__restrict__ projection,
+                                                           const float *__restrict__ kernel,
+                                                           const float *__restrict__ history,
+                                                           float *__restrict__ next,
+                                                           uint32_t hidden, uint32_t width)
+{
+    const uint32_t channel = blockIdx.x * kBlock + threadIdx.x;
+    if (channel >= hidden)
+        return;
+    const uint32_t rows = width - 1;
+    const float u = projection[channel] * projection[2 * uint64_t(hidden) + channel];
+    const float *taps = kernel + uint64_t(channel) * width;
+    float total = 0.0f;
+    for (uint32_t tap = 0; tap < rows; ++tap)
+        total += taps[tap] * history[uint64_t(tap) * hidden + channel];
+    total += taps[rows] * u;
+    for (uint32_t r = 0; r + 1 < rows; ++r)
+        next[uint64_t(r) * hidden + channel] = history[uint64_t(r + 1) * hidden + channel];
+    if (rows)
+        next[uint64_t(rows - 1) * hidden + channel] = u;
+    out[channel] = total * projection[uint64_t(hidden) + channel];
+}
+
 // The history roll of short_conv_kernel on its own, one thread per channel.
 __global__ __launch_bounds__(kBlock) void conv_roll_kernel(const float *__restrict__ projection,
                                                            float *__restrict__ history,
@@ -1611,6 +1639,14 @@ void launch_short_conv(hipStream_t stream, float *out, const float *projection,
         out, projection, kernel, history, tokens, hidden, width);
     conv_roll_kernel<<<(hidden + kBlock - 1) / kBlock, kBlock, 0, stream>>>(projection, history,
                                                                            tokens, hidden, width);
+}
+
+void launch_conv_step(hipStream_t stream, float *out, const float *projection,
+                      const float *kernel, const float *history, float *next, uint32_t hidden,
+                      uint32_t width)
+{
+    conv_step_kernel<<<(hidden + kBlock - 1) / kBlock, kBlock, 0, stream>>>(
+        out, projection, kernel, history, next, hidden, width);
 }
 
 }  // namespace mfh

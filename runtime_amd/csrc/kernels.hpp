@@ -226,5 +226,9 @@ void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p);
 void launch_short_conv(hipStream_t stream, float *out, const float *projection,
                        const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
                        uint32_t width);
+// One decode token; the rolled history goes to `next` (width >= 1).
+void launch_conv_step(hipStream_t stream, float *out, const float *projection,
+                      const float *kernel, const float *history, float *next, uint32_t hidden,
+                      uint32_t width);
 
 }  // namespace mfh

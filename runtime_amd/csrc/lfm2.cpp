@@ -268,14 +268,12 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
                                   1, 3 * h, h, lw.conv_in.tensor, lw.conv_in.scales, nullptr,
                                   nullptr, dev(ws->projection), nullptr)))
                 return s;
-            XForm conv;
-            conv.kind = XKind::Conv;
-            conv.a = dev(ws->projection);
-            conv.b = dev(st.history[st.current]);
-            conv.w = dev(lw.conv_kernel);
-            conv.side = dev(st.history[1 - st.current]);
-            conv.width = cfg.conv_width;
-            if ((s = packed_xform(c, Epilogue::Single, conv, 1, h, h, lw.conv_out.tensor,
+            launch_conv_step(c->stream, dev(ws->convolved), dev(ws->projection),
+                             dev(lw.conv_kernel), dev(st.history[st.current]),
+                             dev(st.history[1 - st.current]), h, cfg.conv_width);
+            XForm convolved;
+            convolved.a = dev(ws->convolved);
+            if ((s = packed_xform(c, Epilogue::Single, convolved, 1, h, h, lw.conv_out.tensor,
                                   lw.conv_out.scales, nullptr, nullptr, op, nullptr)))
                 return s;
             st.current = 1 - st.current;

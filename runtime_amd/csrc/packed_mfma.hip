@@ -1054,7 +1054,7 @@ void gemv_i8_kernel(MfmaArgs a)
             }
         }
     } else if constexpr (PRO == kRegPro + int(XKind::AddRms)) {
-        static_assert(NF == 1, "the register prologue serves m <= 4");
+        static_assert(NF == 1, "the register norm prologue serves m <= 4");
         // s = a + b over the wave's whole K range (at most kRegNormSteps
         // ksteps), every wave's squares summed per batch row, then
         // x = (s * reciprocal) * weight as in the separate prologue.
