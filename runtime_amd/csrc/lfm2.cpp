@@ -377,8 +377,12 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
         right = down;
     }
     if (produce_logits) {
-        XForm head = norm_of(m->embedding_norm, nullptr);
-        head.epsilon = cfg.norm_epsilon;
+        // The final add + norm as a row kernel of its own (the sum goes to a
+        // scratch row), then a plain product.
+        launch_row_rms(c->stream, dev(ws->u[0]), right ? dev(ws->u[1]) : nullptr, left, right,
+                       dev(m->embedding_norm), 1, h, cfg.norm_epsilon);
+        XForm head;
+        head.a = dev(ws->u[0]);
         if ((s = packed_xform(c, Epilogue::Single, head, 1, cfg.vocab, h, m->embedding.tensor,
                               m->embedding.scales, nullptr, nullptr, dev(m->logits), nullptr)))
             return s;
