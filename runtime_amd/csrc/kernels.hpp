@@ -31,16 +31,14 @@ enum class XKind : uint32_t {
     Plain = 0,   // x = a
     AddRms = 1,  // s = a + b (b may be null); x = (s * rsqrt(mean(s^2) + eps)) * w
     Swiglu = 2,  // x = silu(a) * b
-    Conv = 3,    // one token of the gated short convolution (m = 1)
 };
 struct XForm {
     XKind kind = XKind::Plain;
-    const float *a = nullptr;  // Plain x; AddRms left; Swiglu gate; Conv projection [1, 3k]
-    const float *b = nullptr;  // AddRms right; Swiglu up; Conv history [width - 1, k]
-    const float *w = nullptr;  // AddRms norm weight [k]; Conv kernel [k, width]
-    float *side = nullptr;     // AddRms: s [m, k] (may be null); Conv: next history
+    const float *a = nullptr;  // Plain x; AddRms left; Swiglu gate
+    const float *b = nullptr;  // AddRms right; Swiglu up
+    const float *w = nullptr;  // AddRms norm weight [k]
+    float *side = nullptr;     // AddRms: s [m, k] (may be null)
     float epsilon = 0.0f;
-    uint32_t width = 0;        // Conv taps
 };
 
 constexpr uint32_t kMaxSegments = 3;
@@ -70,7 +68,7 @@ struct PackedCall {
     uint32_t seg_n[kMaxSegments] = {};
 };
 
-// A matrix-core GEMV (m <= 2; m = 1 for Conv) whose activation prologue
+// A matrix-core GEMV (m <= 2) whose activation prologue
 // applies `xform`, over admitted weights of n rows and width k (the LFM2
 // decode step).  Fails with MFH_UNSUPPORTED where that kernel does not serve
 // the call, before anything is enqueued.

@@ -223,10 +223,11 @@ bool fused_decode_ready(const mfl_model *m)
 }
 
 // One decode token with the elementwise steps folded into the products'
-// activation prologues (see XForm): per convolution block the in
-// projection (residual add + operator norm), the out projection (the
-// convolution) and the gate/up pair (residual add + FFN norm, with SwiGLU in
-// its epilogue).  Attention blocks run q/k/v as one launch (v lands in its
+// activation prologues (see XForm) where that measured faster: per
+// convolution block the in projection (residual add + operator norm) and the
+// gate/up pair (residual add + FFN norm, with SwiGLU in its epilogue); the
+// one-token convolution and the final norm are kernels of their own ahead of
+// plain products.  Attention blocks run q/k/v as one launch (v lands in its
 // cache row) and qk_norm_rope + the key append + attention as two.  Same
 // operations and order as append() on one row; only the f32 reduction trees
 // of the norms and the softmax differ.

@@ -163,25 +163,9 @@ __device__ __forceinline__ float xform_load(const XForm &t, uint32_t b, uint32_t
             t.side[i] = v;
         weight = t.w[kk];
         return v;
-    } else if constexpr (K == XKind::Swiglu) {
-        return silu_mul(t.a[i], t.b[i]);
     } else {
-        // One token of the gated short convolution (attention_convolution.rs:
-        // 220-340): u = B * x, taps oldest (history row 0) to current, times C.
-        const uint32_t rows = t.width - 1;
-        const float u = t.a[kk] * t.a[2 * size_t(k) + kk];
-        const float *taps = t.w + size_t(kk) * t.width;
-        float total = 0.0f;
-        for (uint32_t tap = 0; tap < rows; ++tap)
-            total += taps[tap] * t.b[size_t(tap) * k + kk];
-        total += taps[rows] * u;
-        if (writer) {
-            for (uint32_t r = 0; r + 1 < rows; ++r)
-                t.side[size_t(r) * k + kk] = t.b[size_t(r + 1) * k + kk];
-            if (rows)
-                t.side[size_t(rows - 1) * k + kk] = u;
-        }
-        return total * t.a[size_t(k) + kk];
+        static_assert(K == XKind::Swiglu, "transform kinds: Plain, AddRms, Swiglu");
+        return silu_mul(t.a[i], t.b[i]);
     }
 }
 
@@ -192,8 +176,7 @@ __device__ __forceinline__ float xform_load_any(const XForm &t, uint32_t b, uint
     switch (t.kind) {
     case XKind::Plain: return xform_load<XKind::Plain>(t, b, kk, k, writer, weight);
     case XKind::AddRms: return xform_load<XKind::AddRms>(t, b, kk, k, writer, weight);
-    case XKind::Swiglu: return xform_load<XKind::Swiglu>(t, b, kk, k, writer, weight);
-    default: return xform_load<XKind::Conv>(t, b, kk, k, writer, weight);
+    default: return xform_load<XKind::Swiglu>(t, b, kk, k, writer, weight);
     }
 }
 
@@ -370,10 +353,11 @@ __global__ __launch_bounds__(64 * kPrologueWaves) void digits_kernel(XForm t, ui
 // Each group is then handed to `emit(b, g, group)`; the fragments land in
 // one block-wide LDS array that every wave reads for its own K range.  The
 // kind is a template parameter so each instantiation holds only its own
-// loads (the convolution's eight loads per value get a smaller budget).
+// loads.
 __host__ __device__ constexpr uint32_t held_groups(XKind kind)
 {
-    return kind == XKind::Conv ? 2 : 8;
+    (void)kind;
+    return 8;
 }
 // Each wave forms its groups one after another, so a share above this many
 // costs more latency than the separate prologue kernel's launch.
@@ -1618,10 +1602,6 @@ void launch_i8_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, in
             if constexpr (E == Epilogue::Single)
                 return launch_i8_kernel<F, T, S, NF, HALF, E, 2>(stream, args, blocks, waves);
             break;
-        case int(XKind::Conv):
-            if constexpr (E == Epilogue::Single)
-                return launch_i8_kernel<F, T, S, NF, HALF, E, 3>(stream, args, blocks, waves);
-            break;
         default:
             break;
         }
@@ -1687,10 +1667,6 @@ void launch_nf4_pro(hipStream_t stream, const MfmaArgs &args, unsigned blocks, i
     case int(XKind::Swiglu):
         if constexpr (E == Epilogue::Single)
             return launch_nf4_kernel<T, S, HALF, E, 2>(stream, args, blocks, waves);
-        break;
-    case int(XKind::Conv):
-        if constexpr (E == Epilogue::Single)
-            return launch_nf4_kernel<T, S, HALF, E, 3>(stream, args, blocks, waves);
         break;
     default:
         break;

@@ -181,17 +181,12 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     if (p.rows != n || p.inner != k)
         return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
     // Every operand the transform reads must be present (the kernels do not
-    // check): a, plus b for SwiGLU, w for the norm, and for the convolution
-    // its kernel, the rolled history output and (width > 1) the history.
+    // check): a, plus b for SwiGLU and w for the norm.
     bool operands = out_a && xform.a && (epilogue != Epilogue::Pair || out_b);
     switch (xform.kind) {
     case XKind::Plain: break;
     case XKind::AddRms: operands = operands && xform.w; break;
     case XKind::Swiglu: operands = operands && xform.b; break;
-    case XKind::Conv:
-        operands = operands && xform.w && xform.side && xform.width > 0 &&
-                   (xform.width == 1 || xform.b);
-        break;
     }
     if (!operands)
         return fail(ctx, MFH_INVALID_ARGUMENT, "fused decode product is missing an operand");
@@ -209,7 +204,7 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     call.xform = xform;
     if (xform.kind == XKind::Plain)
         call.x = xform.a;  // the GEMV reads a Plain source from call.x
-    if (!use_mfma_gemv(ctx, call) || m == 0 || m > 2 || (xform.kind == XKind::Conv && m != 1))
+    if (!use_mfma_gemv(ctx, call) || m == 0 || m > 2)
         return fail(ctx, MFH_UNSUPPORTED, "fused decode product needs the matrix-core GEMV");
     DeviceGuard guard(ctx->device);
     return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
@@ -220,7 +215,7 @@ mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, u
                                  const mfh_buf *const *scales, const uint32_t *n,
                                  float *const *out)
 {
-    if (count == 0 || count > kMaxSegments || m == 0 || m > 2 || xform.kind == XKind::Conv ||
+    if (count == 0 || count > kMaxSegments || m == 0 || m > 2 ||
         !xform.a || (xform.kind == XKind::AddRms && !xform.w) ||
         (xform.kind == XKind::Swiglu && !xform.b))
         return fail(ctx, MFH_UNSUPPORTED, "fused decode product needs the matrix-core GEMV");
