@@ -334,11 +334,17 @@ __global__ __launch_bounds__(64 * kPrologueWaves) void digits_kernel(XForm t, ui
                                                                      uint32_t k, uint32_t groups,
                                                                      uint32_t nfrag,
                                                                      int8_t *afrag, float *xf,
-                                                                     int2 *corr)
+                                                                     int2 *corr, float *zero,
+                                                                     uint32_t zero_count)
 {
     __shared__ float scratch[kPrologueWaves];
     const uint32_t b = blockIdx.y;
     const uint32_t g = blockIdx.x * kPrologueWaves + (threadIdx.x >> 6);
+    // The output a K-split GEMV accumulates into starts at zero.
+    const uint32_t stride = gridDim.x * gridDim.y * blockDim.x;
+    for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+         i < zero_count; i += stride)
+        zero[i] = 0.0f;
     const float reciprocal = prologue_reciprocal(t, b, m, k, scratch);
     if (g >= groups)
         return;
@@ -511,6 +517,10 @@ struct MfmaArgs {
     XForm xform;  // activation source of the prologue
     uint32_t m, n, k, k_pad;
     uint32_t ksteps_per_wave;
+    // K split: kparts blocks per tile group, part p = blockIdx.x / part_blocks
+    // taking K steps [p, p + 1) * waves * ksteps_per_wave and adding its
+    // sums atomically into the zeroed output (Single epilogue only).
+    uint32_t kparts, part_blocks;
     // Segmented launch (one stream, T = 1): blocks [seg_first[i], next) run
     // weight stream i of seg_n[i] rows into seg_out[i]; 0 segments = off.
     uint32_t segments;
@@ -533,7 +543,7 @@ template <int T>
 __device__ __forceinline__ Target target_of(const MfmaArgs &a)
 {
     Target r;
-    uint32_t block = blockIdx.x;
+    uint32_t block = a.kparts > 1 ? blockIdx.x % a.part_blocks : blockIdx.x;
     r.n = a.n;
     for (int st = 0; st < 2; ++st) {
         r.tiles[st] = a.tiles[st];
@@ -559,7 +569,8 @@ __device__ __forceinline__ Target target_of(const MfmaArgs &a)
 template <int S, int T, int NB, Epilogue E>
 __device__ __forceinline__ void reduce_and_store(uint32_t m, const Target &tg,
                                                  float (&vals)[S][T][NB],
-                                                 const uint32_t (&batch)[NB], uint32_t j)
+                                                 const uint32_t (&batch)[NB], uint32_t j,
+                                                 bool accumulate = false)
 {
     const uint32_t tile0 = tg.tile0;
     extern __shared__ float red[];
@@ -588,7 +599,12 @@ __device__ __forceinline__ void reduce_and_store(uint32_t m, const Target &tg,
         if (b < m && row < tg.n) {
             const size_t o = size_t(b) * tg.n + row;
             if constexpr (E == Epilogue::Single) {
-                tg.out[0][o] = v[0];
+                // K-split partials: two addends onto zero, so the sum does
+                // not depend on their order.
+                if (accumulate)
+                    atomicAdd(&tg.out[0][o], v[0]);
+                else
+                    tg.out[0][o] = v[0];
             } else if constexpr (E == Epilogue::Pair) {
                 tg.out[0][o] = v[0];
                 tg.out[1][o] = v[S - 1];
@@ -947,7 +963,8 @@ void gemv_i8_kernel(MfmaArgs a)
     const Target tg = target_of<T>(a);
     const uint32_t tile0 = tg.tile0;
     const uint32_t groups = a.k_pad / 128;
-    const uint32_t s_begin = wave * a.ksteps_per_wave;
+    const uint32_t part = a.kparts > 1 ? blockIdx.x / a.part_blocks : 0;
+    const uint32_t s_begin = (part * (blockDim.x >> 6) + wave) * a.ksteps_per_wave;
     const uint32_t nblk = a.ksteps_per_wave / B::LB;
     const uint32_t g_begin = s_begin / 2;
     const size_t tile_vecs = size_t(a.k_pad) / 64 / KPL * 64;
@@ -1147,7 +1164,7 @@ void gemv_i8_kernel(MfmaArgs a)
 #pragma unroll
     for (int f = 0; f < NF; ++f)
         batch[f] = 4 * f + q;
-    reduce_and_store<S, T, NF, E>(a.m, tg, accf, batch, j);
+    reduce_and_store<S, T, NF, E>(a.m, tg, accf, batch, j, a.kparts > 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1552,6 +1569,14 @@ Plan plan_for(uint32_t n_tiles, uint32_t ksteps, uint32_t lb, int max_t, bool wi
 // take it (one tile, one stream, one fragment; separate or register
 // prologue).
 constexpr int kDeepWaves = 16;
+// Largest grid (blocks) that takes the two-part K split.
+constexpr uint32_t kSplitMaxBlocks = 128;
+
+// Whether float ranges [a, a + na) and [b, b + nb) share memory.
+bool overlaps(const float *a, size_t na, const float *b, size_t nb)
+{
+    return a < b + nb && b < a + na;
+}
 Plan deepen(Plan p, uint32_t n_tiles, uint32_t ksteps, uint32_t lb)
 {
     if (p.tiles_per_block == 1 && p.waves == 8 && uint64_t(n_tiles) * 8 < 2048 &&
@@ -1830,11 +1855,23 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     plan.tiles_per_block = tiles_of(plan);
     if ((pro < 0 || pro == kRegPro) && streams == 1 && nf == 1)
         plan = deepen(plan, n_tiles, ksteps, Geo<F>::lb);
+    // Small grids with the separate prologue split K over two blocks per
+    // tile group (MfmaArgs::kparts); the prologue kernel zeroes the output
+    // they add into, so the output must not overlap the activations.
+    const uint32_t kparts = pro < 0 && streams == 1 && !call.segments &&
+                                    xform.kind == XKind::Plain &&
+                                    n_tiles / plan.tiles_per_block <= kSplitMaxBlocks &&
+                                    ksteps % (2 * plan.waves * Geo<F>::lb) == 0 &&
+                                    !overlaps(call.out_a, size_t(call.m) * call.n, xform.a,
+                                              size_t(call.m) * call.k)
+                                ? 2
+                                : 1;
     if (pro < 0)
         digits_kernel<F>
             <<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 4 * nf), 64 * kPrologueWaves,
                0, stream>>>(xform, call.m, call.k, groups, nf, static_cast<int8_t *>(sc.afrag),
-                            sc.xf, sc.corr);
+                            sc.xf, sc.corr, kparts > 1 ? call.out_a : nullptr,
+                            kparts > 1 ? call.m * call.n : 0);
     MfmaArgs args{};
     args.xform = xform;
     args.k = call.k;
@@ -1850,9 +1887,11 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     args.m = call.m;
     args.n = call.n;
     args.k_pad = k_pad;
-    args.ksteps_per_wave = ksteps / plan.waves;
+    args.ksteps_per_wave = ksteps / (plan.waves * kparts);
+    args.kparts = kparts;
+    args.part_blocks = n_tiles / plan.tiles_per_block;
     set_segments(args, call);
-    const unsigned blocks = n_tiles / plan.tiles_per_block;
+    const unsigned blocks = n_tiles / plan.tiles_per_block * kparts;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {
         if (plan.tiles_per_block == 4)
