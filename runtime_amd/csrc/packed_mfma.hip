@@ -423,12 +423,19 @@ __device__ __forceinline__ void block_prologue(const XForm &t, uint32_t m, uint3
 
 __global__ __launch_bounds__(64 * kPrologueWaves) void halves_kernel(XForm t, uint32_t m,
                                                                      uint32_t k, uint32_t groups,
-                                                                     _Float16 *afrag, float *xf)
+                                                                     _Float16 *afrag, float *xf,
+                                                                     float *zero,
+                                                                     uint32_t zero_count)
 {
     __shared__ float scratch[kPrologueWaves];
     const uint32_t b = blockIdx.y;
     const uint32_t g = blockIdx.x * kPrologueWaves + (threadIdx.x >> 6);
     const uint32_t lane = threadIdx.x & 63;
+    // The output a K-split GEMV accumulates into starts at zero.
+    const uint32_t stride = gridDim.x * gridDim.y * blockDim.x;
+    for (uint32_t i = (blockIdx.y * gridDim.x + blockIdx.x) * blockDim.x + threadIdx.x;
+         i < zero_count; i += stride)
+        zero[i] = 0.0f;
     const float reciprocal = prologue_reciprocal(t, b, m, k, scratch);
     if (g >= groups)
         return;
@@ -1365,7 +1372,9 @@ void gemv_nf4_kernel(MfmaArgs a)
     const Target tg = target_of<T>(a);
     const uint32_t tile0 = tg.tile0;
     const uint32_t groups = a.k_pad / 128;
-    const uint32_t s_begin = wave * a.ksteps_per_wave;  // 32-wide ksteps
+    const uint32_t part = a.kparts > 1 ? blockIdx.x / a.part_blocks : 0;
+    const uint32_t s_begin =
+        (part * (blockDim.x >> 6) + wave) * a.ksteps_per_wave;  // 32-wide ksteps
     const uint32_t nblk = a.ksteps_per_wave / 4;
     const uint32_t g_begin = s_begin / 4;
     const size_t tile_vecs = size_t(a.k_pad) / 128 * 64;
@@ -1460,7 +1469,7 @@ void gemv_nf4_kernel(MfmaArgs a)
         main_loop(gap);
     }
     const uint32_t batch[2] = {2 * q, 2 * q + 1};
-    reduce_and_store<S, T, 2, E>(a.m, tg, accf, batch, j);
+    reduce_and_store<S, T, 2, E>(a.m, tg, accf, batch, j, a.kparts > 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -1945,10 +1954,20 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     }
     if ((pro < 0 || pro == kRegPro) && streams == 1)
         plan = deepen(plan, n_tiles, ksteps, 4);
+    // The two-part K split of gemv_i8_format.
+    const uint32_t kparts = pro < 0 && streams == 1 && !call.segments &&
+                                    xform.kind == XKind::Plain &&
+                                    n_tiles / plan.tiles_per_block <= kSplitMaxBlocks &&
+                                    ksteps % (2 * plan.waves * 4) == 0 &&
+                                    !overlaps(call.out_a, size_t(call.m) * call.n, xform.a,
+                                              size_t(call.m) * call.k)
+                                ? 2
+                                : 1;
     if (pro < 0)
         halves_kernel<<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 8),
-                        64 * kPrologueWaves, 0, stream>>>(xform, call.m, call.k, groups,
-                                                          static_cast<_Float16 *>(sc.afrag), sc.xf);
+                        64 * kPrologueWaves, 0, stream>>>(
+            xform, call.m, call.k, groups, static_cast<_Float16 *>(sc.afrag), sc.xf,
+            kparts > 1 ? call.out_a : nullptr, kparts > 1 ? call.m * call.n : 0);
     MfmaArgs args{};
     args.xform = xform;
     args.k = call.k;
@@ -1963,9 +1982,11 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     args.m = call.m;
     args.n = call.n;
     args.k_pad = k_pad;
-    args.ksteps_per_wave = ksteps / plan.waves;
+    args.ksteps_per_wave = ksteps / (plan.waves * kparts);
+    args.kparts = kparts;
+    args.part_blocks = n_tiles / plan.tiles_per_block;
     set_segments(args, call);
-    const unsigned blocks = n_tiles / plan.tiles_per_block;
+    const unsigned blocks = n_tiles / plan.tiles_per_block * kparts;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     if (streams == 1) {
         if (plan.tiles_per_block == 2)
