@@ -1866,15 +1866,20 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
         plan = deepen(plan, n_tiles, ksteps, Geo<F>::lb);
     // Small grids with the separate prologue split K over two blocks per
     // tile group (MfmaArgs::kparts); the prologue kernel zeroes the output
-    // they add into, so the output must not overlap the activations.
-    const uint32_t kparts = pro < 0 && streams == 1 && !call.segments &&
-                                    xform.kind == XKind::Plain &&
-                                    n_tiles / plan.tiles_per_block <= kSplitMaxBlocks &&
-                                    ksteps % (2 * plan.waves * Geo<F>::lb) == 0 &&
-                                    !overlaps(call.out_a, size_t(call.m) * call.n, xform.a,
-                                              size_t(call.m) * call.k)
-                                ? 2
-                                : 1;
+    // they add into, so the output must not overlap the activations.  Where
+    // K does not divide over twice the waves, each part takes half of them
+    // (the same K range per wave over twice the blocks).
+    uint32_t kparts = 1;
+    if (pro < 0 && streams == 1 && !call.segments && xform.kind == XKind::Plain &&
+        n_tiles / plan.tiles_per_block <= kSplitMaxBlocks &&
+        !overlaps(call.out_a, size_t(call.m) * call.n, xform.a, size_t(call.m) * call.k)) {
+        if (ksteps % (2 * plan.waves * Geo<F>::lb) == 0) {
+            kparts = 2;
+        } else if (plan.waves % 2 == 0 && ksteps % (plan.waves * Geo<F>::lb) == 0) {
+            plan.waves /= 2;
+            kparts = 2;
+        }
+    }
     if (pro < 0)
         digits_kernel<F>
             <<<dim3((groups + kPrologueWaves - 1) / kPrologueWaves, 4 * nf), 64 * kPrologueWaves,
