@@ -1006,24 +1006,56 @@ __global__ __launch_bounds__(kBlock) void gqa_combine_kernel(float *__restrict__
     __shared__ float scratch[kBlock / 64];
     const uint64_t record = uint64_t(head_dim) + 2;
     const float *rec = partial + uint64_t(blockIdx.x) * splits * record;
+    const uint32_t parts = head_dim <= kBlock ? kBlock / head_dim : 1;
+    const uint32_t part_id = threadIdx.x / head_dim, dim0 = threadIdx.x % head_dim;
+    // Every load goes out before the reductions: this thread's range
+    // record (m, l) when splits fit the block, and the acc values it sums
+    // when head_dim fits the block and it sums at most kHeld of them.
+    constexpr uint32_t kHeld = 16;
+    const bool own = splits <= kBlock;
+    const bool holds = part_id < parts && head_dim <= kBlock && splits <= parts * kHeld;
+    float m_own = 0.0f, l_own = 0.0f;
+    if (own && threadIdx.x < splits) {
+        m_own = rec[threadIdx.x * record];
+        l_own = rec[threadIdx.x * record + 1];
+    }
+    float held[kHeld];
+#pragma unroll
+    for (uint32_t i = 0; i < kHeld; ++i) {
+        const uint32_t s = part_id + i * parts;
+        held[i] = holds && s < splits ? rec[s * record + 2 + dim0] : 0.0f;
+    }
     float maximum = -__builtin_inff();
-    for (uint32_t s = threadIdx.x; s < splits; s += kBlock)
-        if (rec[s * record + 1] != 0.0f)
-            maximum = fmaxf(maximum, rec[s * record]);
+    if (own) {
+        if (threadIdx.x < splits && l_own != 0.0f)
+            maximum = fmaxf(maximum, m_own);
+    } else {
+        for (uint32_t s = threadIdx.x; s < splits; s += kBlock)
+            if (rec[s * record + 1] != 0.0f)
+                maximum = fmaxf(maximum, rec[s * record]);
+    }
     maximum = block_max(maximum, scratch);
     float denominator = 0.0f;
     for (uint32_t s = threadIdx.x; s < splits; s += kBlock) {
         // An empty range stores l = 0 and acc = 0: weight 0 drops it.
-        const float l = rec[s * record + 1];
-        const float w = l != 0.0f ? expf(rec[s * record] - maximum) : 0.0f;
+        const float l = own ? l_own : rec[s * record + 1];
+        const float m = own ? m_own : rec[s * record];
+        const float w = l != 0.0f ? expf(m - maximum) : 0.0f;
         weight[s] = w;
         if (l != 0.0f)
             denominator += l * w;
     }
     denominator = block_sum(denominator, scratch);  // also orders the weight stores
-    const uint32_t parts = head_dim <= kBlock ? kBlock / head_dim : 1;
-    const uint32_t part_id = threadIdx.x / head_dim, dim0 = threadIdx.x % head_dim;
-    if (part_id < parts) {
+    if (holds) {
+        float acc = 0.0f;
+#pragma unroll
+        for (uint32_t i = 0; i < kHeld; ++i) {
+            const uint32_t s = part_id + i * parts;
+            if (s < splits)
+                acc += held[i] * weight[s];
+        }
+        part[part_id * head_dim + dim0] = acc;
+    } else if (part_id < parts) {
         for (uint32_t dim = dim0; dim < head_dim; dim += kBlock) {
             float acc = 0.0f;
             for (uint32_t s = part_id; s < splits; s += parts)
