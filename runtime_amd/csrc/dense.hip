@@ -162,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void gather_columns_kernel(float *__restric
 // are cut into ranges scanned by separate blocks whose candidates a second
 // kernel reduces the same way.
 constexpr int kArgmaxBlock = 1024;
-constexpr uint32_t kArgmaxRange = 8192;
+constexpr uint32_t kArgmaxRange = 2048;
 
 struct Candidate {
     float value;
