@@ -1156,6 +1156,20 @@ __global__ __launch_bounds__(kBlock) void gqa_decode_kernel(DecodeAttention p)
                     vq[u] = *reinterpret_cast<const float4 *>(values + key * kv_width + c);
                 }
             }
+            if (base == 0) {
+                // The group's query heads (and the new key) are normalised
+                // and rotated while the range's keys and values are in
+                // flight; an empty range needs neither.
+                for (uint32_t h = wave; h < group; h += kBlock / 64)
+                    norm_rope_head_table(p.query + (head0 + h) * uint64_t(d), q + h * d, nullptr,
+                                         p.query_weight, d, rot, rot + half, p.epsilon);
+                if (holds_new && wave == kBlock / 64 - 1)
+                    norm_rope_head_table(p.key + kv_head * uint64_t(d),
+                                         kl + (count - 1) * (d + 1),
+                                         p.key_cache + p.position * kv_width +
+                                             kv_head * uint64_t(d),
+                                         p.key_weight, d, rot, rot + half, p.epsilon);
+            }
 #pragma unroll
             for (uint32_t u = 0; u < kStage; ++u) {
                 const uint32_t i = base + u * kBlock + threadIdx.x;
@@ -1173,14 +1187,6 @@ __global__ __launch_bounds__(kBlock) void gqa_decode_kernel(DecodeAttention p)
             }
         }
     }
-    __syncthreads();
-    for (uint32_t h = wave; h < group; h += kBlock / 64)
-        norm_rope_head_table(p.query + (head0 + h) * uint64_t(d), q + h * d, nullptr,
-                             p.query_weight, d, rot, rot + half, p.epsilon);
-    if (holds_new && wave == kBlock / 64 - 1)
-        norm_rope_head_table(p.key + kv_head * uint64_t(d), kl + (count - 1) * (d + 1),
-                             p.key_cache + p.position * kv_width + kv_head * uint64_t(d),
-                             p.key_weight, d, rot, rot + half, p.epsilon);
     __syncthreads();
 
     float *out_records = p.partial + (uint64_t(head0) * splits + split) * record;
