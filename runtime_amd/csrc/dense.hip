@@ -281,6 +281,29 @@ __global__ __launch_bounds__(kArgmaxBlock) void argmax_final_kernel(
     }
 }
 
+// The same reduction by one wave (few ranges): shuffles only, no barrier.
+// The merge keeps the largest value, the lowest index among equal values and
+// any poison, so the order of the merges does not change the result.
+__global__ __launch_bounds__(64) void argmax_final_wave_kernel(float *__restrict__ out,
+                                                               float *__restrict__ copy,
+                                                               const Candidate *__restrict__ partial,
+                                                               uint32_t ranges)
+{
+    Candidate c{-__builtin_inff(), UINT32_MAX, 0};
+    const Candidate *row = partial + uint64_t(blockIdx.x) * ranges;
+    for (uint32_t i = threadIdx.x; i < ranges; i += 64)
+        merge(c, row[i].value, row[i].index, row[i].poisoned);
+#pragma unroll
+    for (int offset = 32; offset > 0; offset >>= 1)
+        merge(c, __shfl_xor(c.value, offset, 64), __shfl_xor(c.index, offset, 64),
+              __shfl_xor(c.poisoned, offset, 64));
+    if (threadIdx.x == 0) {
+        out[blockIdx.x] = argmax_marker(c);
+        if (copy)
+            copy[blockIdx.x] = argmax_marker(c);
+    }
+}
+
 // ---- element-wise ------------------------------------------------------
 
 template <int OP>
@@ -1456,7 +1479,10 @@ void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t row
         Candidate *partial = static_cast<Candidate *>(scratch);
         argmax_range_kernel<<<rows * ranges, kArgmaxBlock, 0, stream>>>(partial, in, width,
                                                                        ranges, mask);
-        argmax_final_kernel<<<rows, kArgmaxBlock, 0, stream>>>(out, copy, partial, ranges);
+        if (ranges <= 64)
+            argmax_final_wave_kernel<<<rows, 64, 0, stream>>>(out, copy, partial, ranges);
+        else
+            argmax_final_kernel<<<rows, kArgmaxBlock, 0, stream>>>(out, copy, partial, ranges);
         return;
     }
     argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, copy, in, rows, width,
