@@ -154,9 +154,17 @@ const char *mfh_status_message(mfh_status status);
 mfh_status mfh_identity(const mfh_ctx *ctx, mfh_backend_identity *out);
 /* InferenceOps::capabilities (inference.rs:47). */
 mfh_status mfh_capabilities(const mfh_ctx *ctx, mfh_backend_capabilities *out);
-/* InferenceOps::resource_report (inference.rs:48). */
+/* InferenceOps::resource_report (inference.rs:48).  Counts physical bytes,
+ * like the reference's wgpu backend (backend-wgpu/src/lib.rs:340-370): each
+ * live buffer's device block and its backend-private derived copies (the
+ * binary16 scale shadow, repacked code tiles, tiled scales) under the
+ * buffer's class; context scratch and idle pooled blocks under scratch;
+ * pinned staging of unpolled readbacks as pending bytes.  The sum is the
+ * context's device footprint plus that staging, and every allocation that
+ * would take it past max_total_bytes fails with MFH_RESOURCE_LIMIT. */
 mfh_status mfh_resource_report(const mfh_ctx *ctx, mfh_report *out);
-/* InferenceOps::peak_accounted_bytes (inference.rs:52-56). */
+/* InferenceOps::peak_accounted_bytes (inference.rs:52-56): the highest
+ * such total since mfh_create. */
 mfh_status mfh_peak_accounted_bytes(const mfh_ctx *ctx, uint64_t *out);
 /* InferenceOps::advance_generation (inference.rs:57): older buffers then
  * fail with MFH_STALE_BUFFER (backend-cpu/src/storage.rs:258-267). */
@@ -249,8 +257,21 @@ mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf
 mfh_status mfh_packed_swiglu_pair(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
                                   const mfh_buf *codes_a, const mfh_buf *scales_a,
                                   const mfh_buf *codes_b, const mfh_buf *scales_b);
+/* Build the backend-private copies the matrix-core kernels read for this
+ * (codes, scales) pair now: codes repacked into the tile layout of the format
+ * the widths select and scales in tile order, charged to the buffers'
+ * allocation classes.  Admission is packed_linear's (format, row count,
+ * INT8 reserved code).  A loader calls it after uploading each packed weight
+ * so that a ResourceLimit surfaces at load, the way the reference funds its
+ * LUT2 repack at construction (executor-core/src/lfm2/executor/
+ * construction.rs:404-424).  Without it the first packed operation on the
+ * pair builds the copies, under the same accounting and limits, before
+ * enqueueing anything else.  Idempotent. */
+mfh_status mfh_prepare_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales);
+/* 1 when the pair's copies exist for the format its widths select, else 0. */
+int mfh_packed_prepared(const mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales);
 /* InferenceOps::supports_ternary_lut2 (inference.rs:259-261).  Always 0:
- * the backend's private repack (done at first use) replaces LUT2, so the
+ * the backend's private repack (mfh_prepare_packed) replaces LUT2, so the
  * *_lut2 hooks report MFH_UNSUPPORTED like the trait defaults
  * (inference.rs:268-309). */
 int mfh_supports_ternary_lut2(const mfh_ctx *ctx);
@@ -338,7 +359,9 @@ mfh_status mfh_swiglu(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *gate, const 
 void *mfh_stream(const mfh_ctx *ctx);
 /* Kernel path for packed GEMV/GEMM: 0 = automatic selection, 1 = FP32 FMA
  * kernels only, 2 = automatic but with the matrix-core GEMV's activation
- * prologue run as a kernel of its own.  Returns the previous setting. */
+ * prologue run as a kernel of its own, 3 = automatic kernels, with the LFM2
+ * one-token pass issued op by op through these entry points instead of the
+ * fused decode step.  Returns the previous setting. */
 int mfh_set_kernel_path(mfh_ctx *ctx, int path);
 
 #ifdef __cplusplus

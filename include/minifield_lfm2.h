@@ -68,6 +68,7 @@ typedef enum mfl_role {
 } mfl_role;
 
 typedef struct mfl_model mfl_model;
+typedef struct mfl_prefix mfl_prefix;
 
 /* Validate the configuration and allocate the prefix state (zeroed
  * convolution histories and KV caches of `max_tokens` rows). */
@@ -107,6 +108,21 @@ mfh_status mfl_generate(mfl_model *model, uint32_t steps, mfh_buf *ids_out);
  * mfl_destroy; readable with mfh_read_f32_async). */
 const mfh_buf *mfl_logits(const mfl_model *model);
 const mfh_buf *mfl_sampled(const mfl_model *model);
+
+/* Lfm2Prefix (crates/executor-core/src/lfm2/executor.rs:249-281): an
+ * immutable copy of the model's current prefix state -- per layer the
+ * convolution history or the live key/value rows, the last pass's logits and
+ * sampled id, and the lengths -- in Cache-class buffers of the model's
+ * context.  The model keeps running from its own state. */
+mfh_status mfl_snapshot(mfl_model *model, mfl_prefix **out);
+/* Continue from a stored prefix: the model's prefix state becomes a copy of
+ * `prefix`, which stays unchanged and can be restored again (the reference's
+ * fork of a shared prefix, prefix_task.rs:158 and executor/storage.rs:104-155).
+ * The prefix must come from this model (MFH_INVALID_ARGUMENT otherwise). */
+mfh_status mfl_restore(mfl_model *model, const mfl_prefix *prefix);
+uint64_t mfl_prefix_length(const mfl_prefix *prefix);
+/* Release a prefix's buffers (before its context is destroyed). */
+void mfl_prefix_destroy(mfl_prefix *prefix);
 
 #ifdef __cplusplus
 }

@@ -54,6 +54,8 @@ _SIGS = {
     "mfo_argmax": (None, [_f, _f, _SZ, _SZ, _u64]),
     "mfo_gather_rows": (ctypes.c_int, [_f, _f, _SZ, _SZ, _i64, _SZ]),
     "mfo_causal_gqa": (ctypes.c_int, [_f, _f, _f, _f, _f, _f, _u64, _SZ, _SZ, _SZ, _SZ]),
+    "mfo_causal_gqa_cached": (ctypes.c_int, [_f, _f, _f, _f, _f, _f, _u64, _SZ, _SZ, _SZ, _SZ,
+                                             _SZ]),
     "mfo_gated_short_convolution": (ctypes.c_int, [_f, _f, _f, _f, _SZ, _SZ, _SZ]),
 }
 
@@ -358,16 +360,26 @@ def copy_rect_2d(dst, src, rect) -> np.ndarray:
 
 
 def causal_gqa(query, key, value, key_cache, value_cache, cache_len, query_heads, key_heads,
-               head_dim):
-    """Returns (output, key_cache, value_cache, new_cache_len); the caches
-    passed in are not modified."""
+               head_dim, threads: int = 0, in_place: bool = False):
+    """Returns (output, key_cache, value_cache, new_cache_len).  The caches
+    passed in are not modified unless `in_place` (then they are returned,
+    updated).  `threads` > 0 takes the score-cached restatement on that many
+    threads (the same bits)."""
     query, key, value = _c32(query), _c32(key), _c32(value)
-    kc, vc = _c32(key_cache).copy(), _c32(value_cache).copy()
+    if in_place:
+        kc, vc = key_cache, value_cache
+        assert kc.dtype == np.float32 and vc.dtype == np.float32
+        assert kc.flags.c_contiguous and vc.flags.c_contiguous
+    else:
+        kc, vc = _c32(key_cache).copy(), _c32(value_cache).copy()
     out = np.zeros_like(query)
     length = ctypes.c_uint64(cache_len)
-    _check(lib().mfo_causal_gqa(_fp(out), _fp(query), _fp(key), _fp(value), _fp(kc), _fp(vc),
-                                ctypes.byref(length), query.shape[0], query_heads, key_heads,
-                                head_dim))
+    args = (_fp(out), _fp(query), _fp(key), _fp(value), _fp(kc), _fp(vc), ctypes.byref(length),
+            query.shape[0], query_heads, key_heads, head_dim)
+    if threads > 0:
+        _check(lib().mfo_causal_gqa_cached(*args, threads))
+    else:
+        _check(lib().mfo_causal_gqa(*args))
     return out, kc, vc, length.value
 
 

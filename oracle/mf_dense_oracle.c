@@ -23,6 +23,7 @@
  * and brute-force argmax.
  */
 #include <math.h>
+#include <pthread.h>
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
@@ -331,6 +332,145 @@ int mfo_causal_gqa(float *out, const float *query, const float *key, const float
     free(staged);
     *cache_len = initial_len + tokens;
     return MFO_OK;
+}
+
+/* mfo_causal_gqa with each (token, query head)'s scores computed once and
+ * the units spread over `threads` threads.  The reference recomputes
+ * gqa_score in each of its three passes (attention_convolution.rs:139-176),
+ * but gqa_score is a pure function of its inputs (:190-216) and exp() of the
+ * same argument is the same value, so caching the scores and their
+ * exponentials changes no bit: every sum is taken in the reference's order
+ * over the same values.  A non-finite score, denominator or output fails
+ * the call with the same status, and then nothing is written. */
+struct gqa_job {
+    float *staged;
+    const float *query, *key, *value, *key_cache, *value_cache;
+    size_t tokens, query_heads, group, head_dim, query_width, kv_width, initial_len;
+    float scale;
+    size_t next;  /* next unit, taken under `lock` */
+    int status;
+    pthread_mutex_t lock;
+};
+
+static void *gqa_worker(void *arg)
+{
+    struct gqa_job *job = (struct gqa_job *)arg;
+    const size_t most = job->initial_len + job->tokens;
+    float *scores = (float *)malloc((most ? most : 1) * sizeof(float));
+    float *weights = (float *)malloc((most ? most : 1) * sizeof(float));
+    if (!scores || !weights) {
+        pthread_mutex_lock(&job->lock);
+        job->status = MFO_ERR_RESOURCE_LIMIT;
+        pthread_mutex_unlock(&job->lock);
+        free(scores);
+        free(weights);
+        return NULL;
+    }
+    const size_t units = job->tokens * job->query_heads;
+    for (;;) {
+        pthread_mutex_lock(&job->lock);
+        const size_t unit = job->next++;
+        const int stop = job->status != MFO_OK;
+        pthread_mutex_unlock(&job->lock);
+        if (stop || unit >= units)
+            break;
+        const size_t token = unit / job->query_heads, qh = unit % job->query_heads;
+        const size_t kv_head = qh / job->group;
+        const size_t visible = job->initial_len + token + 1;
+        const size_t query_start = token * job->query_width + qh * job->head_dim;
+        int status = MFO_OK;
+        float maximum = -INFINITY;
+        for (size_t j = 0; j < visible && !status; ++j) {
+            scores[j] = gqa_score(job->query, job->key, job->key_cache, job->initial_len, j,
+                                  query_start, kv_head, job->kv_width, job->head_dim, job->scale);
+            if (!isfinite(scores[j]))
+                status = MFO_ERR_BACKEND_FAILURE;
+            maximum = fmaxf(maximum, scores[j]);
+        }
+        float denominator = 0.0f;
+        for (size_t j = 0; j < visible && !status; ++j) {
+            weights[j] = expf(scores[j] - maximum);
+            denominator += weights[j];
+        }
+        if (!status && (!isfinite(denominator) || denominator <= 0.0f))
+            status = MFO_ERR_BACKEND_FAILURE;
+        for (size_t d = 0; d < job->head_dim && !status; ++d) {
+            float weighted = 0.0f;
+            for (size_t j = 0; j < visible; ++j) {
+                const float probability = weights[j] / denominator;
+                const float v =
+                    j < job->initial_len
+                        ? job->value_cache[j * job->kv_width + kv_head * job->head_dim + d]
+                        : job->value[(j - job->initial_len) * job->kv_width +
+                                     kv_head * job->head_dim + d];
+                weighted += probability * v;
+            }
+            if (!isfinite(weighted))
+                status = MFO_ERR_BACKEND_FAILURE;
+            job->staged[query_start + d] = weighted;
+        }
+        if (status) {
+            pthread_mutex_lock(&job->lock);
+            job->status = status;
+            pthread_mutex_unlock(&job->lock);
+        }
+    }
+    free(scores);
+    free(weights);
+    return NULL;
+}
+
+int mfo_causal_gqa_cached(float *out, const float *query, const float *key, const float *value,
+                          float *key_cache, float *value_cache, uint64_t *cache_len,
+                          size_t tokens, size_t query_heads, size_t key_heads, size_t head_dim,
+                          size_t threads)
+{
+    struct gqa_job job;
+    memset(&job, 0, sizeof job);
+    job.group = query_heads / key_heads;
+    job.query_width = query_heads * head_dim;
+    job.kv_width = key_heads * head_dim;
+    job.initial_len = (size_t)*cache_len;
+    job.scale = 1.0f / sqrtf((float)head_dim);
+    job.query = query;
+    job.key = key;
+    job.value = value;
+    job.key_cache = key_cache;
+    job.value_cache = value_cache;
+    job.tokens = tokens;
+    job.query_heads = query_heads;
+    job.head_dim = head_dim;
+    job.status = MFO_OK;
+    const size_t staged_count = tokens * job.query_width;
+    job.staged = (float *)malloc((staged_count ? staged_count : 1) * sizeof(float));
+    if (!job.staged)
+        return MFO_ERR_RESOURCE_LIMIT;
+    pthread_mutex_init(&job.lock, NULL);
+    if (threads < 1)
+        threads = 1;
+    if (threads > 64)
+        threads = 64;
+    pthread_t pool[64];
+    size_t started = 0;
+    for (; started < threads; ++started)
+        if (pthread_create(&pool[started], NULL, gqa_worker, &job) != 0)
+            break;
+    if (started == 0)
+        gqa_worker(&job);
+    for (size_t i = 0; i < started; ++i)
+        pthread_join(pool[i], NULL);
+    pthread_mutex_destroy(&job.lock);
+    const int status = job.status;
+    if (status == MFO_OK) {
+        memcpy(key_cache + job.initial_len * job.kv_width, key,
+               tokens * job.kv_width * sizeof(float));
+        memcpy(value_cache + job.initial_len * job.kv_width, value,
+               tokens * job.kv_width * sizeof(float));
+        memcpy(out, job.staged, staged_count * sizeof(float));
+        *cache_len = job.initial_len + tokens;
+    }
+    free(job.staged);
+    return status;
 }
 
 /* CpuBackend::gated_short_convolution, attention_convolution.rs:269-339. */

@@ -69,6 +69,12 @@ int mfo_gather_rows(float *out, const float *table, size_t rows, size_t columns,
 int mfo_causal_gqa(float *out, const float *query, const float *key, const float *value,
                    float *key_cache, float *value_cache, uint64_t *cache_len, size_t tokens,
                    size_t query_heads, size_t key_heads, size_t head_dim);
+/* mfo_causal_gqa with the scores cached per (token, query head) and the
+ * units spread over `threads` threads: the same bits and statuses. */
+int mfo_causal_gqa_cached(float *out, const float *query, const float *key, const float *value,
+                          float *key_cache, float *value_cache, uint64_t *cache_len,
+                          size_t tokens, size_t query_heads, size_t key_heads, size_t head_dim,
+                          size_t threads);
 int mfo_gated_short_convolution(float *out, const float *projection, const float *kernel,
                                 float *history, size_t tokens, size_t hidden, size_t width);
 

@@ -98,6 +98,8 @@ SIGNATURES = {
     "mfh_packed_linear_pair": (S, [P, P, P, P, P, P, P, P]),
     "mfh_packed_swiglu_linear": (S, [P, P, P, P, P, P]),
     "mfh_packed_swiglu_pair": (S, [P, P, P, P, P, P, P]),
+    "mfh_prepare_packed": (S, [P, P, P]),
+    "mfh_packed_prepared": (ctypes.c_int, [P, P, P]),
     "mfh_supports_ternary_lut2": (ctypes.c_int, [P]),
     # dense ops
     "mfh_copy": (S, [P, P, P]),
@@ -131,6 +133,10 @@ SIGNATURES = {
     "mfl_generate": (S, [P, ctypes.c_uint32, P]),
     "mfl_logits": (P, [P]),
     "mfl_sampled": (P, [P]),
+    "mfl_snapshot": (S, [P, PP]),
+    "mfl_restore": (S, [P, P]),
+    "mfl_prefix_length": (ctypes.c_uint64, [P]),
+    "mfl_prefix_destroy": (None, [P]),
     # diagnostics
     "mfh_stream": (P, [P]),
     "mfh_set_kernel_path": (ctypes.c_int, [P, ctypes.c_int]),

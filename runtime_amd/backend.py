@@ -292,6 +292,13 @@ class HipBackend:
             self._check(lib.mfh_packed_gather_rows(self._ctx, output.handle, codes.handle,
                                                    scales.handle, ptr, host.size, None))
 
+    def prepare_packed(self, codes: Buffer, scales: Buffer) -> None:
+        """Build the pair's private tile copies now (mfh_prepare_packed)."""
+        self._check(_ffi.lib().mfh_prepare_packed(self._ctx, codes.handle, scales.handle))
+
+    def packed_prepared(self, codes: Buffer, scales: Buffer) -> bool:
+        return bool(_ffi.lib().mfh_packed_prepared(self._ctx, codes.handle, scales.handle))
+
     def packed_linear(self, output: Buffer, input: Buffer, codes: Buffer, scales: Buffer) -> None:
         self._check(_ffi.lib().mfh_packed_linear(self._ctx, output.handle, input.handle,
                                                  codes.handle, scales.handle))

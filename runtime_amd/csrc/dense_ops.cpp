@@ -32,7 +32,7 @@ const void *stage(mfh_ctx *ctx, const void *host, size_t bytes, mfh_status *stat
 {
     void *dst = ids_scratch(ctx, bytes ? bytes : 4);
     if (!dst) {
-        *status = fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        *status = allocation_failed(ctx);
         return nullptr;
     }
     if (bytes && hipMemcpyAsync(dst, host, bytes, hipMemcpyHostToDevice, ctx->stream) != hipSuccess) {
@@ -202,7 +202,7 @@ mfh_status run_argmax(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input, const
     if (const size_t bytes = argmax_scratch_bytes(rows, width)) {
         partials = work_scratch(ctx, bytes);
         if (!partials)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+            return allocation_failed(ctx);
     }
     launch_argmax(ctx->stream, dev_f32(output), dev_f32(input), rows, width, dev_mask, partials);
     return launched(ctx);
@@ -721,7 +721,7 @@ mfh_status mfh_causal_gqa(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *query,
     if (const size_t bytes = gqa_scratch_bytes(g)) {
         partials = static_cast<float *>(work_scratch(ctx, bytes));
         if (!partials)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+            return allocation_failed(ctx);
     }
     launch_gqa(ctx->stream, dev_f32(output), dev_f32(query), dev_f32(key), dev_f32(value),
                dev_f32(key_cache), dev_f32(value_cache), g, partials);

@@ -32,20 +32,29 @@ struct Error {
 // Size-bucketed caching allocator over hipMalloc.  All device work of a
 // context runs on one stream, so a block released by the host can be handed
 // to the next allocation immediately: any later use is stream-ordered after
-// every use already queued.
+// every use already queued.  Every block it holds, handed out or idle, counts
+// as the context's device footprint (`reserved`).
 class Pool {
 public:
     explicit Pool(int device) : device_(device) {}
     ~Pool();
-    void *acquire(size_t bytes, size_t *capacity);
+    // An idle block of bucket(bytes) .. 1.25 x that, or null.
+    void *take(size_t bytes, size_t *capacity);
+    // A new block of bucket(bytes) from the driver, or null.
+    void *grow(size_t bytes, size_t *capacity);
     void release(void *ptr, size_t capacity);
+    // Return every idle block to the driver.  The caller first makes sure no
+    // queued work still uses them.
+    void evict_idle();
     size_t reserved() const { return reserved_; }
+    size_t idle() const { return idle_; }
 
 private:
     int device_;
     size_t reserved_ = 0;
+    size_t idle_ = 0;
     std::multimap<size_t, void *> free_;
-    std::vector<void *> all_;
+    std::unordered_set<void *> all_;
 };
 
 size_t pool_bucket(size_t bytes);
@@ -57,8 +66,12 @@ struct mfh_ctx {
     hipStream_t stream = nullptr;
     mfh_backend_identity identity{};
     mfh_limits limits{};
-    uint64_t live_by_class[4] = {0, 0, 0, 0};
-    uint64_t live_bytes = 0;
+    // Device bytes held per allocation class: each live buffer's block plus
+    // its backend-private derived copies (binary16 shadow, repacked tiles,
+    // tiled scales), charged to the buffer's class.  Context scratch and
+    // idle pooled blocks are the rest of the pool's reserve and count as
+    // scratch.
+    uint64_t held_by_class[4] = {0, 0, 0, 0};
     uint64_t peak_bytes = 0;
     uint64_t pending_result_bytes = 0;
     uint32_t pending_operations = 0;
@@ -92,7 +105,7 @@ struct mfh_buf {
     uint64_t bytes = 0;
     mfh_alloc_class cls = MFH_CLASS_SCRATCH;
     void *dev = nullptr;
-    size_t capacity = 0;
+    size_t capacity = 0;  // device bytes of `dev` (the pool block)
     // U8 streams: whether any byte equals 0x80 (the reserved INT8 code),
     // scanned once at upload (backend-cpu/src/packed.rs:205 scans per call).
     bool has_int8_reserved = false;
@@ -101,13 +114,14 @@ struct mfh_buf {
     // buffer by an operation drops it.
     void *f16_shadow = nullptr;
     size_t f16_capacity = 0;
-    // Backend-private repacked copy of a U8 code stream, built on the first
-    // packed operation that fixes its format.
+    // Backend-private repacked copy of a U8 code stream for one format, built
+    // by prepare_packed (mfh_prepare_packed, or the first packed operation
+    // that fixes the format).
     void *repacked = nullptr;
     size_t repacked_capacity = 0;
     int repacked_format = -1;
     // F32 scale streams: the scales in tile order for one format's padding,
-    // built on first matrix-core use; dropped when the buffer is written.
+    // built with the repacked codes; dropped when the buffer is written.
     void *tiled_scales = nullptr;
     size_t tiled_capacity = 0;
     int tiled_format = -1;
@@ -178,10 +192,31 @@ inline bool aliases(const mfh_buf *out, std::initializer_list<const mfh_buf *> i
     return false;
 }
 
+// Device memory for the context: an idle pool block, else a new one when the
+// context's footprint (every pooled block plus pending readback staging)
+// stays within max_total_bytes, after returning idle blocks to the driver
+// if that makes room.  On failure records the reason and returns
+// MFH_RESOURCE_LIMIT; nothing is allocated.
+mfh_status acquire(mfh_ctx *ctx, size_t bytes, void **out, size_t *capacity);
+// The same for a derived copy of `owner`, charged to the owner's class.
+mfh_status acquire_for(mfh_ctx *ctx, mfh_buf *owner, size_t bytes, void **out, size_t *capacity);
+// Return a block (null is ignored); `owner` non-null uncharges its class.
+void release_block(mfh_ctx *ctx, mfh_buf *owner, void *ptr, size_t capacity);
+
 // Device scratch owned by the context, grown on demand (stream ordered).
+// Null when the allocation is refused; acquire() recorded why, and
+// allocation_failed() is the status to return.
 void *ids_scratch(mfh_ctx *ctx, size_t bytes);
 void *work_scratch(mfh_ctx *ctx, size_t bytes);
 void *digits_scratch(mfh_ctx *ctx, size_t bytes);
+inline mfh_status allocation_failed(mfh_ctx *) { return MFH_RESOURCE_LIMIT; }
+
+
+// Build (once, stream ordered) the tile-order copies the matrix-core
+// kernels read for the format the two streams' widths select: repacked
+// codes on `codes`, tiled scales on `scales`.  Admits the pair like every
+// packed operation.
+mfh_status prepare_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales);
 
 // Fill `count` floats with `value` on the context stream (a kernel, so the
 // call is capturable; no hipMemsetAsync).

@@ -68,6 +68,15 @@ struct PackedCall {
     uint32_t seg_n[kMaxSegments] = {};
 };
 
+// packed_linear's admission (backend-cpu/src/packed.rs:96-140 order and
+// messages): fills `call` for the plain product; enqueues nothing.
+mfh_status admit_packed_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                               const mfh_buf *codes, const mfh_buf *scales, PackedCall *call);
+// Whether the pair already holds its tile copies for `format`; fills the
+// stream's tile fields when it does.
+bool prepared_stream(const mfh_buf *codes, const mfh_buf *scales, Format format,
+                     PackedStream *stream);
+
 // A matrix-core GEMV (m <= 2) whose activation prologue
 // applies `xform`, over admitted weights of n rows and width k (the LFM2
 // decode step).  Fails with MFH_UNSUPPORTED where that kernel does not serve

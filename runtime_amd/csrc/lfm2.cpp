@@ -77,6 +77,7 @@ using namespace mfh;
 
 struct mfl_model {
     mfh_ctx *ctx = nullptr;
+    uint64_t id = 0;  // distinguishes models for prefix ownership checks
     mfl_config config{};
     std::vector<uint8_t> kinds;
     uint64_t kv_width = 0;
@@ -87,6 +88,24 @@ struct mfl_model {
     std::map<uint64_t, std::unique_ptr<Workspace>> workspaces;
     Owned logits, sampled;
     Owned rotation;  // [max_tokens, head_dim] rotation coefficients by position
+};
+
+// An immutable copy of a model's prefix state (Lfm2Prefix,
+// executor-core/src/lfm2/executor.rs:249-281): per layer the convolution
+// history, or the live key/value cache rows; the logits and sampled id of
+// the last pass; the lengths.  Its buffers are Cache class, like the
+// reference's fork storage (executor/storage.rs:104-155).
+struct mfl_prefix {
+    mfh_ctx *ctx = nullptr;
+    uint64_t model_id = 0;
+    uint64_t length = 0;
+    struct Layer {
+        Owned history;      // conv: [conv_width - 1, hidden]
+        Owned key, value;   // attention: [length, kv_width] (none when empty)
+        uint64_t length = 0;
+    };
+    std::vector<Layer> layers;
+    Owned logits, sampled;
 };
 
 namespace mfh {
@@ -201,10 +220,12 @@ const float *dev(const Weight &w)
 // Whether the one-token step can run fused: every matmul role packed (the
 // K/V and FFN gate/up pairs in one format each), every norm and kernel
 // attached, and the matrix-core GEMV in use (kernel path 0 or 2; with 2 the
-// transforms run in the separate prologue kernels).
+// transforms run in the separate prologue kernels; path 3 keeps the
+// automatic kernels but runs the step op by op).
 bool fused_decode_ready(const mfl_model *m)
 {
-    if (m->ctx->kernel_path == 1 || !m->embedding.packed() || !m->embedding_norm.tensor)
+    if (m->ctx->kernel_path == 1 || m->ctx->kernel_path == 3 || !m->embedding.packed() ||
+        !m->embedding_norm.tensor)
         return false;
     for (uint32_t i = 0; i < m->config.layer_count; ++i) {
         const LayerWeights &lw = m->layers[i];
@@ -327,7 +348,7 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
             if (da.splits) {
                 da.partial = static_cast<float *>(work_scratch(c, gqa_decode_scratch_bytes(da)));
                 if (!da.partial)
-                    return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+                    return allocation_failed(c);
                 launch_gqa_decode(c->stream, da);
             } else {
                 Positions positions;
@@ -348,7 +369,7 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
                 if (const size_t bytes = gqa_scratch_bytes(g)) {
                     partials = static_cast<float *>(work_scratch(c, bytes));
                     if (!partials)
-                        return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+                        return allocation_failed(c);
                 }
                 launch_gqa(c->stream, dev(ws->attention), dev(ws->q_rope), nullptr, nullptr,
                            dev(st.key), dev(st.value), g, partials);
@@ -558,8 +579,10 @@ mfh_status mfl_create(mfh_ctx *ctx, const mfl_config *config, mfl_model **out)
     for (uint32_t i = 0; i < c.layer_count; ++i)
         if (c.layer_kinds[i] > 1)
             return fail(ctx, MFH_INVALID_ARGUMENT, "unknown LFM2 layer kind");
+    static uint64_t next_id = 0;
     auto m = std::make_unique<mfl_model>();
     m->ctx = ctx;
+    m->id = ++next_id;
     m->config = c;
     m->kinds.assign(c.layer_kinds, c.layer_kinds + c.layer_count);
     m->config.layer_kinds = m->kinds.data();
@@ -611,6 +634,10 @@ mfh_status mfl_set_weight(mfl_model *m, uint32_t role, uint32_t layer, const mfh
     if (!s && scales)
         s = check_f32(c, scales);
     if (s)
+        return s;
+    // Packed matmul roles get their private tile copies now, so a resource
+    // limit fails the attach rather than a later token pass.
+    if (scales && (s = prepare_packed(c, tensor, scales)))
         return s;
     Weight w{tensor, scales};
     if (role == MFL_TOKEN_EMBEDDING) {
@@ -702,7 +729,7 @@ mfh_status mfl_generate(mfl_model *m, uint32_t steps, mfh_buf *ids_out)
             if (const size_t bytes = argmax_scratch_bytes(1, vocab)) {
                 partials = work_scratch(c, bytes);
                 if (!partials)
-                    return fail(c, MFH_RESOURCE_LIMIT, "device allocation failed");
+                    return allocation_failed(c);
             }
             launch_argmax(c->stream, static_cast<float *>(m->sampled.buf->dev),
                           static_cast<const float *>(m->logits.buf->dev), 1, vocab, nullptr,
@@ -722,6 +749,117 @@ const mfh_buf *mfl_logits(const mfl_model *m)
 const mfh_buf *mfl_sampled(const mfl_model *m)
 {
     return m ? m->sampled.buf : nullptr;
+}
+
+namespace {
+
+void copy_rows(mfh_ctx *c, mfh_buf *dst, const mfh_buf *src, uint64_t elements)
+{
+    launch_copy(c->stream, static_cast<float *>(dst->dev), static_cast<const float *>(src->dev),
+                elements);
+}
+
+}  // namespace
+
+mfh_status mfl_snapshot(mfl_model *m, mfl_prefix **out)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    mfh_ctx *c = m->ctx;
+    if (!out)
+        return fail(c, MFH_INVALID_ARGUMENT, "prefix output pointer is null");
+    *out = nullptr;
+    auto p = std::make_unique<mfl_prefix>();
+    p->ctx = c;
+    p->model_id = m->id;
+    p->length = m->length;
+    p->layers = std::vector<mfl_prefix::Layer>(m->config.layer_count);
+    const uint64_t h = m->config.hidden;
+    // Allocate everything first, so a ResourceLimit records no copy.
+    mfh_status s = MFH_OK;
+    for (uint32_t i = 0; i < m->config.layer_count && !s; ++i) {
+        mfl_prefix::Layer &pl = p->layers[i];
+        const LayerState &st = m->state[i];
+        pl.length = st.length;
+        if (m->kinds[i] == 0) {
+            s = alloc(c, pl.history, m->config.conv_width - 1, h, MFH_CLASS_CACHE, false);
+        } else if (st.length) {
+            s = alloc(c, pl.key, st.length, m->kv_width, MFH_CLASS_CACHE, false);
+            if (!s)
+                s = alloc(c, pl.value, st.length, m->kv_width, MFH_CLASS_CACHE, false);
+        }
+    }
+    if (!s)
+        s = alloc(c, p->logits, 1, m->config.vocab, MFH_CLASS_CACHE, false);
+    if (!s) {
+        const uint64_t dims[1] = {1};
+        s = mfh_alloc_f32(c, dims, 1, MFH_CLASS_CACHE, 0, &p->sampled.buf);
+    }
+    if (s)
+        return s;
+    DeviceGuard guard(c->device);
+    for (uint32_t i = 0; i < m->config.layer_count; ++i) {
+        mfl_prefix::Layer &pl = p->layers[i];
+        const LayerState &st = m->state[i];
+        if (m->kinds[i] == 0) {
+            copy_rows(c, pl.history.buf, st.history[st.current].buf, pl.history.buf->elements);
+        } else if (st.length) {
+            copy_rows(c, pl.key.buf, st.key.buf, st.length * m->kv_width);
+            copy_rows(c, pl.value.buf, st.value.buf, st.length * m->kv_width);
+        }
+    }
+    copy_rows(c, p->logits.buf, m->logits.buf, m->config.vocab);
+    copy_rows(c, p->sampled.buf, m->sampled.buf, 1);
+    if (hipGetLastError() != hipSuccess)
+        return fail(c, MFH_BACKEND_FAILURE, "prefix copy launch failed");
+    *out = p.release();
+    return MFH_OK;
+}
+
+mfh_status mfl_restore(mfl_model *m, const mfl_prefix *p)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    mfh_ctx *c = m->ctx;
+    if (!p || p->ctx != c || p->model_id != m->id)
+        return fail(c, MFH_INVALID_ARGUMENT, "prefix belongs to another model");
+    mfh_status s = check_f32(c, p->logits.buf);
+    for (uint32_t i = 0; i < m->config.layer_count && !s; ++i)
+        if (m->kinds[i] == 0)
+            s = check_f32(c, p->layers[i].history.buf);
+        else if (p->layers[i].length && !(s = check_f32(c, p->layers[i].key.buf)))
+            s = check_f32(c, p->layers[i].value.buf);
+    if (s)
+        return s;
+    DeviceGuard guard(c->device);
+    for (uint32_t i = 0; i < m->config.layer_count; ++i) {
+        const mfl_prefix::Layer &pl = p->layers[i];
+        LayerState &st = m->state[i];
+        st.length = pl.length;
+        if (m->kinds[i] == 0) {
+            st.current = 0;
+            copy_rows(c, st.history[0].buf, pl.history.buf, pl.history.buf->elements);
+        } else if (pl.length) {
+            copy_rows(c, st.key.buf, pl.key.buf, pl.length * m->kv_width);
+            copy_rows(c, st.value.buf, pl.value.buf, pl.length * m->kv_width);
+        }
+    }
+    copy_rows(c, m->logits.buf, p->logits.buf, m->config.vocab);
+    copy_rows(c, m->sampled.buf, p->sampled.buf, 1);
+    m->length = p->length;
+    if (hipGetLastError() != hipSuccess)
+        return fail(c, MFH_BACKEND_FAILURE, "prefix copy launch failed");
+    return MFH_OK;
+}
+
+uint64_t mfl_prefix_length(const mfl_prefix *p)
+{
+    return p ? p->length : 0;
+}
+
+void mfl_prefix_destroy(mfl_prefix *p)
+{
+    delete p;
 }
 
 }  // extern "C"

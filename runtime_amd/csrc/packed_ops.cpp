@@ -64,7 +64,9 @@ PackedStream stream_of(const mfh_buf *codes, const mfh_buf *scales)
 
 // Build (once) the tile-order copies the matrix-core kernels read: the
 // repacked codes live on the code buffer, the tiled scales on the scale
-// buffer.  Both are stream-ordered kernels; nothing synchronizes.
+// buffer, each charged to its buffer's allocation class and bounded by the
+// context's limits.  Both are stream-ordered kernels; nothing synchronizes.
+// Nothing is replaced unless both new copies could be allocated.
 mfh_status prepare_tiles(mfh_ctx *ctx, const mfh_buf *codes_c, const mfh_buf *scales_c,
                          const Packed &p, PackedStream *stream)
 {
@@ -73,33 +75,47 @@ mfh_status prepare_tiles(mfh_ctx *ctx, const mfh_buf *codes_c, const mfh_buf *sc
     mfh_buf *codes = const_cast<mfh_buf *>(codes_c);
     mfh_buf *scales = const_cast<mfh_buf *>(scales_c);
     const int fmt = int(p.format);
-    if (!codes->repacked || codes->repacked_format != fmt) {
-        if (codes->repacked)
-            ctx->pool->release(codes->repacked, codes->repacked_capacity);
-        codes->repacked = ctx->pool->acquire(repacked_bytes(p.format, p.rows, p.inner),
-                                             &codes->repacked_capacity);
-        codes->repacked_format = codes->repacked ? fmt : -1;
-        if (!codes->repacked)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+    const bool half = scales->f16_shadow != nullptr;
+    const bool need_codes = !codes->repacked || codes->repacked_format != fmt;
+    const bool need_scales =
+        !scales->tiled_scales || scales->tiled_format != fmt || scales->tiled_half != half;
+    void *tiles = nullptr, *tiled = nullptr;
+    size_t tiles_cap = 0, tiled_cap = 0;
+    mfh_status s = MFH_OK;
+    if (need_codes)
+        s = acquire_for(ctx, codes, repacked_bytes(p.format, p.rows, p.inner), &tiles, &tiles_cap);
+    if (!s && need_scales) {
+        s = acquire_for(ctx, scales, tiled_scales_bytes(p.format, p.rows, p.inner, half), &tiled,
+                        &tiled_cap);
+        if (s)
+            release_block(ctx, codes, tiles, tiles_cap);
+    }
+    if (s)
+        return s;
+    if (need_codes) {
+        release_block(ctx, codes, codes->repacked, codes->repacked_capacity);
+        codes->repacked = tiles;
+        codes->repacked_capacity = tiles_cap;
+        codes->repacked_format = fmt;
         launch_repack(ctx->stream, p.format, static_cast<const uint8_t *>(codes->dev),
                       static_cast<uint8_t *>(codes->repacked), p.rows, p.inner);
     }
-    const bool half = scales->f16_shadow != nullptr;
-    if (!scales->tiled_scales || scales->tiled_format != fmt || scales->tiled_half != half) {
-        if (scales->tiled_scales)
-            ctx->pool->release(scales->tiled_scales, scales->tiled_capacity);
-        scales->tiled_scales = ctx->pool->acquire(
-            tiled_scales_bytes(p.format, p.rows, p.inner, half), &scales->tiled_capacity);
-        scales->tiled_format = scales->tiled_scales ? fmt : -1;
+    if (need_scales) {
+        release_block(ctx, scales, scales->tiled_scales, scales->tiled_capacity);
+        scales->tiled_scales = tiled;
+        scales->tiled_capacity = tiled_cap;
+        scales->tiled_format = fmt;
         scales->tiled_half = half;
-        if (!scales->tiled_scales)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
         launch_tile_scales(ctx->stream, p.format, static_cast<const float *>(scales->dev),
                            scales->tiled_scales, p.rows, p.inner, half);
     }
-    stream->tiles = static_cast<const uint8_t *>(codes->repacked);
-    stream->tiled_scales = scales->tiled_scales;
-    stream->tiled_half = half;
+    if ((need_codes || need_scales) && hipGetLastError() != hipSuccess)
+        return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
+    if (stream) {
+        stream->tiles = static_cast<const uint8_t *>(codes->repacked);
+        stream->tiled_scales = scales->tiled_scales;
+        stream->tiled_half = half;
+    }
     return MFH_OK;
 }
 
@@ -134,7 +150,7 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
             return s;
         void *scratch = digits_scratch(ctx, gemv_mfma_scratch_bytes(call));
         if (!scratch)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+            return allocation_failed(ctx);
         call.separate_prologue = ctx->kernel_path == 2;
         launch_gemv_mfma(stream, call, scratch);
     } else if (call.m <= 8) {
@@ -149,7 +165,7 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
             return s;
         void *scratch = digits_scratch(ctx, gemm_mfma_scratch_bytes(call));
         if (!scratch)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+            return allocation_failed(ctx);
         launch_gemm_mfma(stream, call, scratch);
     } else {
         launch_gemm_fma(stream, call);
@@ -258,7 +274,7 @@ mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, u
     call.a.tiled_half = call.seg[0].tiled_half;
     void *scratch = digits_scratch(ctx, gemv_mfma_scratch_bytes(call));
     if (!scratch)
-        return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        return allocation_failed(ctx);
     call.separate_prologue = ctx->kernel_path == 2;
     launch_gemv_mfma(ctx->stream, call, scratch);
     if (hipGetLastError() != hipSuccess)
@@ -266,11 +282,91 @@ mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, u
     return MFH_OK;
 }
 
+mfh_status admit_packed_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                               const mfh_buf *codes, const mfh_buf *scales, PackedCall *call)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    mfh_status s = check_operation(ctx, MFH_OP_PACKED_LINEAR);
+    if (!s)
+        s = check_f32(ctx, input);
+    if (s)
+        return s;
+    Packed p;
+    if ((s = check_packed(ctx, codes, scales, &p)))
+        return s;
+    if (input->rank != 2)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input must be rank two");
+    if (input->dims[1] != p.inner)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
+    uint64_t dims[2] = {input->dims[0], p.rows};
+    if ((s = check_output(ctx, output, dims, 2)))
+        return s;
+    if (aliases(output, {input, codes, scales}))
+        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
+    if (input->dims[0] > UINT32_MAX)
+        return fail(ctx, MFH_OVERFLOW, "packed linear row count exceeds the kernel index range");
+    call->format = p.format;
+    call->epilogue = Epilogue::Single;
+    call->m = uint32_t(input->dims[0]);
+    call->n = p.rows;
+    call->k = p.inner;
+    call->x = static_cast<const float *>(input->dev);
+    call->a = stream_of(codes, scales);
+    call->out_a = static_cast<float *>(output->dev);
+    return MFH_OK;
+}
+
+bool prepared_stream(const mfh_buf *codes, const mfh_buf *scales, Format format,
+                     PackedStream *stream)
+{
+    const bool half = scales->f16_shadow != nullptr;
+    if (!codes->repacked || codes->repacked_format != int(format) || !scales->tiled_scales ||
+        scales->tiled_format != int(format) || scales->tiled_half != half)
+        return false;
+    stream->tiles = static_cast<const uint8_t *>(codes->repacked);
+    stream->tiled_scales = scales->tiled_scales;
+    stream->tiled_half = half;
+    return true;
+}
+
+mfh_status prepare_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales)
+{
+    Packed p;
+    mfh_status s = check_packed(ctx, codes, scales, &p);
+    if (s)
+        return s;
+    if (p.rows == 0 || p.inner == 0)
+        return MFH_OK;
+    DeviceGuard guard(ctx->device);
+    return prepare_tiles(ctx, codes, scales, p, nullptr);
+}
+
 }  // namespace mfh
 
 using namespace mfh;
 
 extern "C" {
+
+mfh_status mfh_prepare_packed(mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales)
+{
+    if (!ctx)
+        return MFH_INVALID_ARGUMENT;
+    if (ctx->cancel_requested)
+        return fail(ctx, MFH_CANCELLED, "operation cancelled");
+    return prepare_packed(ctx, codes, scales);
+}
+
+int mfh_packed_prepared(const mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf *scales)
+{
+    if (!ctx || !codes || !scales || codes->ctx != ctx || scales->ctx != ctx)
+        return 0;
+    Packed p;
+    if (check_packed(const_cast<mfh_ctx *>(ctx), codes, scales, &p))
+        return 0;
+    PackedStream unused;
+    return prepared_stream(codes, scales, p.format, &unused) ? 1 : 0;
+}
 
 mfh_status mfh_packed_gather_rows(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *codes,
                                   const mfh_buf *scales, const uint32_t *host_ids,
@@ -324,7 +420,7 @@ mfh_status mfh_packed_gather_rows(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *
             staged[i] = float(host_ids[i]);
         void *dst = ids_scratch(ctx, host_count * sizeof(float));
         if (!dst)
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+            return allocation_failed(ctx);
         if (hipMemcpyAsync(dst, staged.data(), host_count * sizeof(float), hipMemcpyHostToDevice,
                            ctx->stream) != hipSuccess) {
             (void)hipGetLastError();
@@ -344,38 +440,12 @@ mfh_status mfh_packed_gather_rows(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *
 mfh_status mfh_packed_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
                              const mfh_buf *codes, const mfh_buf *scales)
 {
-    if (!ctx)
-        return MFH_INVALID_ARGUMENT;
-    mfh_status s = check_operation(ctx, MFH_OP_PACKED_LINEAR);
-    if (!s)
-        s = check_f32(ctx, input);
+    PackedCall call;
+    mfh_status s = admit_packed_linear(ctx, output, input, codes, scales, &call);
     if (s)
         return s;
-    Packed p;
-    if ((s = check_packed(ctx, codes, scales, &p)))
-        return s;
-    if (input->rank != 2)
-        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input must be rank two");
-    if (input->dims[1] != p.inner)
-        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
-    uint64_t dims[2] = {input->dims[0], p.rows};
-    if ((s = check_output(ctx, output, dims, 2)))
-        return s;
-    if (aliases(output, {input, codes, scales}))
-        return fail(ctx, MFH_INVALID_ARGUMENT, "output aliases an input");
-    if (input->dims[0] > UINT32_MAX)
-        return fail(ctx, MFH_OVERFLOW, "packed linear row count exceeds the kernel index range");
     DeviceGuard guard(ctx->device);
     mark_written(output);
-    PackedCall call;
-    call.format = p.format;
-    call.epilogue = Epilogue::Single;
-    call.m = uint32_t(input->dims[0]);
-    call.n = p.rows;
-    call.k = p.inner;
-    call.x = static_cast<const float *>(input->dev);
-    call.a = stream_of(codes, scales);
-    call.out_a = static_cast<float *>(output->dev);
     return run_packed(ctx, call, codes, scales);
 }
 
@@ -480,7 +550,7 @@ mfh_status mfh_packed_swiglu_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf
     // (backend-cpu/src/packed.rs:425-455).
     float *activated = static_cast<float *>(work_scratch(ctx, count * sizeof(float)));
     if (count && !activated)
-        return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+        return allocation_failed(ctx);
     launch_swiglu(ctx->stream, activated, static_cast<const float *>(gate->dev),
                   static_cast<const float *>(up->dev), count);
     call.x = activated;

@@ -35,37 +35,29 @@ Pool::~Pool()
     (void)hipSetDevice(previous);
 }
 
-void *Pool::acquire(size_t bytes, size_t *capacity)
+void *Pool::take(size_t bytes, size_t *capacity)
 {
-    size_t want = pool_bucket(bytes);
+    const size_t want = pool_bucket(bytes);
     auto it = free_.lower_bound(want);
     // Reuse a block up to 25% larger than needed.
-    if (it != free_.end() && it->first <= want + want / 4) {
-        void *p = it->second;
-        *capacity = it->first;
-        free_.erase(it);
-        return p;
-    }
+    if (it == free_.end() || it->first > want + want / 4)
+        return nullptr;
+    void *p = it->second;
+    *capacity = it->first;
+    idle_ -= it->first;
+    free_.erase(it);
+    return p;
+}
+
+void *Pool::grow(size_t bytes, size_t *capacity)
+{
+    const size_t want = pool_bucket(bytes);
     void *p = nullptr;
     if (hipMalloc(&p, want) != hipSuccess) {
-        // Return cached blocks to the driver and retry once.
-        for (auto &entry : free_) {
-            (void)hipFree(entry.second);
-            for (auto a = all_.begin(); a != all_.end(); ++a)
-                if (*a == entry.second) {
-                    all_.erase(a);
-                    break;
-                }
-            reserved_ -= entry.first;
-        }
-        free_.clear();
         (void)hipGetLastError();
-        if (hipMalloc(&p, want) != hipSuccess) {
-            (void)hipGetLastError();
-            return nullptr;
-        }
+        return nullptr;
     }
-    all_.push_back(p);
+    all_.insert(p);
     reserved_ += want;
     *capacity = want;
     return p;
@@ -73,8 +65,88 @@ void *Pool::acquire(size_t bytes, size_t *capacity)
 
 void Pool::release(void *ptr, size_t capacity)
 {
-    if (ptr)
-        free_.emplace(capacity, ptr);
+    if (!ptr)
+        return;
+    free_.emplace(capacity, ptr);
+    idle_ += capacity;
+}
+
+void Pool::evict_idle()
+{
+    for (auto &entry : free_) {
+        (void)hipFree(entry.second);
+        all_.erase(entry.second);
+        reserved_ -= entry.first;
+    }
+    free_.clear();
+    idle_ = 0;
+}
+
+namespace {
+
+void note_peak(mfh_ctx *ctx)
+{
+    const uint64_t total = ctx->pool->reserved() + ctx->pending_result_bytes;
+    if (total > ctx->peak_bytes)
+        ctx->peak_bytes = total;
+}
+
+// Return the idle blocks to the driver once the stream has drained (a block
+// the host released may still be read by queued work).
+void evict(mfh_ctx *ctx)
+{
+    if (!ctx->pool->idle())
+        return;
+    (void)hipStreamSynchronize(ctx->stream);
+    (void)hipGetLastError();
+    ctx->pool->evict_idle();
+}
+
+}  // namespace
+
+mfh_status acquire(mfh_ctx *ctx, size_t bytes, void **out, size_t *capacity)
+{
+    *out = ctx->pool->take(bytes, capacity);
+    if (*out)
+        return MFH_OK;
+    // resources.rs:27-43 on the physical footprint: every pooled block, idle
+    // ones included, plus pending readback staging.
+    const uint64_t want = pool_bucket(bytes);
+    const uint64_t limit = ctx->limits.max_total_bytes;
+    auto fits = [&] {
+        const uint64_t owned = ctx->pool->reserved() + ctx->pending_result_bytes;
+        return owned + want >= owned && owned + want <= limit;
+    };
+    if (!fits())
+        evict(ctx);
+    if (!fits())
+        return fail(ctx, MFH_RESOURCE_LIMIT, "allocation exceeds configured total resource limit");
+    *out = ctx->pool->grow(bytes, capacity);
+    if (!*out) {
+        evict(ctx);
+        *out = ctx->pool->grow(bytes, capacity);
+    }
+    if (!*out)
+        return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+    note_peak(ctx);
+    return MFH_OK;
+}
+
+mfh_status acquire_for(mfh_ctx *ctx, mfh_buf *owner, size_t bytes, void **out, size_t *capacity)
+{
+    mfh_status s = acquire(ctx, bytes, out, capacity);
+    if (!s)
+        ctx->held_by_class[owner->cls] += *capacity;
+    return s;
+}
+
+void release_block(mfh_ctx *ctx, mfh_buf *owner, void *ptr, size_t capacity)
+{
+    if (!ptr)
+        return;
+    if (owner)
+        ctx->held_by_class[owner->cls] -= capacity;
+    ctx->pool->release(ptr, capacity);
 }
 
 mfh_status fail(mfh_ctx *ctx, mfh_status status, const char *message)
@@ -140,29 +212,33 @@ mfh_status check_operation(mfh_ctx *ctx, mfh_operation op)
 
 void mark_written(mfh_buf *buf)
 {
+    mfh_ctx *ctx = buf->ctx;
     if (buf->f16_shadow) {
-        buf->ctx->pool->release(buf->f16_shadow, buf->f16_capacity);
+        release_block(ctx, buf, buf->f16_shadow, buf->f16_capacity);
         buf->f16_shadow = nullptr;
         buf->f16_capacity = 0;
     }
     if (buf->tiled_scales) {
-        buf->ctx->pool->release(buf->tiled_scales, buf->tiled_capacity);
+        release_block(ctx, buf, buf->tiled_scales, buf->tiled_capacity);
         buf->tiled_scales = nullptr;
         buf->tiled_capacity = 0;
         buf->tiled_format = -1;
     }
 }
 
-// Scratch blocks only grow, and a grown block is never returned to the pool
-// while the context lives: work captured into a graph may still address it.
+// Scratch blocks only grow; a replaced block returns to the pool, where
+// stream order keeps it from being reused before the work queued on it ran.
 static void *grow(mfh_ctx *ctx, void **slot, size_t *capacity, size_t bytes)
 {
     if (bytes > *capacity) {
         size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
-        void *p = ctx->pool->acquire(want, capacity);
-        if (!p)
+        void *p = nullptr;
+        size_t got = 0;
+        if (acquire(ctx, want, &p, &got))
             return nullptr;
+        release_block(ctx, nullptr, *slot, *capacity);
         *slot = p;
+        *capacity = got;
     }
     return *slot;
 }
@@ -224,11 +300,6 @@ mfh_status admit_shape(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, size_t
         return fail(ctx, MFH_RESOURCE_LIMIT, "element count exceeds backend capability");
     if (b > ctx->limits.max_allocation_bytes)
         return fail(ctx, MFH_RESOURCE_LIMIT, "allocation exceeds configured per-buffer limit");
-    uint64_t owned = ctx->live_bytes + ctx->pending_result_bytes;
-    if (owned + b < owned)
-        return fail(ctx, MFH_OVERFLOW, "resource total overflows u64");
-    if (owned + b > ctx->limits.max_total_bytes)
-        return fail(ctx, MFH_RESOURCE_LIMIT, "allocation exceeds configured total resource limit");
     *elements = count;
     *bytes = b;
     return MFH_OK;
@@ -261,18 +332,13 @@ mfh_status make_buffer(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, mfh_dt
     buf->bytes = bytes;
     buf->cls = cls;
     if (bytes > 0) {
-        buf->dev = ctx->pool->acquire(bytes, &buf->capacity);
-        if (!buf->dev) {
+        if (acquire(ctx, bytes, &buf->dev, &buf->capacity)) {
             delete buf;
-            return fail(ctx, MFH_RESOURCE_LIMIT, "device allocation failed");
+            return MFH_RESOURCE_LIMIT;
         }
     }
     ctx->live_buffers.insert(buf);
-    ctx->live_bytes += bytes;
-    ctx->live_by_class[cls] += bytes;
-    uint64_t total = ctx->live_bytes + ctx->pending_result_bytes;
-    if (total > ctx->peak_bytes)
-        ctx->peak_bytes = total;
+    ctx->held_by_class[cls] += buf->capacity;
     *out = buf;
     return MFH_OK;
 }
@@ -412,10 +478,16 @@ mfh_status mfh_resource_report(const mfh_ctx *ctx, mfh_report *out)
 {
     if (!ctx || !out)
         return MFH_INVALID_ARGUMENT;
-    out->resident_weight_bytes = ctx->live_by_class[MFH_CLASS_WEIGHT];
-    out->cache_bytes = ctx->live_by_class[MFH_CLASS_CACHE];
-    out->scratch_bytes = ctx->live_by_class[MFH_CLASS_SCRATCH];
-    out->staged_branch_bytes = ctx->live_by_class[MFH_CLASS_BRANCH];
+    // Every pooled device byte is reported once: live buffers and their
+    // derived copies under the buffer's class, everything else the pool
+    // holds (context scratch, idle blocks) as scratch.  The total is the
+    // context's device footprint plus pending readback staging.
+    const uint64_t *held = ctx->held_by_class;
+    const uint64_t attributed = held[0] + held[1] + held[2] + held[3];
+    out->resident_weight_bytes = held[MFH_CLASS_WEIGHT];
+    out->cache_bytes = held[MFH_CLASS_CACHE];
+    out->scratch_bytes = held[MFH_CLASS_SCRATCH] + (ctx->pool->reserved() - attributed);
+    out->staged_branch_bytes = held[MFH_CLASS_BRANCH];
     out->pending_operation_bytes = ctx->pending_result_bytes;
     out->pending_operations = ctx->pending_operations;
     return MFH_OK;
@@ -510,12 +582,15 @@ mfh_status mfh_upload_f32(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, con
         for (size_t i = 0; i < count && exact; ++i)
             exact = f16_exact(values[i], &half[i]);
         if (exact) {
-            buf->f16_shadow = ctx->pool->acquire(count * 2, &buf->f16_capacity);
+            // The shadow is optional: where the limit leaves no room for it
+            // the kernels read the f32 scales.
+            if (acquire_for(ctx, buf, count * 2, &buf->f16_shadow, &buf->f16_capacity))
+                buf->f16_shadow = nullptr;
             if (buf->f16_shadow &&
                 hipMemcpyAsync(buf->f16_shadow, half.data(), count * 2, hipMemcpyHostToDevice,
                                ctx->stream) != hipSuccess) {
                 (void)hipGetLastError();
-                ctx->pool->release(buf->f16_shadow, buf->f16_capacity);
+                release_block(ctx, buf, buf->f16_shadow, buf->f16_capacity);
                 buf->f16_shadow = nullptr;
             }
         }
@@ -566,12 +641,10 @@ void mfh_release(mfh_buf *buf)
         return;
     mfh_ctx *ctx = buf->ctx;
     if (ctx) {
-        ctx->pool->release(buf->dev, buf->capacity);
-        ctx->pool->release(buf->f16_shadow, buf->f16_capacity);
-        ctx->pool->release(buf->repacked, buf->repacked_capacity);
-        ctx->pool->release(buf->tiled_scales, buf->tiled_capacity);
-        ctx->live_bytes -= buf->bytes;
-        ctx->live_by_class[buf->cls] -= buf->bytes;
+        release_block(ctx, buf, buf->dev, buf->capacity);
+        release_block(ctx, buf, buf->f16_shadow, buf->f16_capacity);
+        release_block(ctx, buf, buf->repacked, buf->repacked_capacity);
+        release_block(ctx, buf, buf->tiled_scales, buf->tiled_capacity);
         ctx->live_buffers.erase(buf);
     }
     delete buf;
@@ -678,6 +751,11 @@ mfh_status mfh_read_f32_async(mfh_ctx *ctx, const mfh_buf *buf, mfh_readback **o
     if (s)
         return s;
     DeviceGuard guard(ctx->device);
+    // The staging the completion owns until it is polled counts against the
+    // total limit like device blocks do.
+    const uint64_t owned = ctx->pool->reserved() + ctx->pending_result_bytes;
+    if (owned + buf->bytes > ctx->limits.max_total_bytes)
+        return fail(ctx, MFH_RESOURCE_LIMIT, "allocation exceeds configured total resource limit");
     auto *rb = new (std::nothrow) mfh_readback();
     if (!rb)
         return fail(ctx, MFH_RESOURCE_LIMIT, "host allocation failed");
@@ -708,6 +786,7 @@ mfh_status mfh_read_f32_async(mfh_ctx *ctx, const mfh_buf *buf, mfh_readback **o
         return fail(ctx, MFH_BACKEND_FAILURE, "readback submission failed");
     }
     ctx->pending_result_bytes += buf->bytes;
+    note_peak(ctx);
     ctx->live_readbacks.insert(rb);
     *out = rb;
     return MFH_OK;

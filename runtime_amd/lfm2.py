@@ -168,6 +168,16 @@ class Lfm2Model:
     def sample(self) -> None:
         self.backend._check(_ffi.lib().mfl_sample(self._model))
 
+    def snapshot(self) -> "Lfm2Prefix":
+        """An immutable copy of the current prefix state (mfl_snapshot)."""
+        out = ctypes.c_void_p()
+        self.backend._check(_ffi.lib().mfl_snapshot(self._model, ctypes.byref(out)))
+        return Lfm2Prefix(out.value, self)
+
+    def restore(self, prefix: "Lfm2Prefix") -> None:
+        """Continue from `prefix` (mfl_restore); the prefix stays unchanged."""
+        self.backend._check(_ffi.lib().mfl_restore(self._model, prefix.handle))
+
     def generate(self, steps: int, ids: Buffer | None = None) -> Buffer:
         """Greedy decode: returns the f32 device buffer of the `steps` ids."""
         ids = ids if ids is not None else self.backend.allocate_f32((steps,))
@@ -175,41 +185,87 @@ class Lfm2Model:
         return ids
 
 
-def synthetic_weights(model: Lfm2Model, seed: int = 0x5EED_1F00, norms: str = "ones",
-                      keep_host: bool = False):
-    """Attach a random-init model: every matrix N(0, 0.02) from the counter
-    generator (seed + 4096 * role + layer), quantized to its role's format;
-    norm weights are ones (`norms="ones"`) or 1 + N(0, 0.1) (`"random"`).
-    Returns {(role, layer): host arrays} when `keep_host`."""
-    cfg, backend = model.cfg, model.backend
-    host = {}
+class Lfm2Prefix:
+    """A stored prefix of one model (include/minifield_lfm2.h mfl_prefix)."""
+
+    def __init__(self, handle: int, model: Lfm2Model):
+        self._handle = handle
+        self._model = model  # keeps the model (and its context) alive
+
+    @property
+    def handle(self) -> int:
+        return self._handle
+
+    @property
+    def length(self) -> int:
+        return int(_ffi.lib().mfl_prefix_length(self._handle))
+
+    def close(self) -> None:
+        if self._handle:
+            _ffi.lib().mfl_prefix_destroy(self._handle)
+            self._handle = 0
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def synthetic_host_weights(cfg: Lfm2Config, seed: int = 0x5EED_1F00, norms: str = "ones",
+                           roles=None):
+    """Yield (role, layer, host arrays) of a random-init model: every matrix
+    N(0, 0.02) from the counter generator (seed + 4096 * role + layer),
+    quantized to its role's format as (codes, f32 scales), dense roles as
+    (values,); norm weights are ones (`norms="ones"`) or 1 + N(0, 0.1)
+    (`"random"`).  `roles`, when given, limits the output to those
+    (role, layer) pairs."""
     for role, layer, shape, matmul in role_shapes(cfg):
+        if roles is not None and (role, layer) not in roles:
+            continue
         role_seed = seed + 4096 * role + layer
         if not matmul and role != CONV_KERNEL:
             if norms == "ones":
                 values = np.ones(shape, dtype=np.float32)
             else:
                 values = convert.normal(shape, role_seed, sigma=0.1, mean=1.0)
-            model.set_weight(role, layer, backend.upload_f32_classified(shape, values, WEIGHT))
-            if keep_host:
-                host[(role, layer)] = (values,)
+            yield role, layer, (values,)
             continue
         dense = convert.normal(shape, role_seed, sigma=0.02)
         fmt = cfg.formats.get(_role_group(role)) if matmul else None
         if fmt is None:
-            model.set_weight(role, layer, backend.upload_f32_classified(shape, dense, WEIGHT))
-            if keep_host:
-                host[(role, layer)] = (dense,)
+            yield role, layer, (dense,)
             continue
         codes, scales16 = convert.quantize(dense, fmt)
         del dense
-        scales = convert.f16_to_f32(scales16)
+        yield role, layer, (codes, convert.f16_to_f32(scales16))
+
+
+def attach(model: Lfm2Model, role: int, layer: int, arrays) -> None:
+    """Upload one role's host arrays (Weight class) and attach them."""
+    backend = model.backend
+    if len(arrays) == 2:
+        codes, scales = arrays
         model.set_weight(role, layer, backend.upload_u8_classified(codes.shape, codes, WEIGHT),
                          backend.upload_f32_classified(scales.shape, scales, WEIGHT))
+    else:
+        (values,) = arrays
+        model.set_weight(role, layer,
+                         backend.upload_f32_classified(values.shape, values, WEIGHT))
+
+
+def synthetic_weights(model: Lfm2Model, seed: int = 0x5EED_1F00, norms: str = "ones",
+                      keep_host: bool = False):
+    """Attach the random-init model of synthetic_host_weights.  Returns
+    {(role, layer): host arrays} when `keep_host`."""
+    host = {}
+    for role, layer, arrays in synthetic_host_weights(model.cfg, seed, norms):
+        attach(model, role, layer, arrays)
         if keep_host:
-            host[(role, layer)] = (codes, scales)
+            host[(role, layer)] = arrays
     return host
 
 
 __all__ = ["Lfm2Config", "Lfm2Model", "lfm2_350m", "lfm2_1_2b", "synthetic_weights",
+           "synthetic_host_weights", "attach",
            "role_shapes", "ExecutorError", "CONV", "ATTENTION"]

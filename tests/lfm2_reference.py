@@ -5,8 +5,17 @@ A restatement of the reference executor's `append_tokens` and
 composed of the oracle's per-operation restatements (oracle/), so that the
 HIP model pass can be compared with the reference's arithmetic on the same
 weights and tokens.
+
+Packed products run on the row-parallel oracle and attention on the
+score-cached one; both are pinned bit-identical to the single-threaded
+restatements (tests/test_oracle.py, tests/test_dense_oracle.py), which is
+what makes full LFM2 shapes affordable.  Pair and SwiGLU products are
+composed from single products and swiglu, which the oracle tests pin
+bitwise to the composite restatements (packed_pair_validation.rs:169-208).
 """
 from __future__ import annotations
+
+import os
 
 import numpy as np
 
@@ -16,11 +25,34 @@ from runtime_amd.lfm2 import (CONV, CONV_IN, CONV_KERNEL, CONV_OUT, EMBEDDING_NO
                               QUERY, QUERY_NORM, TOKEN_EMBEDDING, VALUE, Lfm2Config)
 
 
+THREADS = max(1, min(16, os.cpu_count() or 1))
+
+
+def _linear(x, codes, scales):
+    return oracle.packed_linear_threaded(x, codes, scales, threads=THREADS)
+
+
 class OracleLfm2:
     def __init__(self, cfg: Lfm2Config, weights: dict):
         self.cfg = cfg
         self.w = weights
         self.reset()
+
+    def snapshot(self) -> dict:
+        """A copy of the prefix state (lengths, histories, caches, logits)."""
+        return {"length": self.length, "history": {i: h.copy() for i, h in self.history.items()},
+                "key": {i: c.copy() for i, c in self.key.items()},
+                "value": {i: c.copy() for i, c in self.value.items()},
+                "cache_len": dict(self.cache_len),
+                "logits": None if self.logits is None else self.logits.copy()}
+
+    def restore(self, state: dict) -> None:
+        self.length = state["length"]
+        self.history = {i: h.copy() for i, h in state["history"].items()}
+        self.key = {i: c.copy() for i, c in state["key"].items()}
+        self.value = {i: c.copy() for i, c in state["value"].items()}
+        self.cache_len = dict(state["cache_len"])
+        self.logits = None if state["logits"] is None else state["logits"].copy()
 
     def reset(self):
         cfg = self.cfg
@@ -48,7 +80,7 @@ class OracleLfm2:
         """weight_linear (execution.rs:12-25)."""
         t = self._w(role, layer)
         if len(t) == 2:
-            return oracle.packed_linear(x, t[0], t[1])
+            return _linear(x, t[0], t[1])
         return oracle.linear(x, t[0])
 
     def _ffn(self, index, ffn_input):
@@ -56,18 +88,18 @@ class OracleLfm2:
         pair = self._same_format(FFN_W1, FFN_W3, index)
         if rows >= 96 and pair and self._packed(FFN_W2, index):
             g, u = self._w(FFN_W1, index), self._w(FFN_W3, index)
-            hidden = oracle.packed_swiglu_pair(ffn_input, g[0], g[1], u[0], u[1])
+            hidden = oracle.swiglu(_linear(ffn_input, g[0], g[1]), _linear(ffn_input, u[0], u[1]))
             d = self._w(FFN_W2, index)
-            return oracle.packed_linear(hidden, d[0], d[1])
+            return _linear(hidden, d[0], d[1])
         if pair:
             g, u = self._w(FFN_W1, index), self._w(FFN_W3, index)
-            gate, up = oracle.packed_linear_pair(ffn_input, g[0], g[1], u[0], u[1])
+            gate, up = _linear(ffn_input, g[0], g[1]), _linear(ffn_input, u[0], u[1])
         else:
             gate = self.linear(ffn_input, FFN_W1, index)
             up = self.linear(ffn_input, FFN_W3, index)
         if self._packed(FFN_W2, index):
             d = self._w(FFN_W2, index)
-            return oracle.packed_swiglu_linear(gate, up, d[0], d[1])
+            return _linear(oracle.swiglu(gate, up), d[0], d[1])
         return self.linear(oracle.swiglu(gate, up), FFN_W2, index)
 
     def append(self, tokens, produce_logits=True):
@@ -90,7 +122,7 @@ class OracleLfm2:
                 q = self.linear(u, QUERY, index)
                 if self._same_format(KEY, VALUE, index):
                     kw, vw = self._w(KEY, index), self._w(VALUE, index)
-                    k, v = oracle.packed_linear_pair(u, kw[0], kw[1], vw[0], vw[1])
+                    k, v = _linear(u, kw[0], kw[1]), _linear(u, vw[0], vw[1])
                 else:
                     k, v = self.linear(u, KEY, index), self.linear(u, VALUE, index)
                 q_rope, k_rope = oracle.qk_norm_rope(
@@ -100,7 +132,8 @@ class OracleLfm2:
                 attention, self.key[index], self.value[index], self.cache_len[index] = \
                     oracle.causal_gqa(q_rope, k_rope, v, self.key[index], self.value[index],
                                       self.cache_len[index], cfg.attention_heads,
-                                      cfg.key_value_heads, cfg.head_dim)
+                                      cfg.key_value_heads, cfg.head_dim, threads=THREADS,
+                                      in_place=True)
                 op = self.linear(attention, OUTPUT, index)
             residual, ffn_input = oracle.add_row_rms_norm(
                 x, op, self._w(FFN_NORM, index)[0], np.float32(cfg.block_norm_epsilon))

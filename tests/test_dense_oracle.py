@@ -235,3 +235,53 @@ def test_oracle_reports_nonfinite_like_the_reference():
     with pytest.raises(oracle.OracleError) as info:
         oracle.multiply(x, x)
     assert info.value.variant == "BackendFailure"
+
+
+# ---- the score-cached attention (used by the model oracle) -------------------
+
+@pytest.mark.parametrize("tokens,start,qh,kvh,d", [(1, 0, 2, 1, 4), (5, 3, 4, 2, 8),
+                                                   (17, 40, 6, 3, 16), (33, 0, 8, 8, 64)])
+@pytest.mark.parametrize("threads", [1, 3, 8])
+def test_cached_gqa_equals_the_literal_restatement(tokens, start, qh, kvh, d, threads):
+    """The cached form keeps every sum in the reference's order over the same
+    values, so it must equal the three-pass restatement bit for bit."""
+    rng = np.random.default_rng(tokens * 131 + start)
+    cap = start + tokens + 3
+    q = rng.standard_normal((tokens, qh * d)).astype(np.float32)
+    k = rng.standard_normal((tokens, kvh * d)).astype(np.float32)
+    v = rng.standard_normal((tokens, kvh * d)).astype(np.float32)
+    kc = np.zeros((cap, kvh * d), np.float32)
+    vc = np.zeros((cap, kvh * d), np.float32)
+    kc[:start] = rng.standard_normal((start, kvh * d))
+    vc[:start] = rng.standard_normal((start, kvh * d))
+    want = oracle.causal_gqa(q, k, v, kc, vc, start, qh, kvh, d)
+    got = oracle.causal_gqa(q, k, v, kc, vc, start, qh, kvh, d, threads=threads)
+    for a, b in zip(want[:3], got[:3]):
+        assert a.tobytes() == b.tobytes()
+    assert want[3] == got[3] == start + tokens
+    kc2, vc2 = kc.copy(), vc.copy()
+    got = oracle.causal_gqa(q, k, v, kc2, vc2, start, qh, kvh, d, threads=threads, in_place=True)
+    assert got[1] is kc2 and kc2.tobytes() == want[1].tobytes()
+    assert vc2.tobytes() == want[2].tobytes()
+
+
+def test_cached_gqa_fails_like_the_literal_restatement():
+    rng = np.random.default_rng(7)
+    q = rng.standard_normal((4, 16)).astype(np.float32)
+    k = rng.standard_normal((4, 8)).astype(np.float32)
+    v = rng.standard_normal((4, 8)).astype(np.float32)
+    kc = np.zeros((6, 8), np.float32)
+    vc = np.full((6, 8), 9.0, np.float32)
+    for bad in ("score", "value"):
+        qb, vb = q.copy(), v.copy()
+        if bad == "score":
+            qb[2, 3] = np.inf
+        else:
+            vb[1, 2] = np.nan
+        for threads in (0, 4):
+            kc2, vc2 = kc.copy(), vc.copy()
+            with pytest.raises(oracle.OracleError) as e:
+                oracle.causal_gqa(qb, k, vb, kc2, vc2, 0, 2, 1, 8, threads=threads,
+                                  in_place=True)
+            assert e.value.variant == "BackendFailure"
+            assert np.array_equal(kc2, kc) and np.array_equal(vc2, vc)

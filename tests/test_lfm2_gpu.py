@@ -80,9 +80,8 @@ def test_prefill_then_teacher_forced_decode(backend, path, mix):
 
 @pytest.mark.parametrize("mix", ["mixed", "ternary"])
 def test_decode_past_several_key_ranges(backend, path, mix):
-    # 140 cached keys: the one-launch decode attention splits them into
-    # three 64-key ranges whose records the last block combines; its arrival
-    # counters are reused by every attention layer and step.
+    # 140 cached keys: the decode attention kernel splits them into three
+    # 64-key ranges, whose records the separate combine launch merges.
     say("lfm2 long decode", mix, path)
     cfg, model, ref = build(backend, mix)
     prompt = convert.token_ids(140, 0x7043_0004, cfg.vocab)
@@ -123,6 +122,47 @@ def test_generate_matches_stepwise_sampling(backend):
         model.append(model.sampled)
     assert ids.tolist() == stepwise
     assert model.length == 9 + 8
+    model.close()
+
+
+def test_snapshot_restores_and_stays_unchanged(backend):
+    """A stored prefix continues exactly like the model it was taken from,
+    any number of times, and decoding from it leaves it unchanged
+    (Lfm2Prefix / fork, executor.rs:249-281, prefix_task.rs:158)."""
+    say("lfm2 snapshot")
+    cfg, model, ref = build(backend, "mixed")
+    prompt = convert.token_ids(70, 0x7043_0008, cfg.vocab)
+    model.append(prompt)
+    ref.append(prompt)
+    prefix = model.snapshot()
+    saved = ref.snapshot()
+    assert prefix.length == 70
+    first = backend.read(model.generate(6))
+    first_logits = backend.read(model.logits)
+    # Diverge: teacher-force other tokens, then fork from the prefix again.
+    model.restore(prefix)
+    for token in convert.token_ids(5, 0x7043_0009, cfg.vocab):
+        model.append([int(token)])
+    assert model.length == 75
+    for _ in range(2):
+        model.restore(prefix)
+        assert model.length == 70
+        assert backend.read(model.generate(6)).tobytes() == first.tobytes()
+        assert backend.read(model.logits).tobytes() == first_logits.tobytes()
+    # The restored state matches the oracle continued from its own copy.
+    model.restore(prefix)
+    ref.restore(saved)
+    for token in first[:3]:
+        model.append([int(token)])
+        check_logits(backend.read(model.logits), ref.append([int(token)]))
+    # A prefix belongs to its model.
+    from runtime_amd.backend import ExecutorError
+    other = Lfm2Model(backend, cfg)
+    with pytest.raises(ExecutorError) as info:
+        other.restore(prefix)
+    assert info.value.message == "prefix belongs to another model"
+    other.close()
+    prefix.close()
     model.close()
 
 

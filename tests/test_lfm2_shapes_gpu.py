@@ -1,0 +1,162 @@
+"""The LFM2 token pass at the measured model shapes.
+
+- The 350M shape (hidden 1024, 16 layers, all ternary) and the 1.2B shape
+  (hidden 2048, NF4 convolution/attention, ternary FFN, INT8 tied head):
+  a prompt pass, then greedy decode teacher-forced with the GPU's tokens,
+  every step's logits against the oracle model of the reference executor
+  (tests/lfm2_reference.py) within max|d|/max|cpu| <= 1e-3 and the device
+  rule |d| <= 1e-4 + 1e-4|cpu|.
+- The 1.2B shape past 2048 tokens, where no CPU oracle is affordable:
+  the fused decode step (decode-attention kernel over 40 key ranges, K-split
+  down projections, the 4-tile heads) against the op-by-op pass from the
+  same stored prefix, and the measured workload's properties: a 2048-token
+  prefill reused as a stored prefix, 512 greedy steps with finite logits,
+  mfl_generate equal to step-by-step sampling, and a chunked prefill equal
+  to the single pass within tolerance.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+
+from lfm2_reference import OracleLfm2
+from runtime_amd import convert
+from runtime_amd.backend import HipBackend
+from runtime_amd.lfm2 import Lfm2Model, attach, lfm2_1_2b, lfm2_350m, synthetic_host_weights
+from tests.conftest import assert_close, max_rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*parts):
+    print("[case]", *parts, flush=True)
+    sys.stdout.flush()
+
+
+def check_logits(got, want):
+    assert max_rel_err(got, want) <= 1e-3
+    assert_close(got, want)
+
+
+class Built:
+    def __init__(self, backend, cfg, keep_host):
+        self.cfg = cfg
+        self.model = Lfm2Model(backend, cfg)
+        self.host = {}
+        for role, layer, arrays in synthetic_host_weights(cfg, seed=0x5EED_1F00, norms="random"):
+            attach(self.model, role, layer, arrays)
+            if keep_host:
+                self.host[(role, layer)] = arrays
+
+
+@pytest.fixture(scope="module")
+def gpu():
+    b = HipBackend(0)
+    yield b
+    b.close()
+
+
+@pytest.fixture(scope="module")
+def m350(gpu):
+    say("build 350M shape")
+    built = Built(gpu, lfm2_350m(max_tokens=256), keep_host=True)
+    yield built
+    built.model.close()
+
+
+@pytest.fixture(scope="module")
+def m12(gpu):
+    say("build 1.2B shape")
+    built = Built(gpu, lfm2_1_2b(), keep_host=True)
+    yield built
+    built.model.close()
+
+
+def teacher_forced(backend, built, prompt_len, steps, seed):
+    cfg, model = built.cfg, built.model
+    ref = OracleLfm2(cfg, built.host)
+    model.reset()
+    prompt = convert.token_ids(prompt_len, seed, cfg.vocab)
+    model.append(prompt)
+    check_logits(backend.read(model.logits), ref.append(prompt))
+    for step in range(steps):
+        model.sample()
+        token = backend.read(model.sampled)[0]
+        want = ref.sample()
+        assert np.isfinite(token)
+        top = np.sort(ref.logits.reshape(-1))[-2:]
+        if top[1] - top[0] > 1e-4 * max(1.0, abs(top[1])):
+            assert token == want, (step, token, want)
+        model.append(model.sampled)  # the device id takes the fused step
+        check_logits(backend.read(model.logits), ref.append([int(token)]))
+    assert model.length == ref.length == prompt_len + steps
+
+
+def test_350m_shape_prefill_and_decode_against_the_oracle(gpu, m350):
+    say("350M shape: 128-token prompt, 8 teacher-forced steps")
+    teacher_forced(gpu, m350, 128, 8, 0x7043_0001)
+
+
+def test_1_2b_shape_prefill_and_decode_against_the_oracle(gpu, m12):
+    say("1.2B shape: 64-token prompt, 8 teacher-forced steps")
+    teacher_forced(gpu, m12, 64, 8, 0x7043_0005)
+
+
+def test_1_2b_fused_decode_equals_op_by_op_at_long_context(gpu, m12):
+    """2500 cached tokens: the fused step (kernel path 0) and the op-by-op
+    pass through the entry points (kernel path 3, parity-tested against the
+    oracle) from the same stored prefix, fed the same device ids."""
+    say("1.2B shape: fused vs op-by-op after 2500 tokens")
+    cfg, model = m12.cfg, m12.model
+    model.reset()
+    model.append(convert.token_ids(2500, 0x7043_0006, cfg.vocab))
+    prefix = model.snapshot()
+    ids = convert.token_ids(6, 0x7043_0007, cfg.vocab).astype(np.float32)
+    id_bufs = [gpu.upload_f32((1,), ids[i:i + 1]) for i in range(ids.size)]
+    runs = {}
+    for path in (0, 3):
+        previous = gpu.set_kernel_path(path)
+        try:
+            model.restore(prefix)
+            runs[path] = []
+            for buf in id_bufs:
+                model.append(buf)
+                runs[path].append(gpu.read(model.logits))
+        finally:
+            gpu.set_kernel_path(previous)
+    for fused, stepwise in zip(runs[0], runs[3]):
+        check_logits(fused, stepwise)
+    assert model.length == 2506
+    prefix.close()
+
+
+def test_1_2b_workload_from_a_stored_2048_token_prefix(gpu, m12):
+    say("1.2B shape: 2048-token stored prefix, 512 greedy steps")
+    cfg, model = m12.cfg, m12.model
+    model.reset()
+    prompt = convert.token_ids(2048, 0x7043_0001, cfg.vocab)
+    model.append(prompt)
+    prefix = model.snapshot()
+    assert prefix.length == 2048
+    whole = gpu.read(model.logits)
+    ids = gpu.read(model.generate(512))
+    assert model.length == 2048 + 512
+    # The prefix is unchanged by the decode that continued from it.
+    model.restore(prefix)
+    assert model.length == 2048
+    assert gpu.read(model.logits).tobytes() == whole.tobytes()
+    stepwise = []
+    for _ in range(512):
+        model.sample()
+        stepwise.append(gpu.read(model.sampled)[0])
+        model.append(model.sampled)
+        assert np.all(np.isfinite(gpu.read(model.logits)))
+    assert ids.tolist() == stepwise
+    # A chunked prefill (four passes of 512) gives the single pass's logits.
+    model.reset()
+    for c in range(4):
+        model.append(prompt[512 * c:512 * (c + 1)])
+    check_logits(gpu.read(model.logits), whole)
+    prefix.close()

@@ -133,16 +133,123 @@ def test_non_finite_activations_poison_their_rows(backend, path, scheme, n, k):
         assert_close(got[good], want, 1e-4, 1e-4)
 
 
+# Oracle results of the large cases, computed once per (case, inputs) and
+# shared by the kernel paths.
+_ORACLE_CACHE: dict = {}
+
+
+def cached_oracle(key, x, codes, scales):
+    if key not in _ORACLE_CACHE:
+        _ORACLE_CACHE[key] = oracle.packed_linear_threaded(x, codes, scales)
+    return _ORACLE_CACHE[key]
+
+
+_HEAD_WEIGHTS: dict = {}
+
+
+def head_weights(scheme):
+    if scheme not in _HEAD_WEIGHTS:
+        _HEAD_WEIGHTS.clear()
+        _HEAD_WEIGHTS[scheme] = make_weights(65536, 2048, scheme, 0x5EED0006)
+    return _HEAD_WEIGHTS[scheme]
+
+
 @pytest.mark.parametrize("scheme", SCHEMES)
-def test_lm_head_shape(backend, scheme):
-    say("lm head", scheme)
-    n, k, m = 65536, 2048, 2
-    codes, scales = make_weights(n, k, scheme, 0x5EED0006)
-    x = convert.normal((m, k), 0xAC70002)
+@pytest.mark.parametrize("m", [1, 2, 4, 8])
+def test_lm_head_shape(backend, path, scheme, m):
+    """The 65536 x 2048 LM-head shape at every decode batch: the benchmark's
+    dominant launch (B = 1), the one- and two-fragment kernels (B <= 4,
+    B = 5-8), on every kernel path."""
+    say("lm head", scheme, path, m)
+    n, k = 65536, 2048
+    codes, scales = head_weights(scheme)
+    x = convert.normal((m, k), 0xAC70001 + m)
     got = run_linear(backend, x, codes, scales)
-    want = oracle.packed_linear_threaded(x, codes, scales)
+    want = cached_oracle(("head", scheme, m), x, codes, scales)
     assert max_rel_err(got, want) <= 1e-3
     assert_close(got, want, 1e-4, 1e-4)
+
+
+# The prefill GEMM configuration: M in {512, 2048} tokens against 8192 x 2048
+# and 2048 x 8192 weights.  M = 512 is checked on every row; M = 2048 on a
+# seeded subset of rows (all N columns), the oracle being a scalar CPU path.
+_GEMM_WEIGHTS: dict = {}
+
+
+def gemm_weights(n, k, scheme):
+    key = (n, k, scheme)
+    if key not in _GEMM_WEIGHTS:
+        _GEMM_WEIGHTS.clear()
+        _GEMM_WEIGHTS[key] = make_weights(n, k, scheme, 0x5EED0001 + n + k)
+    return _GEMM_WEIGHTS[key]
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("n,k", [(8192, 2048), (2048, 8192)])
+@pytest.mark.parametrize("m", [512, 2048])
+@pytest.mark.parametrize("gemm_path", ["auto", "fma"])
+def test_prefill_gemm_config_shapes(backend, gemm_path, scheme, n, k, m):
+    say("prefill gemm config", scheme, gemm_path, m, n, k)
+    from tests.conftest import PATHS
+    codes, scales = gemm_weights(n, k, scheme)
+    x = convert.normal((m, k), 0xAC70003 + m)
+    previous = backend.set_kernel_path(PATHS[gemm_path])
+    try:
+        got = run_linear(backend, x, codes, scales)
+    finally:
+        backend.set_kernel_path(previous)
+    if m <= 512:
+        rows = np.arange(m)
+    else:
+        rng = np.random.default_rng(0x6E44 + n + k)
+        rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 94, replace=False)]))
+    want = cached_oracle(("gemm", scheme, n, k, m), x[rows], codes, scales)
+    assert np.all(np.isfinite(got))
+    assert max_rel_err(got[rows], want) <= 1e-3
+    assert_close(got[rows], want, 1e-4, 1e-4)
+
+
+# --- reserved ternary code 3 ----------------------------------------------------
+
+def test_ternary_reserved_code_decodes_as_plus_two(backend, path):
+    """Code 3 is reserved; backend-cpu decodes it as (3 - 1) = +2
+    (kernels-simd/src/lib.rs:77-78), and so must every GPU kernel: the
+    gather, the decode GEMV (whose tiles store field 3 as (c + 2) mod 4) and
+    the prefill GEMM."""
+    say("ternary code 3", path)
+    rng = np.random.default_rng(0x3333)
+    n, k = 320, 1024
+    codes = rng.integers(0, 256, size=(n, k // 4), dtype=np.int64).astype(np.uint8)
+    codes[:, :8] = 0xFF  # every field 3
+    codes[:, 8:16] = 0xC0  # field 3 of the top pair only
+    scales = convert.f16_to_f32(rng.uniform(0.001, 0.05, (n, k // 128)).astype(np.float16))
+    cb, sb = upload_weights(backend, codes, scales)
+    ids = [0, 5, 319, 77]
+    out = backend.allocate_f32((len(ids), k))
+    backend.packed_gather_rows(out, cb, sb, ids)
+    want_rows = oracle.packed_gather_rows(codes, scales, np.array(ids))
+    assert backend.read(out).tobytes() == want_rows.tobytes()
+    assert np.all(want_rows[:, :32] == 2 * np.repeat(scales[ids, :1], 32, axis=1))
+    for m in (1, 5, 100):
+        x = convert.normal((m, k), 0xAC70333 + m)
+        got = run_linear(backend, x, codes, scales)
+        assert_close(got, oracle.packed_linear(x, codes, scales), 1e-4, 1e-4)
+
+
+def test_reference_ternary_fixture_through_the_gpu_gather(backend, golden_dir):
+    """crates/executor-core/tests/fixtures/ternary-v1-001: the five rows'
+    expected dequantization, bit for bit, from the HIP gather."""
+    import json
+    doc = json.loads((golden_dir / "ternary-v1-001" / "vectors.json").read_text())
+    rows = doc["vectors"]
+    codes = np.stack([np.frombuffer(bytes.fromhex(v["expected_codes_hex"]), np.uint8)
+                      for v in rows])
+    scales16 = np.array([[v["scale_f16"]] for v in rows], dtype=np.float16)
+    expected = np.array([v["expected_dequant"] for v in rows], dtype=np.float32)
+    cb, sb = upload_weights(backend, codes, convert.f16_to_f32(scales16))
+    out = backend.allocate_f32((len(rows), 128))
+    backend.packed_gather_rows(out, cb, sb, list(range(len(rows))))
+    assert backend.read(out).tobytes() == expected.tobytes()
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
