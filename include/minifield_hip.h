@@ -276,6 +276,19 @@ int mfh_packed_prepared(const mfh_ctx *ctx, const mfh_buf *codes, const mfh_buf 
  * (inference.rs:268-309). */
 int mfh_supports_ternary_lut2(const mfh_ctx *ctx);
 
+/* No counterpart in the reference.  packed_linear for callers that cannot
+ * allocate device memory (code under stream capture, serving loops,
+ * harnesses that forbid hipMalloc): the same matrix-core decode GEMV as
+ * mfh_packed_linear, with the same admission and result bits, but its
+ * activation scratch is a fixed array of about 532 KiB that each GPU holds
+ * for the life of the process, so the call performs no device allocation.
+ * Serves input rows <= 8 and widths K <= 16384 (MFH_RESOURCE_LIMIT beyond
+ * it), on weights already prepared with mfh_prepare_packed (MFH_UNSUPPORTED
+ * otherwise, and on kernel path 1).  All calls on one GPU share the array:
+ * calls whose work overlaps on one GPU (several contexts or threads) race. */
+mfh_status mfh_packed_linear_noalloc(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
+                                     const mfh_buf *codes, const mfh_buf *scales);
+
 /* ---- dense LFM2 operations (the rest of a forward pass) ---------------- */
 /*
  * Same operand order as the trait.  Spec structs of the reference

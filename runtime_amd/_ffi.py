@@ -101,6 +101,7 @@ SIGNATURES = {
     "mfh_prepare_packed": (S, [P, P, P]),
     "mfh_packed_prepared": (ctypes.c_int, [P, P, P]),
     "mfh_supports_ternary_lut2": (ctypes.c_int, [P]),
+    "mfh_packed_linear_noalloc": (S, [P, P, P, P, P]),
     # dense ops
     "mfh_copy": (S, [P, P, P]),
     "mfh_copy_rect_2d": (S, [P, P, P] + [ctypes.c_uint64] * 6),

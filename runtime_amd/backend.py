@@ -303,6 +303,12 @@ class HipBackend:
         self._check(_ffi.lib().mfh_packed_linear(self._ctx, output.handle, input.handle,
                                                  codes.handle, scales.handle))
 
+    def packed_linear_noalloc(self, output: Buffer, input: Buffer, codes: Buffer,
+                              scales: Buffer) -> None:
+        """packed_linear without device allocation (mfh_packed_linear_noalloc)."""
+        self._check(_ffi.lib().mfh_packed_linear_noalloc(self._ctx, output.handle, input.handle,
+                                                         codes.handle, scales.handle))
+
     def packed_linear_pair(self, out_a: Buffer, out_b: Buffer, input: Buffer, codes_a: Buffer,
                            scales_a: Buffer, codes_b: Buffer, scales_b: Buffer) -> None:
         self._check(_ffi.lib().mfh_packed_linear_pair(

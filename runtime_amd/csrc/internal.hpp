@@ -88,6 +88,10 @@ struct mfh_ctx {
     size_t work_scratch_capacity = 0;
     void *digits_scratch = nullptr;
     size_t digits_scratch_capacity = 0;
+    // This device's address of the allocation-free entry point's fixed
+    // scratch array (noalloc.hip), looked up at mfh_create; null if the
+    // lookup failed.
+    void *noalloc_scratch = nullptr;
     // Live handles, orphaned (their ctx pointer cleared) when the context is
     // destroyed first, so a late release or free stays safe.
     std::unordered_set<mfh_buf *> live_buffers;
@@ -211,6 +215,9 @@ void *work_scratch(mfh_ctx *ctx, size_t bytes);
 void *digits_scratch(mfh_ctx *ctx, size_t bytes);
 inline mfh_status allocation_failed(mfh_ctx *) { return MFH_RESOURCE_LIMIT; }
 
+// The device address of the allocation-free scratch array on `device`
+// (which must be current), looked up once per device.
+mfh_status noalloc_scratch(int device, void **out);
 
 // Build (once, stream ordered) the tile-order copies the matrix-core
 // kernels read for the format the two streams' widths select: repacked

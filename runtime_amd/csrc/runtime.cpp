@@ -415,6 +415,8 @@ mfh_status mfh_create(uint32_t ordinal, uint64_t owner, const mfh_limits *limits
     ctx->identity.generation = 1;
     ctx->limits = *limits;
     ctx->pool.reset(new mfh::Pool(ctx->device));
+    if (noalloc_scratch(ctx->device, &ctx->noalloc_scratch))
+        ctx->noalloc_scratch = nullptr;
     *out = ctx;
     return MFH_OK;
 }
