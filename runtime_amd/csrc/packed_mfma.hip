@@ -1175,6 +1175,184 @@ void gemv_i8_kernel(MfmaArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Streaming ternary GEMV for wide matrices (the LM head, plain activations,
+// m <= 8).  Each wave owns one whole tile (16 rows x all of K), so there is
+// no cross-wave reduction and no second round of waves: the grid is one
+// block of kStreamWaves waves per kStreamWaves tiles.  Loads leave in the
+// order they are needed, because the vector memory counter retires them in
+// order: the tile's scale block (one coalesced load), the activations of the
+// wave's share of the prologue, then every weight load of the tile (KL
+// 16-byte loads per lane).  While the weights are in flight the block forms
+// the activation fragments of all of K in LDS: wave w takes fragment w / KL,
+// K block w % KL (256 k) and forms it with the register prologue's
+// arithmetic (reg_digits, the bytes digits_kernel writes; batch slots at or
+// beyond m become zero rows).  After one barrier each wave runs its tile's
+// MFMAs with the fragments, group constants and scales read from LDS.
+// Group sums are formed and scaled exactly as in i8_compute and accumulated
+// over the groups in order.
+// ---------------------------------------------------------------------------
+constexpr int kStreamWaves = 16;
+// Widest grids only: below this many tiles the K-split plans keep more
+// waves busy.
+constexpr uint32_t kStreamMinTiles = 1024;
+
+struct StreamArgs {
+    const float *x;  // [m, k] plain activations, 16-byte aligned
+    const uint8_t *tiles;
+    const void *scales;
+    float *out;
+    uint32_t m, n, k, n_tiles;
+};
+
+// One (batch slot, group) record of the prologue: the correction pair and
+// the group factor, read with one 16-byte LDS load.
+struct StreamRecord {
+    int2 corr;
+    float xf;
+    float pad;
+};
+
+template <int NF, int KL, bool HALF>
+__global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(StreamArgs a)
+{
+    using ST = typename ScaleT<HALF>::type;
+    using B = I8Block<Format::Ternary, 1, 1, NF, HALF>;
+    constexpr int G = 2 * KL;   // 128-groups of K (the tile width is 256 * KL)
+    constexpr int KS = 4 * KL;  // 64-wide ksteps
+    static_assert(NF * KL <= kStreamWaves, "one prologue K block per wave");
+    // Scale block of a tile: G * 16 values, one SV vector per lane for the
+    // first SLANES lanes.
+    typedef typename std::conditional<HALF, uint2, v4u>::type SV;
+    constexpr int SLANES = G * 16 * (HALF ? 2 : 4) / int(sizeof(SV));
+    // Fragments [kstep][fragment][lane] (the MFMA A operand of every lane),
+    // records [slot][group], each wave's scale block.
+    __shared__ v4i frag[KS * NF * 64];
+    __shared__ StreamRecord rec[4 * NF * G];
+    __shared__ SV scale_lds[kStreamWaves * SLANES];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t tile_id = blockIdx.x * kStreamWaves + wave;
+    const uint32_t tile = tile_id < a.n_tiles ? tile_id : a.n_tiles - 1;
+
+    // 1. The tile's scale block.
+    SV sv{};
+    if (lane < uint32_t(SLANES))
+        sv = reinterpret_cast<const SV *>(a.scales)[size_t(tile) * SLANES + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. The activations of this wave's prologue block (fragment pf, K block
+    // pu): lane 16q + 4b + p holds x[4 pf + b][256 pu + 64 kk + 16q + 4p + t].
+    const bool former = wave < uint32_t(NF * KL);
+    const uint32_t pf = wave / KL, pu = wave % KL;
+    const uint32_t pb = 4 * pf + ((lane >> 2) & 3);
+    const bool row_live = former && pb < a.m;
+    RegX<4> rx;
+    reg_load(rx, a.x + size_t(row_live ? pb : 0) * a.k, row_live, a.k, 0, pu);
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. Every weight load of the tile.
+    v4u w[KL];
+    {
+        const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * KL * 64 + lane;
+        // Each weight byte is read once: non-temporal loads keep the
+        // activations and scales of the next calls in the caches.
+#pragma unroll
+        for (int l = 0; l < KL; ++l)
+            w[l] = __builtin_nontemporal_load(&wp[l * 64]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 4. The prologue block's fragments and records, then the scale block,
+    // into LDS.
+    if (former) {
+        B blk;
+        auto emit = [&](auto f_tag) {
+            constexpr int F = decltype(f_tag)::value;
+            reg_digits(rx, blk, F);
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                frag[((4 * pu + ks) * NF + F) * 64 + lane] = blk.af[ks][F];
+            if (j == 0) {
+#pragma unroll
+                for (int gg = 0; gg < 2; ++gg)
+                    rec[(4 * F + q) * G + 2 * pu + gg] =
+                        StreamRecord{blk.cv[gg][F], blk.xf[gg][F], 0.0f};
+            }
+        };
+        if (NF == 1 || pf == 0)
+            emit(std::integral_constant<int, 0>{});
+        else
+            emit(std::integral_constant<int, NF - 1>{});
+    }
+    if (lane < uint32_t(SLANES))
+        scale_lds[wave * SLANES + lane] = sv;
+    __syncthreads();
+
+    // 5. The tile's products.  The fragments of the next group are read
+    // while the current group's MFMAs run; the compiler barrier keeps reads
+    // from being hoisted further.
+    const v4i *ap = frag + lane;
+    const ST *scl = reinterpret_cast<const ST *>(scale_lds + wave * SLANES) + j;
+    auto read_group = [&](int g, v4i (&av)[2][NF]) {
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                av[kk][f] = ap[((2 * g + kk) * NF + f) * 64];
+    };
+    float accf[NF];
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+        accf[f] = 0.0f;
+    v4i cur[2][NF], next[2][NF];
+    read_group(0, cur);
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        if (g + 1 < G)
+            read_group(g + 1, next);
+        v4i acci[NF];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            acci[f] = v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int s = 2 * g + kk;
+            const unsigned word = w[s / 4][s % 4];
+            const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
+                               int(word & 0xC0C0C0C0u)};
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                acci[f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[kk][f], bw, acci[f], 0, 0, 0);
+        }
+        const float scale = to_f32<HALF>(scl[g * 16]);
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            const StreamRecord r = rec[(4 * f + q) * G + g];
+            const v4i d = acci[f];
+            // |d.x| < 2^21, so the pairs combine exactly in int32.
+            const int hi = (d.x << 8) + d.y - r.corr.x;
+            const int lo = (d.z << 8) + d.w - r.corr.y;
+            const float gsum = float(hi) * 65536.0f + float(lo);
+            accf[f] += gsum * (scale * r.xf);
+            // Keep the accumulation here: otherwise it sinks into the
+            // guarded store below and every group's MFMA results stay live.
+            asm volatile("" : "+v"(accf[f]));
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                cur[kk][f] = next[kk][f];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint32_t row = tile_id * 16 + j;
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const uint32_t b = 4 * f + q;
+        if (tile_id < a.n_tiles && b < a.m && row < a.n)
+            a.out[size_t(b) * a.n + row] = accf[f];
+    }
+}
+
+// ---------------------------------------------------------------------------
 // NF4 GEMV on f16 MFMA.  One loop block = one 16-byte lane load per tile =
 // four 32-wide ksteps = one 128-weight group.
 // ---------------------------------------------------------------------------
@@ -1777,12 +1955,61 @@ void set_segments(MfmaArgs &args, const PackedCall &call)
     }
 }
 
+template <int NF, int KL>
+void launch_stream_ternary(hipStream_t stream, const StreamArgs &args, bool half)
+{
+    const unsigned blocks = (args.n_tiles + kStreamWaves - 1) / kStreamWaves;
+    if (half)
+        stream_ternary_kernel<NF, KL, true><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
+    else
+        stream_ternary_kernel<NF, KL, false><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
+}
+
+// Serves the call with the streaming kernel when it applies; false leaves
+// it to the K-split plans.
+bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
+{
+    const uint32_t k_pad = pad_to(call.k, 256);
+    const uint32_t kl = k_pad / 256;
+    if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
+        call.epilogue != Epilogue::Single || call.m == 0 || call.m > 8 ||
+        n_tiles < kStreamMinTiles || (kl != 4 && kl != 8) ||
+        reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
+        return false;
+    StreamArgs args{};
+    args.x = call.x;
+    args.tiles = call.a.tiles;
+    args.scales = call.a.tiled_scales;
+    args.out = call.out_a;
+    args.m = call.m;
+    args.n = call.n;
+    args.k = call.k;
+    args.n_tiles = n_tiles;
+    const bool half = call.a.tiled_half;
+    auto go = [&](auto nf_tag) {
+        constexpr int NF = decltype(nf_tag)::value;
+        if (kl == 4)
+            launch_stream_ternary<NF, 4>(stream, args, half);
+        else
+            launch_stream_ternary<NF, 8>(stream, args, half);
+    };
+    if (call.m <= 4)
+        go(std::integral_constant<int, 1>{});
+    else
+        go(std::integral_constant<int, 2>{});
+    return true;
+}
+
 template <Format F>
 void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
 {
     const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
+    if constexpr (F == Format::Ternary) {
+        if (try_stream_ternary(stream, call, n_tiles))
+            return;
+    }
     const int nf = call.m <= 4 ? 1 : 2;
     Scratch sc = carve(scratch, k_pad);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
