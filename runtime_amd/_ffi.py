@@ -138,6 +138,18 @@ SIGNATURES = {
     "mfl_restore": (S, [P, P]),
     "mfl_prefix_length": (ctypes.c_uint64, [P]),
     "mfl_prefix_destroy": (None, [P]),
+    # safetensors loader (minifield_loader.h)
+    "mfs_open": (S, [ctypes.c_char_p, ctypes.c_uint64, PP]),
+    "mfs_close": (None, [P]),
+    "mfs_error": (ctypes.c_char_p, []),
+    "mfs_tensor_count": (SZ, [P]),
+    "mfs_tensor_name": (ctypes.c_char_p, [P, SZ]),
+    "mfs_tensor_info": (S, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int), c_u32_p, c_u64_p]),
+    "mfs_metadata": (ctypes.c_char_p, [P, ctypes.c_char_p]),
+    "mfs_matmul_scheme": (S, [P, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int)]),
+    "mfs_upload_packed": (S, [P, P, ctypes.c_char_p, ctypes.c_int, PP, PP]),
+    "mfs_upload_dense": (S, [P, P, ctypes.c_char_p, ctypes.c_int, PP]),
+    "mfl_load_safetensors": (S, [P, P]),
     # diagnostics
     "mfh_stream": (P, [P]),
     "mfh_set_kernel_path": (ctypes.c_int, [P, ctypes.c_int]),

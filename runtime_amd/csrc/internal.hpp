@@ -215,6 +215,13 @@ void *work_scratch(mfh_ctx *ctx, size_t bytes);
 void *digits_scratch(mfh_ctx *ctx, size_t bytes);
 inline mfh_status allocation_failed(mfh_ctx *) { return MFH_RESOURCE_LIMIT; }
 
+// An F32 rank-2 buffer of binary16 file values: the 2-byte values are
+// uploaded into the buffer's binary16 shadow and decoded to f32 on the
+// device (exact; the loader's f16 -> f32 rule).  The caller has checked that
+// every value is finite.
+mfh_status upload_scales_f16(mfh_ctx *ctx, const uint64_t *dims, const uint16_t *bits,
+                             size_t count, mfh_alloc_class cls, mfh_buf **out);
+
 // The device address of the allocation-free scratch array on `device`
 // (which must be current), looked up once per device.
 mfh_status noalloc_scratch(int device, void **out);

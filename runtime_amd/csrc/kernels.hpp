@@ -116,6 +116,9 @@ void launch_gemm_fma(hipStream_t stream, const PackedCall &call);
 size_t gemm_mfma_scratch_bytes(const PackedCall &call);
 void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch);
 
+// out[i] = the binary16 value bits[i] as f32 (exact).
+void launch_f16_to_f32(hipStream_t stream, float *out, const uint16_t *bits, size_t count);
+
 // out[i] = silu(gate[i]) * up[i], the reference's SwiGLU staging
 // (backend-cpu/src/packed.rs:431-441).
 void launch_swiglu(hipStream_t stream, float *out, const float *gate, const float *up,

@@ -10,9 +10,12 @@
 #include <cmath>
 #include <map>
 #include <memory>
+#include <set>
+#include <string>
 #include <vector>
 
 #include "../../include/minifield_lfm2.h"
+#include "../../include/minifield_loader.h"
 #include "internal.hpp"
 #include "kernels.hpp"
 
@@ -88,6 +91,8 @@ struct mfl_model {
     std::map<uint64_t, std::unique_ptr<Workspace>> workspaces;
     Owned logits, sampled;
     Owned rotation;  // [max_tokens, head_dim] rotation coefficients by position
+    // Weights uploaded by mfl_load_safetensors (the model owns them).
+    std::vector<std::unique_ptr<Owned>> loaded;
 };
 
 // An immutable copy of a model's prefix state (Lfm2Prefix,
@@ -860,6 +865,158 @@ uint64_t mfl_prefix_length(const mfl_prefix *p)
 void mfl_prefix_destroy(mfl_prefix *p)
 {
     delete p;
+}
+
+}  // extern "C"
+
+namespace {
+
+struct RolePlan {
+    uint32_t role, layer;
+    std::string name;
+    uint64_t dims[3];
+    uint32_t rank;
+    bool matmul;
+};
+
+// weights.rs:268-500: the tensor of every role of the configuration.
+std::vector<RolePlan> role_plan(const mfl_model *m)
+{
+    const mfl_config &c = m->config;
+    const uint64_t h = c.hidden, inter = c.intermediate, kv = m->kv_width;
+    std::vector<RolePlan> plan;
+    plan.push_back({MFL_TOKEN_EMBEDDING, 0, "model.embed_tokens.weight", {c.vocab, h, 0}, 2, true});
+    plan.push_back({MFL_EMBEDDING_NORM, 0, "model.embedding_norm.weight", {h, 0, 0}, 1, false});
+    for (uint32_t i = 0; i < c.layer_count; ++i) {
+        const std::string p = "model.layers." + std::to_string(i);
+        if (m->kinds[i] == 0) {
+            plan.push_back({MFL_CONV_KERNEL, i, p + ".conv.conv.weight", {h, 1, c.conv_width}, 3,
+                            false});
+            plan.push_back({MFL_CONV_IN, i, p + ".conv.in_proj.weight", {3 * h, h, 0}, 2, true});
+            plan.push_back({MFL_CONV_OUT, i, p + ".conv.out_proj.weight", {h, h, 0}, 2, true});
+        } else {
+            plan.push_back({MFL_QUERY_NORM, i, p + ".self_attn.q_layernorm.weight",
+                            {c.head_dim, 0, 0}, 1, false});
+            plan.push_back({MFL_KEY_NORM, i, p + ".self_attn.k_layernorm.weight",
+                            {c.head_dim, 0, 0}, 1, false});
+            plan.push_back({MFL_QUERY, i, p + ".self_attn.q_proj.weight", {h, h, 0}, 2, true});
+            plan.push_back({MFL_KEY, i, p + ".self_attn.k_proj.weight", {kv, h, 0}, 2, true});
+            plan.push_back({MFL_VALUE, i, p + ".self_attn.v_proj.weight", {kv, h, 0}, 2, true});
+            plan.push_back({MFL_OUTPUT, i, p + ".self_attn.out_proj.weight", {h, h, 0}, 2, true});
+        }
+        plan.push_back({MFL_FFN_W1, i, p + ".feed_forward.w1.weight", {inter, h, 0}, 2, true});
+        plan.push_back({MFL_FFN_W2, i, p + ".feed_forward.w2.weight", {h, inter, 0}, 2, true});
+        plan.push_back({MFL_FFN_W3, i, p + ".feed_forward.w3.weight", {inter, h, 0}, 2, true});
+        plan.push_back({MFL_FFN_NORM, i, p + ".ffn_norm.weight", {h, 0, 0}, 1, false});
+        plan.push_back({MFL_OPERATOR_NORM, i, p + ".operator_norm.weight", {h, 0, 0}, 1, false});
+    }
+    return plan;
+}
+
+mfh_status load_error(mfh_ctx *c, mfh_status s)
+{
+    // Keep the loader's message on the context too.
+    return fail(c, s, mfs_error());
+}
+
+bool dims_equal(const uint64_t *a, uint32_t ra, const uint64_t *b, uint32_t rb)
+{
+    if (ra != rb)
+        return false;
+    for (uint32_t i = 0; i < ra; ++i)
+        if (a[i] != b[i])
+            return false;
+    return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+mfh_status mfl_load_safetensors(mfl_model *m, const mfs_file *file)
+{
+    if (!m)
+        return MFH_INVALID_ARGUMENT;
+    mfh_ctx *c = m->ctx;
+    if (!file)
+        return fail(c, MFH_INVALID_ARGUMENT, "safetensors file is null");
+    const std::vector<RolePlan> plan = role_plan(m);
+    // 1. Check the whole inventory before uploading anything.
+    std::vector<mfs_scheme> schemes(plan.size(), MFS_SCHEME_DENSE);
+    std::set<std::string> consumed;
+    for (size_t r = 0; r < plan.size(); ++r) {
+        const RolePlan &rp = plan[r];
+        mfs_dtype dtype;
+        uint32_t rank = 0;
+        uint64_t dims[4] = {0, 0, 0, 0};
+        if (rp.matmul) {
+            mfh_status s = mfs_matmul_scheme(file, rp.name.c_str(), &schemes[r]);
+            if (s)
+                return load_error(c, s);
+        }
+        if (schemes[r] == MFS_SCHEME_DENSE) {
+            mfh_status s = mfs_tensor_info(file, rp.name.c_str(), &dtype, &rank, dims);
+            if (s)
+                return load_error(c, s);
+            if (!dims_equal(dims, rank, rp.dims, rp.rank))
+                return fail(c, MFH_INVALID_SHAPE, "tensor shape differs from the model plan");
+            if (dtype == MFS_U8)
+                return fail(c, MFH_INVALID_DTYPE, "dense LFM2 weights are F32, F16 or BF16");
+            consumed.insert(rp.name);
+            continue;
+        }
+        const uint64_t wpb = schemes[r] == MFS_SCHEME_TERNARY ? 4
+                             : schemes[r] == MFS_SCHEME_NF4   ? 2
+                                                              : 1;
+        if (rp.dims[1] % 128)
+            return fail(c, MFH_INVALID_SHAPE, "packed weight input width must be a multiple of 128");
+        const uint64_t codes_dims[2] = {rp.dims[0], rp.dims[1] / wpb};
+        const uint64_t scale_dims[2] = {rp.dims[0], rp.dims[1] / 128};
+        const std::string cn = rp.name + ".codes", sn = rp.name + ".scales";
+        mfh_status s = mfs_tensor_info(file, cn.c_str(), &dtype, &rank, dims);
+        if (s)
+            return load_error(c, s);
+        if (dtype != MFS_U8 || !dims_equal(dims, rank, codes_dims, 2))
+            return fail(c, MFH_INVALID_SHAPE, "packed codes differ from the role's stored scheme");
+        if ((s = mfs_tensor_info(file, sn.c_str(), &dtype, &rank, dims)))
+            return load_error(c, s);
+        if (dtype != MFS_F16 || !dims_equal(dims, rank, scale_dims, 2))
+            return fail(c, MFH_INVALID_SHAPE, "packed scales differ from the role's stored scheme");
+        consumed.insert(cn);
+        consumed.insert(sn);
+    }
+    for (size_t i = 0; i < mfs_tensor_count(file); ++i)
+        if (!consumed.count(mfs_tensor_name(file, i)))
+            return fail(c, MFH_UNEXPECTED_TENSOR, "undeclared tensor is present");
+    // 2. Upload and attach.
+    for (size_t r = 0; r < plan.size(); ++r) {
+        const RolePlan &rp = plan[r];
+        mfh_status s;
+        if (schemes[r] == MFS_SCHEME_DENSE) {
+            auto t = std::make_unique<Owned>();
+            if ((s = mfs_upload_dense(c, file, rp.name.c_str(), MFH_CLASS_WEIGHT, &t->buf)))
+                return load_error(c, s);
+            if (rp.role == MFL_CONV_KERNEL) {
+                // [hidden, 1, width] -> [hidden, width]: the same elements.
+                t->buf->rank = 2;
+                t->buf->dims[1] = rp.dims[2];
+                t->buf->dims[2] = 0;
+            }
+            if ((s = mfl_set_weight(m, rp.role, rp.layer, t->buf, nullptr)))
+                return s;
+            m->loaded.push_back(std::move(t));
+        } else {
+            auto codes = std::make_unique<Owned>(), scales = std::make_unique<Owned>();
+            if ((s = mfs_upload_packed(c, file, rp.name.c_str(), MFH_CLASS_WEIGHT, &codes->buf,
+                                       &scales->buf)))
+                return load_error(c, s);
+            if ((s = mfl_set_weight(m, rp.role, rp.layer, codes->buf, scales->buf)))
+                return s;
+            m->loaded.push_back(std::move(codes));
+            m->loaded.push_back(std::move(scales));
+        }
+    }
+    return MFH_OK;
 }
 
 }  // extern "C"

@@ -505,6 +505,42 @@ void launch_packed_gather(hipStream_t stream, Format format, float *out, const u
     }
 }
 
+// f16_to_f32 of the loader (executor-core/src/loader.rs:408-421), in integer
+// steps so that no floating-point mode (denormal flushing) can change a bit:
+// a subnormal m * 2^-24 is normalised by its leading bit.
+__global__ void f16_to_f32_kernel(float *out, const uint16_t *bits, size_t count)
+{
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const uint32_t h = bits[i];
+        const uint32_t sign = (h & 0x8000u) << 16;
+        const uint32_t exponent = (h >> 10) & 0x1Fu;
+        uint32_t mantissa = h & 0x3FFu;
+        uint32_t w;
+        if (exponent == 0) {
+            if (mantissa == 0) {
+                w = 0;
+            } else {
+                // value = mantissa * 2^-24 = 1.f * 2^(lead - 24)
+                const int lead = 31 - __clz(mantissa);
+                mantissa = (mantissa << (23 - lead)) & 0x7FFFFFu;
+                w = (uint32_t(lead - 24 + 127) << 23) | mantissa;
+            }
+        } else if (exponent == 31) {
+            w = 0x7F800000u | (mantissa << 13);
+        } else {
+            w = ((exponent + 112) << 23) | (mantissa << 13);
+        }
+        out[i] = __uint_as_float(w | sign);
+    }
+}
+
+void launch_f16_to_f32(hipStream_t stream, float *out, const uint16_t *bits, size_t count)
+{
+    if (count)
+        f16_to_f32_kernel<<<grid_for(count), 256, 0, stream>>>(out, bits, count);
+}
+
 void launch_fill_f32(hipStream_t stream, float *dst, size_t count, float value)
 {
     if (count)

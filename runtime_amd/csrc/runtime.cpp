@@ -8,6 +8,7 @@
 #include <new>
 
 #include "internal.hpp"
+#include "kernels.hpp"
 #include "../../include/minifield_convert.h"
 
 namespace mfh {
@@ -636,6 +637,51 @@ mfh_status mfh_upload_u8(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, cons
     }
     return MFH_OK;
 }
+
+}  // extern "C"
+
+namespace mfh {
+
+mfh_status upload_scales_f16(mfh_ctx *ctx, const uint64_t *dims, const uint16_t *bits,
+                             size_t count, mfh_alloc_class cls, mfh_buf **out)
+{
+    DeviceGuard guard(ctx->device);
+    mfh_status s = make_buffer(ctx, dims, 2, MFH_DTYPE_F32, cls, out);
+    if (s)
+        return s;
+    mfh_buf *buf = *out;
+    if (count != buf->elements || (count && !bits)) {
+        mfh_release(buf);
+        *out = nullptr;
+        return fail(ctx, MFH_INVALID_SHAPE, "upload length differs from shape element count");
+    }
+    if (!count)
+        return MFH_OK;
+    if ((s = acquire_for(ctx, buf, count * 2, &buf->f16_shadow, &buf->f16_capacity))) {
+        buf->f16_shadow = nullptr;
+        mfh_release(buf);
+        *out = nullptr;
+        return s;
+    }
+    if (hipMemcpyAsync(buf->f16_shadow, bits, count * 2, hipMemcpyHostToDevice, ctx->stream) !=
+        hipSuccess) {
+        (void)hipGetLastError();
+        mfh_release(buf);
+        *out = nullptr;
+        return fail(ctx, MFH_BACKEND_FAILURE, "host to device copy failed");
+    }
+    launch_f16_to_f32(ctx->stream, static_cast<float *>(buf->dev),
+                      static_cast<const uint16_t *>(buf->f16_shadow), count);
+    if (hipStreamSynchronize(ctx->stream) != hipSuccess) {
+        (void)hipGetLastError();
+        return fail(ctx, MFH_BACKEND_FAILURE, "host to device copy failed");
+    }
+    return MFH_OK;
+}
+
+}  // namespace mfh
+
+extern "C" {
 
 void mfh_release(mfh_buf *buf)
 {
