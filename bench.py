@@ -7,9 +7,12 @@ the sweep -- {ternary, nf4, int8} x {1024x1024, 4608x1024, 2048x2048,
 matrices quantized by the backend's converter (group-128, FP16-exact scales);
 activations are seeded N(0, 1).  Everything is resident in HBM before timing.
 
-Launches are eager (the host enqueues ahead of the device); consecutive uses
-of one matrix rotate over weight copies so that the large matrices stream
-from HBM rather than the 256 MB Infinity Cache.
+Launches are eager (the host enqueues ahead of the device).  Each launch of a
+step takes its own weight copy (one per batch size) and steps rotate over
+`--copies` sets, so a matrix is reused only after more than 1 GB of other
+weights have streamed: every launch reads HBM, not the 256 MB Infinity
+Cache.  The per-launch table rotates each shape over copies totalling at
+least 1 GiB.
 
 `value` = algorithmic bytes of all launches / device time of the K timed
 steps (HIP events on the backend's stream), where a launch's bytes are
@@ -18,7 +21,9 @@ their stored FP16 width, activations, outputs).  The roofline object is for
 the dominant operation (the 65536x2048 INT8 head at B=1, one GEMV kernel
 that forms its activation digits in registers): its bytes over its average
 duration across back-to-back launches on rotating copies, against the
-8 TB/s HBM peak.
+8 TB/s HBM peak.  Its `traffic` is measured by this run: two rocprofv3
+--pmc child runs of the dominant launch (FETCH_SIZE, then WRITE_SIZE, KiB per
+dispatch) each scaled by the same counter over a 256 MiB device copy.
 """
 from __future__ import annotations
 
@@ -36,10 +41,9 @@ SHAPES = [(1024, 1024), (4608, 1024), (2048, 2048), (8192, 2048), (2048, 8192), 
 BATCHES = [1, 2, 4, 8]
 HBM_PEAK_GBS = 8000.0
 DOMINANT = ("int8", (65536, 2048), 1)
-# HBM bytes per dominant launch (one GEMV kernel) from rocprofv3 FETCH_SIZE
-# and WRITE_SIZE runs of `--profile dominant`, scaled by the same counters
-# over `--profile copy` (profiles/int8_gemv_65536x2048_b1.md).
-DOMINANT_TRAFFIC_BYTES = 136_726_339
+# Weight bytes each shape of the per-launch table rotates over.
+ROTATE_BYTES = 1 << 30
+COPY_BYTES = 256 << 20  # the calibration copy of the traffic counters
 
 
 def algorithmic_bytes(n: int, k: int, b: int, fmt: str) -> int:
@@ -50,28 +54,116 @@ def log(*parts):
     print("[bench]", *parts, file=sys.stderr, flush=True)
 
 
+def host_cpu() -> dict:
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "nproc": os.cpu_count(),
+            "allowed_cpus": len(os.sched_getaffinity(0))}
+
+
 def cpu_baseline(weights, xs) -> dict:
     """The oracle (a C restatement of the reference's single-threaded
     backend-cpu path, admission scans included) over every launch of one
-    sweep step, on one host core."""
+    sweep step, pinned to one host core."""
     import oracle
 
-    total_bytes = 0
-    sweeps = 0
-    start = time.perf_counter()
-    while sweeps == 0 or time.perf_counter() - start < 10.0:
-        for fmt in FORMATS:
-            for (n, k) in SHAPES:
-                codes, scales = weights[(fmt, n, k)]
-                for b in BATCHES:
-                    oracle.packed_linear(xs[(b, k)], codes, scales)
-                    total_bytes += algorithmic_bytes(n, k, b, fmt)
-        sweeps += 1
-    seconds = time.perf_counter() - start
-    return {"value": round(total_bytes / seconds / 1e9, 3), "unit": "GB/s", "cores": 1,
-            "kind": "port",
-            "sample": f"oracle packed_linear over {sweeps} full sweep steps (72 launches each, "
-                      f"{total_bytes / 1e6:.0f} MB algorithmic, {seconds:.1f} s)"}
+    allowed = os.sched_getaffinity(0)
+    core = min(allowed)
+    os.sched_setaffinity(0, {core})
+    try:
+        total_bytes = 0
+        sweeps = 0
+        start = time.perf_counter()
+        while sweeps == 0 or time.perf_counter() - start < 10.0:
+            for fmt in FORMATS:
+                for (n, k) in SHAPES:
+                    codes, scales = weights[(fmt, n, k)]
+                    for b in BATCHES:
+                        oracle.packed_linear(xs[(b, k)], codes, scales)
+                        total_bytes += algorithmic_bytes(n, k, b, fmt)
+            sweeps += 1
+        seconds = time.perf_counter() - start
+    finally:
+        os.sched_setaffinity(0, allowed)
+    out = {"value": round(total_bytes / seconds / 1e9, 3), "unit": "GB/s", "cores": 1,
+           "kind": "port",
+           "sample": f"oracle packed_linear over {sweeps} full sweep steps (72 launches each, "
+                     f"{total_bytes / 1e6:.0f} MB algorithmic, {seconds:.1f} s) pinned to "
+                     f"host core {core}"}
+    out.update(host_cpu())
+    return out
+
+
+def measure_traffic() -> dict:
+    """HBM bytes per dominant launch from two rocprofv3 --pmc runs
+    (FETCH_SIZE, then WRITE_SIZE, in KiB per dispatch) of `--profile
+    dominant`, each scaled by what the same counter reads for a 256 MiB
+    device copy (`--profile copy`).  Run as child processes before this
+    process touches the GPU; None when rocprofv3 is unavailable."""
+    import shutil
+    import signal
+    import sqlite3
+    import subprocess
+    import tempfile
+
+    tool = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(tool):
+        return {"bytes": None, "note": "rocprofv3 not found"}
+    me = os.path.abspath(__file__)
+    env = dict(os.environ, TMPDIR="/tmp")
+
+    def per_dispatch(counter: str, profile: str, kernel: str) -> float:
+        with tempfile.TemporaryDirectory(dir="/tmp") as tmp:
+            cmd = [tool, "--pmc", counter, "-d", tmp, "-o", "run", "--", sys.executable, me,
+                   "--profile", profile]
+            # Its own process group, so a run past its limit is ended whole.
+            proc = subprocess.Popen(cmd, cwd="/tmp", env=env, stdout=subprocess.PIPE,
+                                    stderr=subprocess.STDOUT, text=True, start_new_session=True)
+            try:
+                text, _ = proc.communicate(timeout=150)
+            except subprocess.TimeoutExpired:
+                os.killpg(proc.pid, signal.SIGKILL)
+                proc.communicate()
+                raise RuntimeError(f"rocprofv3 {counter} {profile}: over 150 s")
+            dbs = [os.path.join(root, f) for root, _, files in os.walk(tmp)
+                   for f in files if f.endswith("results.db")]
+            # 139: the profiler's own exit after a complete run.
+            if proc.returncode not in (0, 139) or not dbs:
+                raise RuntimeError(f"rocprofv3 {counter} {profile}: rc {proc.returncode}: "
+                                   f"{text[-400:]}")
+            con = sqlite3.connect(dbs[0])
+            rows = con.execute("select dispatch_id, kernel_name, value from counters_collection "
+                               "where counter_name = ?", (counter,)).fetchall()
+        per = {}
+        for d, name, v in rows:
+            if kernel in name:
+                per[d] = per.get(d, 0.0) + v
+        values = sorted(per.values())
+        if not values:
+            raise RuntimeError(f"no {kernel} dispatch in the {counter} run")
+        return values[len(values) // 2]
+
+    try:
+        out = {}
+        total = 0.0
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            log(f"  {counter}: calibration copy, then the dominant launch")
+            copy_kib = per_dispatch(counter, "copy", "copy_kernel")
+            dom_kib = per_dispatch(counter, "dominant", "gemv")
+            scale = (COPY_BYTES / 1024) / copy_kib  # real KiB per counted KiB
+            out[counter] = {"dominant_kib": round(dom_kib, 1), "copy_kib": round(copy_kib, 1),
+                            "scale": round(scale, 4)}
+            total += dom_kib * scale * 1024
+        out["bytes"] = int(total)
+        return out
+    except Exception as e:  # the bench still reports everything else
+        return {"bytes": None, "note": str(e)[:300]}
 
 
 # Prefill GEMM workload: M tokens x (N x K) weights, every format.
@@ -138,10 +230,13 @@ LFM2_WORKLOADS = {
 def lfm2_decode(backend, name: str) -> dict:
     """Random-init model of the named shape (seeded N(0, 0.02) weights
     quantized per role, unit norm weights), a uniform-random prompt
-    (seed 0x7043_0001) prefilled as one token pass, then greedy decode on the
-    device (argmax -> device-id gather each step, no host round trip).
-    Decode tok/s = steps / device time of the decode loop (HIP events);
-    prefill tok/s likewise for the prompt pass."""
+    (seed 0x7043_0001) prefilled as one token pass and kept as a stored
+    prefix (mfl_snapshot), then greedy decode from that prefix on the device
+    (argmax -> device-id gather each step, no host round trip), twice: the
+    fused one-token step, and the same pass issued op by op through the
+    InferenceOps entry points (kernel path 3).  Decode tok/s = steps / device
+    time of the decode loop (HIP events); prefill tok/s likewise for the
+    prompt pass."""
     from runtime_amd import convert, hiptime, lfm2
 
     factory, prompt_len, steps = LFM2_WORKLOADS[name]
@@ -157,44 +252,64 @@ def lfm2_decode(backend, name: str) -> dict:
     build_s = time.perf_counter() - t0
     prompt = convert.token_ids(prompt_len, 0x7043_0001, cfg.vocab)
     stream = backend.stream()
-    # Warm pass: builds the repacked layouts and the workspaces of both row
-    # counts, so the timed passes allocate nothing.
+    # Warm pass: the workspaces of both row counts, so the timed passes
+    # allocate nothing.
     model.append(prompt)
     model.generate(4)
     backend.synchronize()
     model.reset()
-    e0, e1, e2 = hiptime.Event(), hiptime.Event(), hiptime.Event()
+    e0, e1 = hiptime.Event(), hiptime.Event()
     e0.record(stream)
     model.append(prompt)
     e1.record(stream)
-    h0 = time.perf_counter()
-    ids = model.generate(steps)
-    host_ms = (time.perf_counter() - h0) * 1e3
-    e2.record(stream)
-    e2.synchronize()
+    e1.synchronize()
     prefill_ms = e1.elapsed_ms(e0)
-    decode_ms = e2.elapsed_ms(e1)
-    tokens = backend.read(ids)
-    finite = bool(np.all(np.isfinite(tokens)))
+    prefix = model.snapshot()
+    out = {"config": factory, "prompt": prompt_len, "decode_steps": steps,
+           "prefill_tok_s": round(prompt_len / (prefill_ms / 1e3), 1),
+           "weight_bytes_per_token": weight_bytes, "build_s": round(build_s, 1)}
+    tokens = {}
+    for label, path in (("fused", 0), ("op_by_op", 3)):
+        previous = backend.set_kernel_path(path)
+        try:
+            model.restore(prefix)
+            model.generate(2)
+            model.restore(prefix)
+            backend.synchronize()
+            d0, d1 = hiptime.Event(), hiptime.Event()
+            d0.record(stream)
+            h0 = time.perf_counter()
+            ids = model.generate(steps)
+            host_ms = (time.perf_counter() - h0) * 1e3
+            d1.record(stream)
+            d1.synchronize()
+        finally:
+            backend.set_kernel_path(previous)
+        decode_ms = d1.elapsed_ms(d0)
+        tokens[label] = backend.read(ids)
+        line = {"decode_tok_s": round(steps / (decode_ms / 1e3), 1),
+                "decode_ms_per_token": round(decode_ms / steps, 4),
+                "decode_weight_GBs": round(weight_bytes / (decode_ms / steps / 1e3) / 1e9, 1),
+                "host_enqueue_ms_per_token": round(host_ms / steps, 4)}
+        if label == "fused":
+            out.update(line)
+        else:
+            out["op_by_op"] = line
+        log(f"lfm2 {name} {label}: prefill {prompt_len} in {prefill_ms:.1f} ms, "
+            f"decode {steps} in {decode_ms:.1f} ms")
+    out["tokens_finite"] = bool(np.all(np.isfinite(tokens["fused"])))
+    out["op_by_op_tokens_equal"] = bool(np.array_equal(tokens["fused"], tokens["op_by_op"]))
+    prefix.close()
     model.close()
-    log(f"lfm2 {name}: prefill {prompt_len} in {prefill_ms:.1f} ms, "
-        f"decode {steps} in {decode_ms:.1f} ms")
-    return {"config": factory, "prompt": prompt_len, "decode_steps": steps,
-            "decode_tok_s": round(steps / (decode_ms / 1e3), 1),
-            "decode_ms_per_token": round(decode_ms / steps, 4),
-            "prefill_tok_s": round(prompt_len / (prefill_ms / 1e3), 1),
-            "weight_bytes_per_token": weight_bytes,
-            "decode_weight_GBs": round(weight_bytes / (decode_ms / steps / 1e3) / 1e9, 1),
-            "host_enqueue_ms_per_token": round(host_ms / steps, 4),
-            "tokens_finite": finite, "build_s": round(build_s, 1)}
+    return out
 
 
 def profile_only(backend, args) -> int:
     """Launch sequences for rocprofv3: `dominant` builds the 65536x2048 INT8
-    head (same seed as the sweep) on `copies` buffers and launches it
-    8 * copies times after one untimed pass; `copy` moves 256 MiB with
-    mfh_copy four times, the known-size reference for FETCH_SIZE and
-    WRITE_SIZE."""
+    head (same seed as the sweep) on copies totalling 1 GiB and launches it
+    100 times over them after one untimed pass per copy; `copy` moves
+    256 MiB with mfh_copy four times, the known-size reference for
+    FETCH_SIZE and WRITE_SIZE."""
     from runtime_amd import convert
     from runtime_amd.backend import WEIGHT
 
@@ -224,24 +339,64 @@ def profile_only(backend, args) -> int:
         log(f"copied {count * 4} bytes x 4")
         return 0
     fmt, (n, k), b = DOMINANT
-    dense = convert.normal((n, k), 0x5EED0001 + SHAPES.index((n, k)), sigma=0.02)
-    codes, scales16 = convert.quantize(dense, fmt)
-    scales = convert.f16_to_f32(scales16)
-    del dense
-    copies = [(backend.upload_u8_classified(codes.shape, codes, WEIGHT),
-               backend.upload_f32_classified(scales.shape, scales, WEIGHT))
-              for _ in range(args.copies)]
+    codes, scales = sweep_weights(convert, fmt, n, k)
+    copies = rotation(backend, codes, scales)
     x = backend.upload_f32((b, k), convert.normal((b, k), 0xAC70001 + b))
     out = backend.allocate_f32((b, n))
     for c, s in copies:
         backend.packed_linear(out, x, c, s)
     backend.synchronize()
-    for r in range(8 * args.copies):
-        c, s = copies[r % args.copies]
+    launches = max(100, 4 * len(copies))
+    for r in range(launches):
+        c, s = copies[r % len(copies)]
         backend.packed_linear(out, x, c, s)
     backend.synchronize()
-    log(f"{fmt} {n}x{k} B={b}: {8 * args.copies} launches after one pass per copy")
+    log(f"{fmt} {n}x{k} B={b}: {launches} launches over {len(copies)} copies "
+        f"after one pass per copy")
     return 0
+
+
+def sweep_weights(convert, fmt: str, n: int, k: int):
+    """The sweep's weights of one (format, shape): codes and f32 scales."""
+    dense = convert.normal((n, k), 0x5EED0001 + SHAPES.index((n, k)), sigma=0.02)
+    codes, scales16 = convert.quantize(dense, fmt)
+    return codes, convert.f16_to_f32(scales16)
+
+
+def stored_bytes(codes, scales) -> int:
+    return codes.size + scales.size * 2
+
+
+def rotation(backend, codes, scales, total: int = ROTATE_BYTES):
+    """Device copies of one matrix, prepared, totalling at least `total`
+    stored bytes, so a rotation over them reuses a copy only after about
+    1 GiB of other weights has streamed."""
+    from runtime_amd.backend import WEIGHT
+    count = -(-total // stored_bytes(codes, scales))
+    out = []
+    for _ in range(count):
+        c = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
+        s = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
+        backend.prepare_packed(c, s)
+        out.append((c, s))
+    return out
+
+
+def time_launches(backend, stream, run, reps: int, prime) -> float:
+    """Average device time (us) of `reps` calls of run(r), bracketed by one
+    HIP event pair on the backend's stream.  `prime()` first enqueues enough
+    long launches that the host has enqueued the timed ones before the
+    device reaches them (a small matrix takes less device time than its
+    host-side enqueue)."""
+    from runtime_amd import hiptime
+    prime()
+    e0, e1 = hiptime.Event(), hiptime.Event()
+    e0.record(stream)
+    for r in range(reps):
+        run(r)
+    e1.record(stream)
+    e1.synchronize()
+    return e1.elapsed_ms(e0) / reps * 1e3
 
 
 def main() -> int:
@@ -249,8 +404,13 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--copies", type=int, default=3)
+    ap.add_argument("--copies", type=int, default=len(BATCHES),
+                    help="weight sets the sweep rotates over (one per batch size by default)")
+    ap.add_argument("--reps", type=int, default=100,
+                    help="launches per entry of the per-launch table")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-traffic", action="store_true",
+                    help="skip the rocprofv3 --pmc traffic measurement")
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM cases")
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
@@ -266,6 +426,14 @@ def main() -> int:
               "run it with --gpus 1", file=sys.stderr)
         return 2
 
+    traffic = None
+    if not args.profile and not args.no_traffic:
+        # Child processes own the GPU for these runs; this one has not
+        # touched it yet.
+        log("measuring dominant-launch HBM traffic (rocprofv3 --pmc)")
+        traffic = measure_traffic()
+        log(f"traffic: {traffic}")
+
     from runtime_amd import convert, hiptime
     from runtime_amd.backend import WEIGHT, HipBackend
 
@@ -275,49 +443,46 @@ def main() -> int:
         return profile_only(backend, args)
 
     log("generating and quantizing weights")
-    weights = {}
-    for si, (n, k) in enumerate(SHAPES):
-        dense = convert.normal((n, k), 0x5EED0001 + si, sigma=0.02)
-        for fmt in FORMATS:
-            codes, scales16 = convert.quantize(dense, fmt)
-            weights[(fmt, n, k)] = (codes, convert.f16_to_f32(scales16))
-        del dense
+    weights = {(fmt, n, k): sweep_weights(convert, fmt, n, k)
+               for (n, k) in SHAPES for fmt in FORMATS}
     xs = {(b, k): convert.normal((b, k), 0xAC70001 + b)
           for b in BATCHES for k in sorted({k for _, k in SHAPES})}
 
-    log(f"uploading {args.copies} weight copies")
+    log(f"uploading {args.copies} weight sets")
     dev_w = {}
     for key, (codes, scales) in weights.items():
-        dev_w[key] = [(backend.upload_u8_classified(codes.shape, codes, WEIGHT),
-                       backend.upload_f32_classified(scales.shape, scales, WEIGHT))
-                      for _ in range(args.copies)]
+        dev_w[key] = []
+        for _ in range(args.copies):
+            c = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
+            s = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
+            backend.prepare_packed(c, s)
+            dev_w[key].append((c, s))
     dev_x = {key: backend.upload_f32(x.shape, x) for key, x in xs.items()}
     dev_out = {(b, n): backend.allocate_f32((b, n)) for b in BATCHES for n, _ in SHAPES}
+    set_bytes = sum(stored_bytes(c, s) for c, s in weights.values())
 
     launches = [(fmt, (n, k), b) for b in BATCHES for fmt in FORMATS for (n, k) in SHAPES]
     step_bytes = sum(algorithmic_bytes(n, k, b, fmt) for fmt, (n, k), b in launches)
 
     def launch(i: int, copy_set: int) -> None:
         fmt, (n, k), b = launches[i]
-        # Successive launches of one matrix (one per batch size) take
-        # successive copies.
+        # The launches of one matrix in a step (one per batch size) take
+        # distinct weight sets.
         c, s = dev_w[(fmt, n, k)][(copy_set + BATCHES.index(b)) % args.copies]
         backend.packed_linear(dev_out[(b, n)], dev_x[(b, k)], c, s)
 
-    def enqueue(first: int, last: int, copy_set: int) -> None:
-        for i in range(first, last):
+    def enqueue(copy_set: int) -> None:
+        for i in range(len(launches)):
             launch(i, copy_set)
 
-    # Eager pass: builds every per-buffer derived layout (repacked tiles,
-    # tiled scales) before anything is timed.
     for cs in range(args.copies):
-        enqueue(0, len(launches), cs)
+        enqueue(cs)
     backend.synchronize()
 
     # Launches are eager: the host enqueues ahead of the device, so the
     # stream stays busy and the timed region is device time.
     for w in range(args.warmup):
-        enqueue(0, len(launches), w % args.copies)
+        enqueue(w)
     backend.synchronize()
 
     log(f"timing {args.steps} steps")
@@ -325,58 +490,75 @@ def main() -> int:
     start.record(stream)
     t0 = time.perf_counter()
     for step in range(args.steps):
-        enqueue(0, len(launches), step % args.copies)
+        enqueue(step)
     enqueue_s = time.perf_counter() - t0
     stop.record(stream)
     stop.synchronize()
     wall_s = time.perf_counter() - t0
     total_ms = stop.elapsed_ms(start)
-
-    # Dominant operation: back-to-back launches over rotating weight copies
-    # (each launch streams its matrix from HBM), bracketed by one event pair
-    # on the backend's stream.  One launch is one GEMV kernel.
-    di = launches.index(DOMINANT)
-    dom_reps = 8 * args.copies
-    for r in range(args.copies):
-        launch(di, r)
-    backend.synchronize()
-    d0, d1 = hiptime.Event(), hiptime.Event()
-    d0.record(stream)
-    for r in range(dom_reps):
-        launch(di, r)
-    d1.record(stream)
-    d1.synchronize()
-    dom_ms = d1.elapsed_ms(d0) / dom_reps
-
     ms_per_step = total_ms / args.steps
     value_gbs = step_bytes * args.steps / (total_ms / 1e3) / 1e9
-    fmt, (n, k), b = DOMINANT
-    dom_bytes = algorithmic_bytes(n, k, b, fmt)
-    achieved = dom_bytes / (dom_ms / 1e3) / 1e9
+    host_us = enqueue_s * 1e6 / (args.steps * len(launches))
 
-    # Per-launch table (outside the timed region): each operation launched
-    # back to back over the rotating copies between one event pair.  Matrices
-    # far smaller than the 256 MB Infinity Cache stay resident in it here.
-    # Eight dominant launches (about 200 us of device work) go first, so the
-    # host has enqueued the timed launches before the device reaches them: a
-    # two-kernel launch of a small matrix takes less device time than its
-    # host-side enqueue.
+    # Dominant operation: >= 100 back-to-back launches over copies totalling
+    # 1 GiB (each launch streams its matrix from HBM), between one event pair
+    # on the backend's stream.  One launch is one GEMV kernel.
+    log("dominant operation")
+    fmt, (n, k), b = DOMINANT
+    dom_copies = rotation(backend, *weights[(fmt, n, k)])
+    dom_x, dom_out = dev_x[(b, k)], dev_out[(b, n)]
+    dom_rot = [0]
+
+    def dominant(_r: int = 0) -> None:
+        c, s = dom_copies[dom_rot[0] % len(dom_copies)]
+        dom_rot[0] += 1
+        backend.packed_linear(dom_out, dom_x, c, s)
+
+    for _ in range(len(dom_copies)):
+        dominant()
+    backend.synchronize()
+    dom_reps = max(100, 4 * len(dom_copies))
+    dom_us = time_launches(backend, stream, dominant, dom_reps, lambda: None)
+    dom_bytes = algorithmic_bytes(n, k, b, fmt)
+    achieved = dom_bytes / (dom_us / 1e6) / 1e9
+
+    # Per-launch table (outside the timed region): each (format, shape) over
+    # copies totalling at least 1 GiB, `reps` launches per batch size
+    # continuing one rotation, primed with dominant launches covering the
+    # host-side enqueue of the timed ones.
     log("per-launch table")
-    repeats = 4 * args.copies
+    prime_count = int(np.ceil(1.5 * args.reps * host_us / dom_us)) + 2
+
+    def prime() -> None:
+        for _ in range(prime_count):
+            dominant()
+
     detail = {}
-    for i, (fmt_i, (n_i, k_i), b_i) in enumerate(launches):
-        for r in range(8):
-            launch(di, r)
-        e0, e1 = hiptime.Event(), hiptime.Event()
-        e0.record(stream)
-        for r in range(repeats):
-            launch(i, r)
-        e1.record(stream)
-        e1.synchronize()
-        us = e1.elapsed_ms(e0) / repeats * 1e3
-        detail[f"{fmt_i}:{n_i}x{k_i}:B{b_i}"] = {
-            "us": round(us, 2),
-            "GBs": round(algorithmic_bytes(n_i, k_i, b_i, fmt_i) / (us / 1e6) / 1e9, 1)}
+    rotations = {}
+    for fmt_i in FORMATS:
+        for (n_i, k_i) in SHAPES:
+            copies = rotation(backend, *weights[(fmt_i, n_i, k_i)])
+            rotations[f"{fmt_i}:{n_i}x{k_i}"] = len(copies)
+            rot = [0]
+            for b_i in BATCHES:
+                x_i, out_i = dev_x[(b_i, k_i)], dev_out[(b_i, n_i)]
+
+                def run(_r, copies=copies, x_i=x_i, out_i=out_i):
+                    c, s = copies[rot[0] % len(copies)]
+                    rot[0] += 1
+                    backend.packed_linear(out_i, x_i, c, s)
+
+                us = time_launches(backend, stream, run, args.reps, prime)
+                detail[f"{fmt_i}:{n_i}x{k_i}:B{b_i}"] = {
+                    "us": round(us, 2),
+                    "GBs": round(algorithmic_bytes(n_i, k_i, b_i, fmt_i) / (us / 1e6) / 1e9, 1)}
+            del copies
+    heads = {}
+    for fmt_i in FORMATS:
+        entry = detail[f"{fmt_i}:65536x2048:B1"]
+        heads[fmt_i] = {"us": entry["us"], "achieved": entry["GBs"],
+                        "frac": round(entry["GBs"] / HBM_PEAK_GBS, 4),
+                        "algorithmic_bytes": algorithmic_bytes(65536, 2048, 1, fmt_i)}
 
     result = {
         "metric": "packed GEMV HBM GB/s (% of 8 TB/s peak); LFM2 batch-1 decode tok/s",
@@ -395,7 +577,8 @@ def main() -> int:
             "workload": "decode GEMV sweep {ternary,nf4,int8} x {1024x1024,4608x1024,"
                         "2048x2048,8192x2048,2048x8192,65536x2048} x B{1,2,4,8}, "
                         "72 launches per step",
-            "weight_copies": args.copies,
+            "weight_sets": args.copies,
+            "weight_set_bytes": set_bytes,
             "bytes_per_step": step_bytes,
             "host_wall_s": round(wall_s, 4),
             "host_enqueue_ms_per_step": round(enqueue_s * 1e3 / args.steps, 4),
@@ -407,12 +590,19 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": DOMINANT_TRAFFIC_BYTES,
+            "traffic": traffic["bytes"] if traffic else None,
+            "traffic_detail": traffic,
             "algorithmic_bytes": dom_bytes,
-            "avg_launch_us": round(dom_ms * 1e3, 3),
+            "avg_launch_us": round(dom_us, 3),
+            "launches": dom_reps,
+            "rotating_copies": len(dom_copies),
         },
+        "roofline_by_format": heads,
         "detail": detail,
+        "detail_method": {"reps": args.reps, "rotating_copies": rotations,
+                          "prime_launches": prime_count},
     }
+    del dom_copies
     if not args.no_cpu:
         log("timing the CPU baseline")
         result["cpu_baseline"] = cpu_baseline(weights, xs)
