@@ -307,7 +307,8 @@ def lfm2_decode(backend, name: str) -> dict:
 def profile_only(backend, args) -> int:
     """Launch sequences for rocprofv3: `dominant` builds the 65536x2048 INT8
     head (same seed as the sweep) on copies totalling 1 GiB and launches it
-    100 times over them after one untimed pass per copy; `copy` moves
+    100 times over them after one untimed pass per copy (`head-ternary` and
+    `head-nf4`: the same for that format's head); `copy` moves
     256 MiB with mfh_copy four times, the known-size reference for
     FETCH_SIZE and WRITE_SIZE."""
     from runtime_amd import convert
@@ -339,6 +340,8 @@ def profile_only(backend, args) -> int:
         log(f"copied {count * 4} bytes x 4")
         return 0
     fmt, (n, k), b = DOMINANT
+    if args.profile.startswith("head-"):
+        fmt = args.profile[5:]
     codes, scales = sweep_weights(convert, fmt, n, k)
     copies = rotation(backend, codes, scales)
     x = backend.upload_f32((b, k), convert.normal((b, k), 0xAC70001 + b))
@@ -414,11 +417,12 @@ def main() -> int:
     ap.add_argument("--no-gemm", action="store_true", help="skip the prefill GEMM cases")
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
-    ap.add_argument("--profile", choices=["dominant", "copy", "lfm2-350m", "lfm2-1.2b", "gemm"],
-                    help="run only the dominant operation (or a 256 MiB device copy, the "
-                         "counter calibration, an LFM2 decode, or the ternary "
-                         "M=2048 x 8192x2048 prefill GEMM) for rocprofv3, and print no "
-                         "JSON line")
+    ap.add_argument("--profile", choices=["dominant", "head-ternary", "head-nf4", "copy",
+                                          "lfm2-350m", "lfm2-1.2b", "gemm"],
+                    help="run only the dominant operation (or the 65536x2048 head of "
+                         "another format, a 256 MiB device copy, the counter calibration, "
+                         "an LFM2 decode, or the ternary M=2048 x 8192x2048 prefill GEMM) "
+                         "for rocprofv3, and print no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the packed GEMV path on a "

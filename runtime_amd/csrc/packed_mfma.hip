@@ -852,6 +852,23 @@ __device__ __forceinline__ void reg_load(RegX<LB> &rx, const float *xrow, bool l
     }
 }
 
+// As reg_load, for the streaming kernels: every load is issued (a dead row
+// reads clamped addresses of row 0 and is zeroed afterwards), because a branch
+// around a load can make the compiler wait for it before the weight loads that
+// follow.
+template <int LB>
+__device__ __forceinline__ void reg_load_issued(RegX<LB> &rx, const float *xrow, bool live,
+                                                uint32_t k, uint32_t index, uint32_t off,
+                                                uint32_t kstep)
+{
+#pragma unroll
+    for (int kk = 0; kk < LB; ++kk) {
+        const uint32_t kx = kstep * (index * LB + kk) + off;
+        const v4f v = *reinterpret_cast<const v4f *>(xrow + (kx < k ? kx : k - 4));
+        rx.v[kk] = live && kx < k ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+}
+
 // Fragment f (batch rows 4f..4f+3) of a loop block from this lane's values.
 template <Format F, int T, int S, int NF, bool HALF>
 __device__ __forceinline__ void reg_digits(const RegX<Geo<F>::lb> &rx,
@@ -1181,8 +1198,9 @@ void gemv_i8_kernel(MfmaArgs a)
 // block of kStreamWaves waves per kStreamWaves tiles.  Loads leave in the
 // order they are needed, because the vector memory counter retires them in
 // order: the tile's scale block (one coalesced load), the activations of the
-// wave's share of the prologue, then every weight load of the tile (KL
-// 16-byte loads per lane).  While the weights are in flight the block forms
+// wave's share of the prologue, then the first weight loads of the tile (one
+// 16-byte load per lane per 256 k), the rest following kStreamTernaryAhead
+// loads ahead of the products.  While the weights are in flight the block forms
 // the activation fragments of all of K in LDS: wave w takes fragment w / KL,
 // K block w % KL (256 k) and forms it with the register prologue's
 // arithmetic (reg_digits, the bytes digits_kernel writes; batch slots at or
@@ -1192,6 +1210,14 @@ void gemv_i8_kernel(MfmaArgs a)
 // over the groups in order.
 // ---------------------------------------------------------------------------
 constexpr int kStreamWaves = 16;
+// Weight loads a wave keeps in flight ahead of its products: a wave that
+// issues all of its loads first stalls at the issue of the later ones and
+// only computes once they have nearly all arrived.  Measured at 65536 x 2048,
+// one row: ternary (one load = 256 k) 9.9 us with all eight ahead, 9.5 /
+// 8.8 / 8.1 / 8.2 with one to four; NF4 (one load = 128 k) 28.4 us with all
+// sixteen, 24.4 with eight, 21.5 / 20.0 / 21.5 / 21.9 with one to four.
+constexpr int kStreamTernaryAhead = 3;
+constexpr int kStreamNf4Ahead = 2;
 // Widest grids only: below this many tiles the K-split plans keep more
 // waves busy.
 constexpr uint32_t kStreamMinTiles = 1024;
@@ -1246,18 +1272,20 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(Strea
     const uint32_t pb = 4 * pf + ((lane >> 2) & 3);
     const bool row_live = former && pb < a.m;
     RegX<4> rx;
-    reg_load(rx, a.x + size_t(row_live ? pb : 0) * a.k, row_live, a.k, 0, pu);
+    reg_load_issued(rx, a.x + size_t(row_live ? pb : 0) * a.k, row_live, a.k, pu,
+                    16 * (lane >> 4) + 4 * (lane & 3), 64);
     __builtin_amdgcn_sched_barrier(0);
-    // 3. Every weight load of the tile.
+    // 3. The first kStreamTernaryAhead weight loads of the tile; the load
+    // of K block l + kStreamTernaryAhead leaves when block l's products
+    // begin.  Each
+    // weight byte is read once: non-temporal loads keep the activations and
+    // scales of the next calls in the caches.
     v4u w[KL];
-    {
-        const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * KL * 64 + lane;
-        // Each weight byte is read once: non-temporal loads keep the
-        // activations and scales of the next calls in the caches.
+    const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * KL * 64 + lane;
+    constexpr int AHEAD = KL < kStreamTernaryAhead ? KL : kStreamTernaryAhead;
 #pragma unroll
-        for (int l = 0; l < KL; ++l)
-            w[l] = __builtin_nontemporal_load(&wp[l * 64]);
-    }
+    for (int l = 0; l < AHEAD; ++l)
+        w[l] = __builtin_nontemporal_load(&wp[l * 64]);
     __builtin_amdgcn_sched_barrier(0);
 
     // 4. The prologue block's fragments and records, then the scale block,
@@ -1306,6 +1334,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(Strea
     read_group(0, cur);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+        if (g % 2 == 0 && g / 2 + AHEAD < KL)
+            w[g / 2 + AHEAD] = __builtin_nontemporal_load(&wp[(g / 2 + AHEAD) * 64]);
         if (g + 1 < G)
             read_group(g + 1, next);
         v4i acci[NF];
@@ -1361,6 +1391,20 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(Strea
 // copies 27.2, 31.3 and 45.6 us against 25.4) -- the build work and LDS
 // footprint cost more than the bank conflicts they remove.
 constexpr uint32_t kLutCopies = 1;
+
+// Table entry for one code byte: x = hi halves of (low nibble, high nibble),
+// y = lo halves, each a packed f16 pair for consecutive k.
+__device__ __forceinline__ uint2 nf4_lut_entry(uint32_t e)
+{
+    const float l0 = kNf4Levels[e & 15], l1 = kNf4Levels[e >> 4];
+    const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
+    const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
+    return uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
+                     (unsigned(__builtin_bit_cast(unsigned short, h1)) << 16),
+                 unsigned(__builtin_bit_cast(unsigned short, r0)) |
+                     (unsigned(__builtin_bit_cast(unsigned short, r1)) << 16)};
+}
+
 template <int T, int S, bool HALF>
 struct Nf4Block {
     v4u w[S][T];
@@ -1531,18 +1575,8 @@ void gemv_nf4_kernel(MfmaArgs a)
     // kLutCopies interleaved copies of the 256-entry table; lane l reads copy
     // l % kLutCopies, so the lanes of one LDS cycle spread over distinct banks.
     __shared__ uint2 lut_all[256 * kLutCopies];
-    for (uint32_t i = threadIdx.x; i < 256 * kLutCopies; i += blockDim.x) {
-        // Entry for one code byte: x = hi halves of (low nibble, high nibble),
-        // y = lo halves, each a packed f16 pair for consecutive k.
-        const uint32_t e = i / kLutCopies;
-        const float l0 = kNf4Levels[e & 15], l1 = kNf4Levels[e >> 4];
-        const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
-        const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
-        lut_all[i] = uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
-                               (unsigned(__builtin_bit_cast(unsigned short, h1)) << 16),
-                           unsigned(__builtin_bit_cast(unsigned short, r0)) |
-                               (unsigned(__builtin_bit_cast(unsigned short, r1)) << 16)};
-    }
+    for (uint32_t i = threadIdx.x; i < 256 * kLutCopies; i += blockDim.x)
+        lut_all[i] = nf4_lut_entry(i / kLutCopies);
     __syncthreads();
     const uint2 *lut = lut_all + (threadIdx.x % kLutCopies);
 
@@ -1649,6 +1683,185 @@ void gemv_nf4_kernel(MfmaArgs a)
     }
     const uint32_t batch[2] = {2 * q, 2 * q + 1};
     reduce_and_store<S, T, 2, E>(a.m, tg, accf, batch, j, a.kparts > 1);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming NF4 GEMV for wide matrices (the LM head, plain activations,
+// m <= 8), laid out as stream_ternary_kernel: each wave owns one whole tile
+// (16 rows x all of K) and the block forms the f16 activation fragments of
+// all of K once, in LDS, for its kStreamWaves tiles.  Loads leave in the
+// order they are needed: the tile's scale block, the activations of the
+// wave's prologue group (wave w forms 128-group w with nf4_reg_halves'
+// arithmetic; batch slots at or beyond m become zero rows), then the first
+// weight loads of the tile (16 bytes per lane per group), the rest following
+// kStreamNf4Ahead groups ahead of the products.  After the barriers each wave
+// runs its tile's MFMAs kstep by kstep, reading the next kstep's fragment and
+// table entries while the current kstep's MFMAs run.  Group sums are formed
+// and scaled exactly as in nf4_compute and accumulated over the groups in
+// order.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kStreamLutCopies = 32;
+
+// nf4_lut_entry with the levels read by scalar loads and picked by selects:
+// a per-lane constant-memory load issued after the weight loads would wait
+// for all of them (loads retire in order).
+__device__ __forceinline__ uint2 nf4_lut_entry_uniform(uint32_t e)
+{
+    float lv[16];
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+        lv[c] = kNf4Levels[c];
+    float l0 = lv[0], l1 = lv[0];
+#pragma unroll
+    for (int c = 1; c < 16; ++c) {
+        l0 = (e & 15u) == uint32_t(c) ? lv[c] : l0;
+        l1 = (e >> 4) == uint32_t(c) ? lv[c] : l1;
+    }
+    const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
+    const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
+    return uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
+                     (unsigned(__builtin_bit_cast(unsigned short, h1)) << 16),
+                 unsigned(__builtin_bit_cast(unsigned short, r0)) |
+                     (unsigned(__builtin_bit_cast(unsigned short, r1)) << 16)};
+}
+template <int G, bool HALF>
+__global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArgs a)
+{
+    using ST = typename ScaleT<HALF>::type;
+    constexpr int KS = 4 * G;  // 32-wide ksteps
+    static_assert(G <= kStreamWaves, "one prologue group per wave");
+    typedef typename std::conditional<HALF, uint2, v4u>::type SV;
+    constexpr int SLANES = G * 16 * (HALF ? 2 : 4) / int(sizeof(SV));
+    static_assert(SLANES <= 64, "one scale vector per lane");
+    // Fragments [kstep][lane], group factors [batch slot][group], each
+    // wave's scale block, and the code-byte table: 256 B per byte value,
+    // kStreamLutCopies copies of its hi word, then as many of its lo word.
+    // Lane l reads copy l % 32, so every word of a read comes from the bank
+    // of its copy, and a byte's cell address is one byte permute of the code
+    // word.
+    __shared__ v8h frag[KS * 64];
+    __shared__ float xfs[8 * G];
+    __shared__ SV scale_lds[kStreamWaves * SLANES];
+    __shared__ unsigned lut[256 * 2 * kStreamLutCopies];
+    __shared__ uint2 entries[256];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t tile_id = blockIdx.x * kStreamWaves + wave;
+    const uint32_t tile = tile_id < a.n_tiles ? tile_id : a.n_tiles - 1;
+
+    // 1. The tile's scale block.
+    SV sv{};
+    if (lane < uint32_t(SLANES))
+        sv = reinterpret_cast<const SV *>(a.scales)[size_t(tile) * SLANES + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. The activations of this wave's prologue group (lane 16q + 2b + h:
+    // batch slot b).
+    const bool former = wave < uint32_t(G);
+    const uint32_t pb = (lane >> 1) & 7;
+    const bool row_live = former && pb < a.m;
+    RegX<4> rx;
+    reg_load_issued(rx, a.x + size_t(row_live ? pb : 0) * a.k, row_live, a.k,
+                    former ? wave : 0, nf4_reg_offset(), 32);
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. The first kStreamNf4Ahead weight loads of the tile (each byte is
+    // read once); the load of group g + kStreamNf4Ahead leaves when group g's
+    // products begin.
+    v4u w[G];
+    const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * G * 64 + lane;
+    constexpr int AHEAD = G < kStreamNf4Ahead ? G : kStreamNf4Ahead;
+#pragma unroll
+    for (int g = 0; g < AHEAD; ++g)
+        w[g] = __builtin_nontemporal_load(&wp[g * 64]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 4. The table, the prologue group's fragments and factors and the
+    // scale block, into LDS.  Only the fragment rows of live batch slots
+    // (j < 2m) are written; a lane of a dead slot reads a live row of its
+    // lane block instead (its output rows are never stored, and the read
+    // shares the live lane's address).
+    const uint32_t rp = 2 * a.m;
+    const bool row_read = j < rp;
+    if (threadIdx.x < 256)
+        entries[threadIdx.x] = nf4_lut_entry_uniform(threadIdx.x);
+    __syncthreads();
+    for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
+        const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
+        const unsigned word = v % (2 * kStreamLutCopies / 4) < kStreamLutCopies / 4 ? e.x : e.y;
+        reinterpret_cast<v4u *>(lut)[v] = v4u{word, word, word, word};
+    }
+    if (former) {
+        Nf4Block<1, 1, HALF> blk;
+        nf4_reg_halves(rx, blk);
+        if (row_read) {
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+                frag[(4 * wave + ks) * 64 + lane] = blk.af[ks];
+        }
+        if (j == 0) {
+            xfs[(2 * q) * G + wave] = blk.xf[0];
+            xfs[(2 * q + 1) * G + wave] = blk.xf[1];
+        }
+    }
+    if (lane < uint32_t(SLANES))
+        scale_lds[wave * SLANES + lane] = sv;
+    __syncthreads();
+
+    // 5. The tile's products.
+    const ST *scl = reinterpret_cast<const ST *>(scale_lds + wave * SLANES) + j;
+    struct Step {
+        v8h af;
+        v4u hi, lo;
+    };
+    const v8h *ap = frag + 16 * q + (row_read ? j : j % rp);
+    // Byte 0 of the cell address: the lane's copy.
+    const unsigned copy_byte = 4 * (lane % kStreamLutCopies);
+    const char *cells = reinterpret_cast<const char *>(lut);
+    auto read_step = [&](int s, Step &st) {
+        st.af = ap[s * 64];
+        const unsigned word = w[s / 4][s % 4];
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+            // (code byte p) * 256 + copy_byte.
+            const unsigned at = __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + p) << 8));
+            const unsigned *cell = reinterpret_cast<const unsigned *>(cells + at);
+            st.hi[p] = cell[0];
+            st.lo[p] = cell[kStreamLutCopies];
+        }
+    };
+    float accf[2] = {0.0f, 0.0f};
+    Step cur, next;
+    read_step(0, cur);
+    v4f acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+        if (s % 4 == 0 && s / 4 + AHEAD < G)
+            w[s / 4 + AHEAD] = __builtin_nontemporal_load(&wp[(s / 4 + AHEAD) * 64]);
+        if (s + 1 < KS)
+            read_step(s + 1, next);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.af, __builtin_bit_cast(v8h, cur.hi), acc,
+                                                     0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(cur.af, __builtin_bit_cast(v8h, cur.lo), acc,
+                                                     0, 0, 0);
+        if (s % 4 == 3) {
+            // Rows 4q + {0,1} are batch 2q (hi, lo), rows 4q + {2,3} batch 2q+1.
+            const int g = s / 4;
+            const float sc = to_f32<HALF>(scl[g * 16]);
+            accf[0] += (acc.x + acc.y) * (sc * xfs[(2 * q) * G + g]);
+            accf[1] += (acc.z + acc.w) * (sc * xfs[(2 * q + 1) * G + g]);
+            // Keep the accumulation here (see stream_ternary_kernel).
+            asm volatile("" : "+v"(accf[0]), "+v"(accf[1]));
+            acc = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+        cur = next;
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    const uint32_t row = tile_id * 16 + j;
+#pragma unroll
+    for (int f = 0; f < 2; ++f) {
+        const uint32_t b = 2 * q + f;
+        if (tile_id < a.n_tiles && b < a.m && row < a.n)
+            a.out[size_t(b) * a.n + row] = accf[f];
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -2145,11 +2358,48 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     }
 }
 
+template <int G>
+void launch_stream_nf4(hipStream_t stream, const StreamArgs &args, bool half)
+{
+    const unsigned blocks = (args.n_tiles + kStreamWaves - 1) / kStreamWaves;
+    if (half)
+        stream_nf4_kernel<G, true><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
+    else
+        stream_nf4_kernel<G, false><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
+}
+
+// As try_stream_ternary: K of 8 or 16 groups (one prologue group per wave).
+bool try_stream_nf4(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
+{
+    const uint32_t groups = pad_to(call.k, 128) / 128;
+    if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
+        call.epilogue != Epilogue::Single || call.m == 0 || call.m > 8 ||
+        n_tiles < kStreamMinTiles || (groups != 8 && groups != 16) ||
+        reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
+        return false;
+    StreamArgs args{};
+    args.x = call.x;
+    args.tiles = call.a.tiles;
+    args.scales = call.a.tiled_scales;
+    args.out = call.out_a;
+    args.m = call.m;
+    args.n = call.n;
+    args.k = call.k;
+    args.n_tiles = n_tiles;
+    if (groups == 8)
+        launch_stream_nf4<8>(stream, args, call.a.tiled_half);
+    else
+        launch_stream_nf4<16>(stream, args, call.a.tiled_half);
+    return true;
+}
+
 void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
 {
     const uint32_t k_pad = pad_to(call.k, 128);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
+    if (try_stream_nf4(stream, call, n_tiles))
+        return;
     Scratch sc = carve(scratch, k_pad);
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const uint32_t ksteps = k_pad / 32;

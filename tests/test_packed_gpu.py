@@ -170,6 +170,22 @@ def test_lm_head_shape(backend, path, scheme, m):
     assert_close(got, want, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("n,k", [(16384, 1024), (16421, 1024), (16421, 2048)])
+def test_wide_matrix_shapes(backend, path, scheme, m, n, k):
+    """At least 1024 row tiles at K = 1024 and 2048 (the streaming wide-matrix
+    kernels), with a row count that leaves the last tile partial and the
+    last block short of tiles."""
+    say("wide", scheme, path, m, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0007 + n + k)
+    x = convert.normal((m, k), 0xAC70011 + m)
+    got = run_linear(backend, x, codes, scales)
+    want = cached_oracle(("wide", scheme, m, n, k), x, codes, scales)
+    assert max_rel_err(got, want) <= 1e-3
+    assert_close(got, want, 1e-4, 1e-4)
+
+
 # The prefill GEMM configuration: M in {512, 2048} tokens against 8192 x 2048
 # and 2048 x 8192 weights.  M = 512 is checked on every row; M = 2048 on a
 # seeded subset of rows (all N columns), the oracle being a scalar CPU path.
