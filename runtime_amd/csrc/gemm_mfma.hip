@@ -4,16 +4,18 @@
 // the reference's group-then-scale order (kernels-simd/src/lib.rs:54,205).
 //
 // Exactness plan.
-// - The activation prologue (split_kernel) scales every (row, 128-group) by
-//   2^-e so its largest magnitude is below 1, and splits each value as
-//   x = hi + lo with both halves binary16 (22 significant bits).
+// - The activation prologue (split_kernel) scales every row by 2^-e so its
+//   largest magnitude is below 1, and splits each value as x = hi + lo with
+//   both halves binary16 (22 significant bits; values below 2^-14 of the
+//   row's largest keep an absolute error under 2^-24 of it).
 // - Weight levels are exact in binary16 for ternary (-1, 0, 1, 2) and INT8
 //   (-127..127).  NF4 levels are split the same way as the activations.
 // - v_mfma_f32_16x16x32_f16 forms the products exactly in f32 and
 //   accumulates each 128-group separately.
-// - The group epilogue adds group_sum * (2^e * scale) in f32.  2^e is a
-//   power of two, so this equals the reference's scale * dot.  NF4 drops
-//   the lo * lo product, which is below 2^-22 of each term.
+// - The group epilogue adds group_sum * scale in f32 (one FMA), and the
+//   store multiplies by the row's 2^e, a power of two, so the result equals
+//   the reference's sum of scale * dot.  NF4 drops the lo * lo product,
+//   which is below 2^-22 of each term.
 //
 // Operands.  B (the weights) is read straight from the decode GEMV's
 // repacked tiles: 16 rows x K per tile, one 16-byte load per lane covering
@@ -82,55 +84,60 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-// One wave per (128-group, row), kSplitWaves groups of a row per block:
-// factor[m, g] = 2^e (NaN for a group with a non-finite value) and the
-// binary16 halves of x * 2^-e.
-constexpr int kSplitWaves = 4;
+// One block per row: factor[m] = 2^e with every |x| of the row below 2^e
+// (NaN for a row with a non-finite value), and the binary16 halves of
+// x * 2^-e.  K is a multiple of 128.
+constexpr int kSplitThreads = 256;
 
-__global__ __launch_bounds__(64 * kSplitWaves) void split_kernel(const float *__restrict__ x,
-                                                                 uint32_t m, uint32_t k,
-                                                                 _Float16 *__restrict__ xh,
-                                                                 _Float16 *__restrict__ xl,
-                                                                 float *__restrict__ factor)
+__global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__restrict__ x,
+                                                              uint32_t k,
+                                                              _Float16 *__restrict__ xh,
+                                                              _Float16 *__restrict__ xl,
+                                                              float *__restrict__ factor)
 {
-    const uint32_t g = blockIdx.x * kSplitWaves + (threadIdx.x >> 6), row = blockIdx.y;
-    const uint32_t lane = threadIdx.x & 63;
-    const uint32_t groups = k / 128;
-    if (g >= groups)
-        return;
-    const float *src = x + size_t(row) * k + g * 128;
-    float v[2];
-    bool bad = false;
+    __shared__ float wave_mx[kSplitThreads / 64];
+    const uint32_t row = blockIdx.x, tid = threadIdx.x;
+    const float4 *src = reinterpret_cast<const float4 *>(x + size_t(row) * k);
+    const uint32_t vecs = k / 4;
+    // A non-finite value makes the row's maximum +inf.
     float mx = 0.0f;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        v[h] = src[h * 64 + lane];
-        if (!isfinite(v[h])) {
-            bad = true;
-            v[h] = 0.0f;
-        }
-        mx = fmaxf(mx, fabsf(v[h]));
+    for (uint32_t i = tid; i < vecs; i += kSplitThreads) {
+        const float4 v = src[i];
+        for (float c : {v.x, v.y, v.z, v.w})
+            mx = fmaxf(mx, isfinite(c) ? fabsf(c) : __builtin_inff());
     }
-    bad = __any(bad);
     mx = wave_max(mx);
+    if ((tid & 63) == 0)
+        wave_mx[tid >> 6] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(wave_mx[0], wave_mx[1]), fmaxf(wave_mx[2], wave_mx[3]));
+    const bool bad = !isfinite(mx);
     int e = 0;
-    if (mx > 0.0f)
+    if (!bad && mx > 0.0f)
         frexpf(mx, &e);  // |x| < 2^e
-    if (lane == 0)
-        factor[size_t(row) * groups + g] = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const float s = ldexpf(v[h], -e);
-        const _Float16 hi = _Float16(s);
-        const size_t o = size_t(row) * k + g * 128 + h * 64 + lane;
-        xh[o] = hi;
-        xl[o] = _Float16(s - float(hi));
+    if (tid == 0)
+        factor[row] = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+    typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+    h4 *dh = reinterpret_cast<h4 *>(xh + size_t(row) * k);
+    h4 *dl = reinterpret_cast<h4 *>(xl + size_t(row) * k);
+    for (uint32_t i = tid; i < vecs; i += kSplitThreads) {
+        const float4 v = src[i];
+        h4 hi, lo;
+        int t = 0;
+        for (float c : {v.x, v.y, v.z, v.w}) {
+            const float sv = bad ? 0.0f : ldexpf(c, -e);
+            hi[t] = _Float16(sv);
+            lo[t] = _Float16(sv - float(hi[t]));
+            ++t;
+        }
+        dh[i] = hi;
+        dl[i] = lo;
     }
 }
 
 struct GemmArgs {
     const _Float16 *xh, *xl;
-    const float *factor;       // [m, k / 128]
+    const float *factor;       // [m]: 2^e of each row
     const uint8_t *wtiles[2];  // repacked codes per stream
     const void *scales[2];     // tiled scales per stream: [tile][groups_pad][16]
     float *out[2];
@@ -206,7 +213,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     constexpr int BNS = kBN / S;                 // block columns per stream
     constexpr int SPC = Chunk<F>::stages;
     __shared__ _Float16 As[2][2][kBM][kRow];  // [stage][hi, lo][row][k]
-    __shared__ float fac[2][kBM];                // 2^e per row, by group parity
     __shared__ uint2 lut[F == Format::Nf4 ? 256 : 1];
 
     if constexpr (F == Format::Nf4) {
@@ -234,7 +240,6 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave >> 1, wn = wave & 1;
     const int li = lane & 15, lq = lane >> 4;
-    const uint32_t groups = g.k / 128;
     const uint32_t chunk_stages = g.k / kBK / g.chunks;
     const uint32_t s_begin = chunk * chunk_stages, s_end = s_begin + chunk_stages;
 
@@ -298,16 +303,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
             total[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
 
-    // Group constants, loaded when the group starts and used at its end (so
-    // the in-order load counter never makes an early instruction wait for
-    // them): each lane's weight scales, kept in their stored form, and the
-    // block's 2^e per activation row (threads < kBM), which reach LDS at the
-    // end of the group's first stage, a barrier before they are read.
+    // Each lane's weight scales of a group, kept in their stored form:
+    // loaded when the group starts and used at its end, so the in-order load
+    // counter never makes an early instruction wait for them.
     typename std::conditional<HALF, unsigned short, float>::type gsc_raw[kTJ];
-    float fac_raw = 0.0f;
-    const uint32_t fac_row = m0 + (tid & (kBM - 1)) < g.m ? m0 + (tid & (kBM - 1)) : 0;
     auto load_group_constants = [&](uint32_t grp) {
-        fac_raw = g.factor[size_t(fac_row) * groups + grp];
 #pragma unroll
         for (int jt = 0; jt < kTJ; ++jt) {
             if constexpr (HALF)
@@ -324,13 +324,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     store_a(0, next);
     __syncthreads();
 
-    for (uint32_t s = s_begin; s < s_end; ++s) {
+    // One 64-wide stage; a group is two stages.  With the group unrolled the
+    // first MFMA of each tile starts from zero instead of a cleared
+    // accumulator; INT8, whose tile load refills every stage, keeps one stage
+    // per iteration (unrolled it spills) and clears after the epilogue.
+    constexpr bool UNROLL = F != Format::Int8;
+    auto stage = [&](uint32_t s, auto first_tag) {
+        const bool FIRST = first_tag;
         const int buf = (s - s_begin) & 1;
         // The last stage re-fetches itself and stores to the idle buffer:
         // with no conditional fetch, no path leaves a load pending at the
         // loop's back edge.
         fetch_a(s + 1 < s_end ? s + 1 : s, next);
-        if (s % 2 == 0 && s != s_begin)
+        if (FIRST && s != s_begin)
             load_group_constants(s / 2);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -366,8 +372,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                 const v8h al = *reinterpret_cast<const v8h *>(&As[buf][1][row][koff]);
 #pragma unroll
                 for (int jt = 0; jt < kTJ; ++jt) {
-                    v4f c = acc[i][jt];
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[jt], c, 0, 0, 0);
+                    v4f c;
+                    if (UNROLL && FIRST && h == 0)
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[jt], v4f{}, 0, 0, 0);
+                    else
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[jt], acc[i][jt], 0, 0,
+                                                                   0);
                     c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[jt], c, 0, 0, 0);
                     if constexpr (P == 2)
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[jt], c, 0, 0, 0);
@@ -375,8 +385,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                 }
             }
         }
-        if (s % 2 == 1) {
-            // Group epilogue: total += group_sum * (2^e[m] * scale[n]).
+        if (!FIRST) {
+            // Group epilogue: total += group_sum * scale[n].
             float gsc[kTJ];
 #pragma unroll
             for (int jt = 0; jt < kTJ; ++jt) {
@@ -386,24 +396,39 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                     gsc[jt] = gsc_raw[jt];
             }
 #pragma unroll
-            for (int i = 0; i < kTI; ++i) {
-                const v4f gfx =
-                    *reinterpret_cast<const v4f *>(&fac[(s / 2) & 1][wm * 64 + i * 16 + lq * 4]);
+            for (int i = 0; i < kTI; ++i)
 #pragma unroll
-                for (int jt = 0; jt < kTJ; ++jt) {
+                for (int jt = 0; jt < kTJ; ++jt)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r)
-                        total[i][jt][r] += acc[i][jt][r] * (gfx[r] * gsc[jt]);
-                    acc[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                }
-            }
+                    for (int r = 0; r < 4; ++r) {
+                        total[i][jt][r] = fmaf(acc[i][jt][r], gsc[jt], total[i][jt][r]);
+                        if (!UNROLL)
+                            acc[i][jt][r] = 0.0f;
+                    }
         }
         store_a(buf ^ 1, next);
-        if (s % 2 == 0 && tid < kBM)
-            fac[(s / 2) & 1][tid] = fac_raw;
         __syncthreads();
+    };
+    // Chunks are whole groups, so every run starts on a group's first stage.
+    if constexpr (UNROLL) {
+        for (uint32_t s = s_begin; s < s_end; s += 2) {
+            stage(s, std::true_type{});
+            stage(s + 1, std::false_type{});
+        }
+    } else {
+        for (uint32_t s = s_begin; s < s_end; ++s)
+            stage(s, (s - s_begin) % 2 == 0);
     }
 
+    // The rows' 2^e (rows past m read row 0; they are never stored).
+    float rowf[kTI][4];
+#pragma unroll
+    for (int i = 0; i < kTI; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const uint32_t mm = m0 + wm * 64 + i * 16 + lq * 4 + r;
+            rowf[i][r] = g.factor[mm < g.m ? mm : 0];
+        }
 #pragma unroll
     for (int i = 0; i < kTI; ++i)
 #pragma unroll
@@ -417,22 +442,24 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                 if (nn >= g.n)
                     continue;
                 const size_t o = size_t(mm) * g.n + nn;
+                const float rf = rowf[i][r];
                 if (g.chunks > 1) {
-                    // Raw sums per chunk; splitk_reduce_kernel finishes them.
+                    // Chunk sums; splitk_reduce_kernel finishes them.
                     const size_t plane = size_t(g.m) * g.n;
 #pragma unroll
                     for (int st = 0; st < S; ++st)
                         g.partial[(size_t(chunk) * S + st) * plane + o] =
-                            total[i][st * TJS + tt][r];
+                            total[i][st * TJS + tt][r] * rf;
                     continue;
                 }
                 if constexpr (E == Epilogue::Single) {
-                    g.out[0][o] = total[i][tt][r];
+                    g.out[0][o] = total[i][tt][r] * rf;
                 } else if constexpr (E == Epilogue::Pair) {
-                    g.out[0][o] = total[i][tt][r];
-                    g.out[1][o] = total[i][(S - 1) * TJS + tt][r];
+                    g.out[0][o] = total[i][tt][r] * rf;
+                    g.out[1][o] = total[i][(S - 1) * TJS + tt][r] * rf;
                 } else {
-                    g.out[0][o] = silu_mul(total[i][tt][r], total[i][(S - 1) * TJS + tt][r]);
+                    g.out[0][o] = silu_mul(total[i][tt][r] * rf,
+                                           total[i][(S - 1) * TJS + tt][r] * rf);
                 }
             }
         }
@@ -520,8 +547,8 @@ size_t gemm_mfma_scratch_bytes(const PackedCall &call)
     const uint32_t chunks = split_chunks(tiles_of(call, &tiles_n), call.k / 128);
     const int S = call.epilogue == Epilogue::Single ? 1 : 2;
     const size_t partial = chunks > 1 ? size_t(chunks) * S * call.m * call.n * sizeof(float) : 0;
-    return size_t(call.m) * call.k * 2 * sizeof(_Float16) +
-           size_t(call.m) * (call.k / 128) * sizeof(float) + partial;
+    return size_t(call.m) * call.k * 2 * sizeof(_Float16) + size_t(call.m) * sizeof(float) +
+           partial;
 }
 
 void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
@@ -531,8 +558,7 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     _Float16 *xh = reinterpret_cast<_Float16 *>(p);
     _Float16 *xl = xh + size_t(call.m) * call.k;
     float *factor = reinterpret_cast<float *>(xl + size_t(call.m) * call.k);
-    split_kernel<<<dim3((groups + kSplitWaves - 1) / kSplitWaves, call.m), 64 * kSplitWaves, 0,
-                   stream>>>(call.x, call.m, call.k, xh, xl, factor);
+    split_kernel<<<call.m, kSplitThreads, 0, stream>>>(call.x, call.k, xh, xl, factor);
     // The repacked tiles pad K to 256 (ternary) or 128; one 16-byte lane load
     // covers 64 (INT8), 128 (NF4) or 256 (ternary) k.
     const uint32_t align = call.format == Format::Ternary ? 256 : 128;
@@ -557,7 +583,7 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     args.groups_pad = k_pad / 128;
     args.tiles = tiles_of(call, &args.tiles_n);
     args.chunks = split_chunks(args.tiles, groups);
-    args.partial = factor + size_t(call.m) * groups;
+    args.partial = factor + call.m;
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     switch (call.format) {
