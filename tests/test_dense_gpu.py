@@ -347,6 +347,22 @@ def test_argmax_wide_rows_ties_and_poison(backend):
     assert bits_equal(got, oracle.argmax(x))
 
 
+def test_argmax_wider_than_64_ranges(backend):
+    # Past 64 ranges of 2048 (131072 entries) the range winners no longer fit
+    # one lane each of the final wave.
+    width = 140000
+    x = np.random.default_rng(0xA86).integers(-50, 50, size=(4, width)).astype(np.float32)
+    x[0, 1000] = x[0, 139000] = 99.0   # tie across the first and the last range
+    x[1, 135000] = np.nan              # poison past 131072
+    x[2, 131072] = 100.0               # the unique maximum, first entry past 64 ranges
+    x[3, :] = 7.0                      # all equal: index 0
+    out = backend.allocate_f32((4,))
+    backend.argmax(out, up(backend, x))
+    got = backend.read(out)
+    assert got[0] == 1000 and np.isnan(got[1]) and got[2] == 131072 and got[3] == 0
+    assert bits_equal(got, oracle.argmax(x))
+
+
 @pytest.mark.parametrize("width", [1, 64, 130, 65536])
 def test_argmax_masked(backend, width):
     say("argmax_masked", width)
