@@ -1221,6 +1221,8 @@ constexpr int kStreamNf4Ahead = 2;
 // Widest grids only: below this many tiles the K-split plans keep more
 // waves busy.
 constexpr uint32_t kStreamMinTiles = 1024;
+// Fewest blocks a streaming launch spreads its tiles over.
+constexpr uint32_t kStreamMinBlocks = 256;
 
 struct StreamArgs {
     const float *x;  // [m, k] plain activations, 16-byte aligned
@@ -1238,14 +1240,16 @@ struct StreamRecord {
     float pad;
 };
 
-template <int NF, int KL, bool HALF>
-__global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(StreamArgs a)
+template <int NF, int KL, bool HALF, int W>
+__global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
 {
     using ST = typename ScaleT<HALF>::type;
     using B = I8Block<Format::Ternary, 1, 1, NF, HALF>;
     constexpr int G = 2 * KL;   // 128-groups of K (the tile width is 256 * KL)
     constexpr int KS = 4 * KL;  // 64-wide ksteps
-    static_assert(NF * KL <= kStreamWaves, "one prologue K block per wave");
+    // Prologue units (fragment, 256-k block), wave w taking w, w + W, ...
+    constexpr int UNITS = NF * KL;
+    constexpr int PER = (UNITS + W - 1) / W;
     // Scale block of a tile: G * 16 values, one SV vector per lane for the
     // first SLANES lanes.
     typedef typename std::conditional<HALF, uint2, v4u>::type SV;
@@ -1254,10 +1258,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(Strea
     // records [slot][group], each wave's scale block.
     __shared__ v4i frag[KS * NF * 64];
     __shared__ StreamRecord rec[4 * NF * G];
-    __shared__ SV scale_lds[kStreamWaves * SLANES];
+    __shared__ SV scale_lds[W * SLANES];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t tile_id = blockIdx.x * kStreamWaves + wave;
+    const uint32_t tile_id = blockIdx.x * W + wave;
     const uint32_t tile = tile_id < a.n_tiles ? tile_id : a.n_tiles - 1;
 
     // 1. The tile's scale block.
@@ -1265,15 +1269,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(Strea
     if (lane < uint32_t(SLANES))
         sv = reinterpret_cast<const SV *>(a.scales)[size_t(tile) * SLANES + lane];
     __builtin_amdgcn_sched_barrier(0);
-    // 2. The activations of this wave's prologue block (fragment pf, K block
+    // 2. The activations of this wave's prologue units (fragment pf, K block
     // pu): lane 16q + 4b + p holds x[4 pf + b][256 pu + 64 kk + 16q + 4p + t].
-    const bool former = wave < uint32_t(NF * KL);
-    const uint32_t pf = wave / KL, pu = wave % KL;
-    const uint32_t pb = 4 * pf + ((lane >> 2) & 3);
-    const bool row_live = former && pb < a.m;
-    RegX<4> rx;
-    reg_load_issued(rx, a.x + size_t(row_live ? pb : 0) * a.k, row_live, a.k, pu,
-                    16 * (lane >> 4) + 4 * (lane & 3), 64);
+    RegX<4> rx[PER];
+#pragma unroll
+    for (int pi = 0; pi < PER; ++pi) {
+        const uint32_t u = wave + W * pi;
+        const bool former = u < uint32_t(UNITS);
+        const uint32_t pf = u / KL, pu = u % KL;
+        const uint32_t pb = 4 * pf + ((lane >> 2) & 3);
+        const bool row_live = former && pb < a.m;
+        reg_load_issued(rx[pi], a.x + size_t(row_live ? pb : 0) * a.k, row_live, a.k, pu,
+                        16 * (lane >> 4) + 4 * (lane & 3), 64);
+    }
     __builtin_amdgcn_sched_barrier(0);
     // 3. The first kStreamTernaryAhead weight loads of the tile; the load
     // of K block l + kStreamTernaryAhead leaves when block l's products
@@ -1288,13 +1296,18 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_ternary_kernel(Strea
         w[l] = __builtin_nontemporal_load(&wp[l * 64]);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 4. The prologue block's fragments and records, then the scale block,
+    // 4. The prologue units' fragments and records, then the scale block,
     // into LDS.
-    if (former) {
+#pragma unroll
+    for (int pi = 0; pi < PER; ++pi) {
+        const uint32_t u = wave + W * pi;
+        if (u >= uint32_t(UNITS))
+            continue;
+        const uint32_t pf = u / KL, pu = u % KL;
         B blk;
         auto emit = [&](auto f_tag) {
             constexpr int F = decltype(f_tag)::value;
-            reg_digits(rx, blk, F);
+            reg_digits(rx[pi], blk, F);
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks)
                 frag[((4 * pu + ks) * NF + F) * 64 + lane] = blk.af[ks][F];
@@ -2171,11 +2184,28 @@ void set_segments(MfmaArgs &args, const PackedCall &call)
 template <int NF, int KL>
 void launch_stream_ternary(hipStream_t stream, const StreamArgs &args, bool half)
 {
-    const unsigned blocks = (args.n_tiles + kStreamWaves - 1) / kStreamWaves;
-    if (half)
-        stream_ternary_kernel<NF, KL, true><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
+    // Waves per block: the most that still leave at least kStreamMinBlocks
+    // blocks (one tile each wave), so small grids spread over the CUs.
+    auto go = [&](auto w_tag) {
+        constexpr int W = decltype(w_tag)::value;
+        const unsigned blocks = (args.n_tiles + W - 1) / W;
+        if (half)
+            stream_ternary_kernel<NF, KL, true, W><<<blocks, 64 * W, 0, stream>>>(args);
+        else
+            stream_ternary_kernel<NF, KL, false, W><<<blocks, 64 * W, 0, stream>>>(args);
+    };
+    // (n_tiles >= kStreamMinTiles = 4 * kStreamMinBlocks.)  Measured at
+    // 16384 x 1024, one row: 16 waves per block 5.3 us, 4 waves 4.6-4.8 us.
+    // Smaller matrices stay on the K-split kernels: streamed with 1-4 waves
+    // per block they measured slower (8192 x 2048 5.5-8.1 against 5.8 us,
+    // 2048 x 2048 8.0-12.5 against 4.3 us).
+    static_assert(kStreamMinTiles >= 4 * kStreamMinBlocks, "at least four waves per block");
+    if (args.n_tiles >= 16 * kStreamMinBlocks)
+        go(std::integral_constant<int, 16>{});
+    else if (args.n_tiles >= 8 * kStreamMinBlocks)
+        go(std::integral_constant<int, 8>{});
     else
-        stream_ternary_kernel<NF, KL, false><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
+        go(std::integral_constant<int, 4>{});
 }
 
 // Serves the call with the streaming kernel when it applies; false leaves
@@ -2368,13 +2398,14 @@ void launch_stream_nf4(hipStream_t stream, const StreamArgs &args, bool half)
         stream_nf4_kernel<G, false><<<blocks, 64 * kStreamWaves, 0, stream>>>(args);
 }
 
-// As try_stream_ternary: K of 8 or 16 groups (one prologue group per wave).
+// As try_stream_ternary: K of 8 or 16 groups (one prologue group per wave),
+// and grids of at least kStreamMinBlocks full 16-wave blocks.
 bool try_stream_nf4(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 {
     const uint32_t groups = pad_to(call.k, 128) / 128;
     if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > 8 ||
-        n_tiles < kStreamMinTiles || (groups != 8 && groups != 16) ||
+        n_tiles < kStreamWaves * kStreamMinBlocks || (groups != 8 && groups != 16) ||
         reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
         return false;
     StreamArgs args{};
