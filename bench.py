@@ -172,16 +172,19 @@ GEMM_SHAPES = [(8192, 2048), (2048, 8192)]
 F16_MFMA_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 # MFMA products issued per algorithmic product: activations as binary16
-# hi + lo, NF4 levels as hi + lo without the lo * lo term.
+# hi + lo, NF4 levels as hi + lo without the lo * lo term; with the opt-in
+# single-half activations (mfh_set_gemm_activations(1)) one fewer.
 MFMA_PASSES = {"ternary": 2, "int8": 2, "nf4": 3}
+MFMA_PASSES_SINGLE = {"ternary": 1, "int8": 1, "nf4": 2}
 
 
 def prefill_gemm(backend, reps: int = 5) -> dict:
     """Packed GEMM at M in {512, 2048} x {8192x2048, 2048x8192} x 3 formats
-    on the matrix-core kernel and on the FP32-FMA kernel (seeded N(0, 0.02)
-    weights, N(0, 1) activations).  Reports algorithmic TFLOP/s (2*M*N*K),
-    its fraction of the dense f16 MFMA peak, and the fraction counting the
-    MFMA products actually issued (hi/lo passes)."""
+    on the matrix-core kernel (exact hi + lo activations, the default, and
+    the opt-in single-half activations) and on the FP32-FMA kernel (seeded
+    N(0, 0.02) weights, N(0, 1) activations).  Reports algorithmic TFLOP/s
+    (2*M*N*K), its fraction of the dense f16 MFMA peak, and the fraction
+    counting the MFMA products actually issued (hi/lo passes)."""
     from runtime_amd import convert, hiptime
     from runtime_amd.backend import WEIGHT
 
@@ -197,8 +200,9 @@ def prefill_gemm(backend, reps: int = 5) -> dict:
                 xb = backend.upload_f32((m, k), convert.normal((m, k), 0xAC70101 + m))
                 out = backend.allocate_f32((m, n))
                 row = {}
-                for label, path in (("mfma", 0), ("fma", 1)):
+                for label, path, mode in (("mfma", 0, 0), ("mfma_single", 0, 1), ("fma", 1, 0)):
                     previous = backend.set_kernel_path(path)
+                    previous_mode = backend.set_gemm_activations(mode)
                     backend.packed_linear(out, xb, cb, sb)
                     backend.synchronize()
                     e0, e1 = hiptime.Event(), hiptime.Event()
@@ -208,11 +212,15 @@ def prefill_gemm(backend, reps: int = 5) -> dict:
                     e1.record(stream)
                     e1.synchronize()
                     backend.set_kernel_path(previous)
+                    backend.set_gemm_activations(previous_mode)
                     us = e1.elapsed_ms(e0) / reps * 1e3
                     row[label + "_us"] = round(us, 1)
                     row[label + "_TFLOPs"] = round(2 * m * n * k / (us / 1e6) / 1e12, 1)
                 row["mfma_util"] = round(row["mfma_TFLOPs"] / F16_MFMA_PEAK_TFLOPS, 4)
                 row["mfma_issued_util"] = round(row["mfma_util"] * MFMA_PASSES[fmt], 4)
+                row["mfma_single_util"] = round(row["mfma_single_TFLOPs"] / F16_MFMA_PEAK_TFLOPS, 4)
+                row["mfma_single_issued_util"] = round(
+                    row["mfma_single_util"] * MFMA_PASSES_SINGLE[fmt], 4)
                 row["fma_util"] = round(row["fma_TFLOPs"] / FP32_PEAK_TFLOPS, 4)
                 cases[f"{fmt}:M{m}:{n}x{k}"] = row
     best = max(cases.items(), key=lambda kv: kv[1]["mfma_TFLOPs"])

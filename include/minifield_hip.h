@@ -376,6 +376,13 @@ void *mfh_stream(const mfh_ctx *ctx);
  * one-token pass issued op by op through these entry points instead of the
  * fused decode step.  Returns the previous setting. */
 int mfh_set_kernel_path(mfh_ctx *ctx, int path);
+/* Activation precision of the matrix-core prefill GEMM (m > 8): 0 (the
+ * default) = each activation as binary16 hi + lo halves, two MFMAs per
+ * product (three for NF4), 22 significant bits; 1 = one binary16 half, one
+ * MFMA per product (two for NF4), each activation within 2^-12 of itself.
+ * Weights, scales and the group epilogue are the same in both.  Any other
+ * value selects 0.  Returns the previous setting (-1 for a null context). */
+int mfh_set_gemm_activations(mfh_ctx *ctx, int mode);
 
 #ifdef __cplusplus
 }

@@ -153,6 +153,7 @@ SIGNATURES = {
     # diagnostics
     "mfh_stream": (P, [P]),
     "mfh_set_kernel_path": (ctypes.c_int, [P, ctypes.c_int]),
+    "mfh_set_gemm_activations": (ctypes.c_int, [P, ctypes.c_int]),
     # converters
     "mfc_quantize": (ctypes.c_int, [c_float_p, SZ, SZ, ctypes.c_int, c_u8_p, c_u16_p,
                                     ctypes.c_uint]),

@@ -214,6 +214,10 @@ class HipBackend:
         """0 automatic, 1 FP32 FMA kernels only, 2 matrix-core kernels only."""
         return _ffi.lib().mfh_set_kernel_path(self._ctx, path)
 
+    def set_gemm_activations(self, mode: int) -> int:
+        """Prefill GEMM activations: 0 binary16 hi + lo (default), 1 one half."""
+        return _ffi.lib().mfh_set_gemm_activations(self._ctx, mode)
+
     def stream(self) -> int:
         return _ffi.lib().mfh_stream(self._ctx)
 

@@ -16,6 +16,10 @@
 //   store multiplies by the row's 2^e, a power of two, so the result equals
 //   the reference's sum of scale * dot.  NF4 drops the lo * lo product,
 //   which is below 2^-22 of each term.
+// - Single-half mode (opt-in, mfh_set_gemm_activations): the activations
+//   keep only the hi half, one MFMA per product (NF4: two), each activation
+//   within 2^-12 of itself relative (2^-25 of the row's largest absolute
+//   below 2^-14 of it); weights and the epilogue are unchanged.
 //
 // Operands.  B (the weights) is read straight from the decode GEMV's
 // repacked tiles: 16 rows x K per tile, one 16-byte load per lane covering
@@ -86,7 +90,8 @@ __device__ __forceinline__ float wave_max(float v)
 
 // One block per row: factor[m] = 2^e with every |x| of the row below 2^e
 // (NaN for a row with a non-finite value), and the binary16 halves of
-// x * 2^-e.  K is a multiple of 128.
+// x * 2^-e (the lo half only where `xl` is non-null).  K is a multiple of
+// 128.
 constexpr int kSplitThreads = 256;
 
 __global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__restrict__ x,
@@ -131,7 +136,8 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__res
             ++t;
         }
         dh[i] = hi;
-        dl[i] = lo;
+        if (xl)
+            dl[i] = lo;
     }
 }
 
@@ -205,14 +211,15 @@ __device__ __forceinline__ v8h decode_ternary(unsigned w, int h)
     return out;
 }
 
-template <Format F, int S, Epilogue E, bool HALF>
+template <Format F, int S, Epilogue E, bool HALF, bool LO>
 __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
 {
     constexpr int P = F == Format::Nf4 ? 2 : 1;  // weight level planes
+    constexpr int PA = LO ? 2 : 1;               // activation planes (hi, lo)
     constexpr int TJS = kTJ / S;                 // column tiles per stream per wave
     constexpr int BNS = kBN / S;                 // block columns per stream
     constexpr int SPC = Chunk<F>::stages;
-    __shared__ _Float16 As[2][2][kBM][kRow];  // [stage][hi, lo][row][k]
+    __shared__ _Float16 As[2][PA][kBM][kRow];  // [stage][hi, lo][row][k]
     __shared__ uint2 lut[F == Format::Nf4 ? 256 : 1];
 
     if constexpr (F == Format::Nf4) {
@@ -251,18 +258,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     const _Float16 *a_src[2] = {g.xh + size_t(a_live ? m0 + a_row : 0) * g.k + a_k,
                                 g.xl + size_t(a_live ? m0 + a_row : 0) * g.k + a_k};
     struct ARaw {
-        v8h v[2][4];
+        v8h v[PA][4];
     };
     auto fetch_a = [&](uint32_t s, ARaw &r) {
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < PA; ++p)
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 r.v[p][u] = *reinterpret_cast<const v8h *>(a_src[p] + s * kBK + 8 * u);
     };
     auto store_a = [&](int buf, const ARaw &r) {
 #pragma unroll
-        for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < PA; ++p)
 #pragma unroll
             for (int u = 0; u < 4; ++u)
                 *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k + 8 * u]) = r.v[p][u];
@@ -369,7 +376,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
             for (int i = 0; i < kTI; ++i) {
                 const int row = wm * 64 + i * 16 + li;
                 const v8h ah = *reinterpret_cast<const v8h *>(&As[buf][0][row][koff]);
-                const v8h al = *reinterpret_cast<const v8h *>(&As[buf][1][row][koff]);
+                const v8h al = *reinterpret_cast<const v8h *>(&As[buf][PA - 1][row][koff]);
 #pragma unroll
                 for (int jt = 0; jt < kTJ; ++jt) {
                     v4f c;
@@ -378,7 +385,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                     else
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[jt], acc[i][jt], 0, 0,
                                                                    0);
-                    c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[jt], c, 0, 0, 0);
+                    if constexpr (LO)
+                        c = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh[jt], c, 0, 0, 0);
                     if constexpr (P == 2)
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl[jt], c, 0, 0, 0);
                     acc[i][jt] = c;
@@ -494,13 +502,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(float *__restrict__ 
 }
 
 template <Format F, int S, Epilogue E>
-void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half)
+void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half, bool lo)
 {
     const unsigned grid = args.tiles * args.chunks;
-    if (half)
-        gemm_mfma_kernel<F, S, E, true><<<grid, kThreads, 0, stream>>>(args);
+    if (half && lo)
+        gemm_mfma_kernel<F, S, E, true, true><<<grid, kThreads, 0, stream>>>(args);
+    else if (lo)
+        gemm_mfma_kernel<F, S, E, false, true><<<grid, kThreads, 0, stream>>>(args);
+    else if (half)
+        gemm_mfma_kernel<F, S, E, true, false><<<grid, kThreads, 0, stream>>>(args);
     else
-        gemm_mfma_kernel<F, S, E, false><<<grid, kThreads, 0, stream>>>(args);
+        gemm_mfma_kernel<F, S, E, false, false><<<grid, kThreads, 0, stream>>>(args);
     if (args.chunks > 1) {
         const size_t plane = size_t(args.m) * args.n;
         const unsigned rgrid = unsigned(std::min<size_t>((plane + 255) / 256, 65536));
@@ -512,13 +524,14 @@ void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half)
 template <Format F>
 void launch_format(hipStream_t stream, const PackedCall &call, const GemmArgs &args, bool half)
 {
+    const bool lo = !call.single_half;
     switch (call.epilogue) {
     case Epilogue::Single:
-        return launch_epilogue<F, 1, Epilogue::Single>(stream, args, half);
+        return launch_epilogue<F, 1, Epilogue::Single>(stream, args, half, lo);
     case Epilogue::Pair:
-        return launch_epilogue<F, 2, Epilogue::Pair>(stream, args, half);
+        return launch_epilogue<F, 2, Epilogue::Pair>(stream, args, half, lo);
     case Epilogue::SwigluPair:
-        return launch_epilogue<F, 2, Epilogue::SwigluPair>(stream, args, half);
+        return launch_epilogue<F, 2, Epilogue::SwigluPair>(stream, args, half, lo);
     }
 }
 
@@ -558,7 +571,8 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     _Float16 *xh = reinterpret_cast<_Float16 *>(p);
     _Float16 *xl = xh + size_t(call.m) * call.k;
     float *factor = reinterpret_cast<float *>(xl + size_t(call.m) * call.k);
-    split_kernel<<<call.m, kSplitThreads, 0, stream>>>(call.x, call.k, xh, xl, factor);
+    split_kernel<<<call.m, kSplitThreads, 0, stream>>>(call.x, call.k, xh,
+                                                       call.single_half ? nullptr : xl, factor);
     // The repacked tiles pad K to 256 (ternary) or 128; one 16-byte lane load
     // covers 64 (INT8), 128 (NF4) or 256 (ternary) k.
     const uint32_t align = call.format == Format::Ternary ? 256 : 128;

@@ -78,6 +78,8 @@ struct mfh_ctx {
     bool cancel_requested = false;
     const char *last_error = "no error";
     int kernel_path = 0;
+    // Prefill GEMM activations: 0 = binary16 hi + lo halves, 1 = one half.
+    int gemm_activations = 0;
     int cu_count = 256;
     std::unique_ptr<mfh::Pool> pool;
     // Small device scratch for staged host token ids and per-call partials;

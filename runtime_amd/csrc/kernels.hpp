@@ -56,6 +56,8 @@ struct PackedCall {
     // Matrix-core GEMV: run the activation prologue as its own kernel even
     // where the in-kernel one fits (diagnostics).
     bool separate_prologue = false;
+    // Matrix-core GEMM: activations as one binary16 half instead of hi + lo.
+    bool single_half = false;
     // Matrix-core GEMV only: a transform other than Plain replaces `x`.
     XForm xform;
     // Matrix-core GEMV, Single epilogue only: when non-zero, the launch

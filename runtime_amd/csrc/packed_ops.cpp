@@ -166,6 +166,7 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
         void *scratch = digits_scratch(ctx, gemm_mfma_scratch_bytes(call));
         if (!scratch)
             return allocation_failed(ctx);
+        call.single_half = ctx->gemm_activations == 1;
         launch_gemm_mfma(stream, call, scratch);
     } else {
         launch_gemm_fma(stream, call);

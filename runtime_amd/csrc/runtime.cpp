@@ -927,6 +927,15 @@ int mfh_set_kernel_path(mfh_ctx *ctx, int path)
     return previous;
 }
 
+int mfh_set_gemm_activations(mfh_ctx *ctx, int mode)
+{
+    if (!ctx)
+        return -1;
+    int previous = ctx->gemm_activations;
+    ctx->gemm_activations = mode == 1 ? 1 : 0;
+    return previous;
+}
+
 int mfh_supports_ternary_lut2(const mfh_ctx *ctx)
 {
     (void)ctx;

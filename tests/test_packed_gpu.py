@@ -307,6 +307,72 @@ def test_prefill_gemm_ragged_shapes(backend, path, scheme, m, n, k):
     assert_close(got[~bad], want[~bad], 1e-4, 1e-4)
 
 
+# --- single-half GEMM activations (opt-in) ----------------------------------------
+# mfh_set_gemm_activations(1) keeps one binary16 half of each activation
+# (within 2^-12 of itself; absolute 2^-25 of the row's largest below 2^-14 of
+# it), so each output is pinned by the a-priori bound
+# |d| <= 2^-11 * sum_k |x_k| |w_k| + 1e-6 * max|cpu| (dequantized weights,
+# twice the rounding for the sums' own f32 error) and by the normwise rule
+# max|d| / max|cpu| <= 1e-3; the per-element 1e-4 rule is the exact default's.
+
+@pytest.fixture
+def single_half(backend):
+    previous = backend.set_gemm_activations(1)
+    yield
+    backend.set_gemm_activations(previous)
+
+
+def _single_half_bound(x, codes, scales, scheme, want):
+    w = np.abs(oracle.dequantize_f32(codes, scales, scheme)).astype(np.float64)
+    return 2.0 ** -11 * (np.abs(x).astype(np.float64) @ w.T) + 1e-6 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m,n,k", [(2048, 8192, 2048), (512, 2048, 8192), (130, 200, 640),
+                                   (257, 70, 1152), (33, 1000, 128)])
+def test_prefill_gemm_single_half(backend, single_half, scheme, m, n, k):
+    say("prefill gemm single half", scheme, m, n, k)
+    codes, scales = gemm_weights(n, k, scheme)
+    x = convert.normal((m, k), 0xAC70005 + m)
+    got = run_linear(backend, x, codes, scales)
+    if m <= 512:
+        rows = np.arange(m)
+    else:
+        rng = np.random.default_rng(0x6E45 + n + k)
+        rows = np.unique(np.concatenate([[0, m - 1], rng.choice(m, 62, replace=False)]))
+    want = oracle.packed_linear_threaded(x[rows], codes, scales)
+    assert np.all(np.isfinite(got))
+    assert max_rel_err(got[rows], want) <= 1e-3
+    diff = np.abs(got[rows].astype(np.float64) - want)
+    assert np.all(diff <= _single_half_bound(x[rows], codes, scales, scheme, want))
+    # The mode is in effect: the dropped lo halves show at this size.
+    assert diff.max() > 1e-6 * np.max(np.abs(want))
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_pair_and_swiglu_single_half(backend, single_half, scheme):
+    say("pair/swiglu single half", scheme)
+    m, n, k = 100, 320, 768
+    ca, sa = make_weights(n, k, scheme, 0x5EED0410)
+    cb, sb = make_weights(n, k, scheme, 0x5EED0411)
+    x = convert.normal((m, k), 0xAC70410)
+    ga, gsa = upload_weights(backend, ca, sa)
+    gb, gsb = upload_weights(backend, cb, sb)
+    xb = backend.upload_f32(x.shape, x)
+    out_a = backend.allocate_f32((m, n))
+    out_b = backend.allocate_f32((m, n))
+    backend.packed_linear_pair(out_a, out_b, xb, ga, gsa, gb, gsb)
+    want_a, want_b = oracle.packed_linear_pair(x, ca, sa, cb, sb)
+    for got, want, c, s_ in ((backend.read(out_a), want_a, ca, sa),
+                             (backend.read(out_b), want_b, cb, sb)):
+        assert max_rel_err(got, want) <= 1e-3
+        assert np.all(np.abs(got.astype(np.float64) - want) <=
+                      _single_half_bound(x, c, s_, scheme, want))
+    fused = backend.allocate_f32((m, n))
+    backend.packed_swiglu_pair(fused, xb, ga, gsa, gb, gsb)
+    assert max_rel_err(backend.read(fused), oracle.packed_swiglu_pair(x, ca, sa, cb, sb)) <= 1e-3
+
+
 # --- pair / SwiGLU variants -----------------------------------------------------------
 
 @pytest.mark.parametrize("scheme", SCHEMES)
