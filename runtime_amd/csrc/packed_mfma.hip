@@ -1748,10 +1748,12 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
     static_assert(SLANES <= 64, "one scale vector per lane");
     // Fragments [kstep][lane], group factors [batch slot][group], each
     // wave's scale block, and the code-byte table: 256 B per byte value,
-    // kStreamLutCopies copies of its hi word, then as many of its lo word.
-    // Lane l reads copy l % 32, so every word of a read comes from the bank
-    // of its copy, and a byte's cell address is one byte permute of the code
-    // word.
+    // kStreamLutCopies copies of its (hi, lo) word pair.  Lane l reads copy
+    // l % 32 with one 8-byte load, so the 32 lanes of each half-wave read 256
+    // distinct bytes of banks, and a byte's cell address is one byte permute
+    // of the code word.  (Two 4-byte reads per byte measured half the rate:
+    // 4-byte LDS reads run at about 265 GB/s per CU whatever their pattern,
+    // 8-byte ones at about 515, scattered table reads included.)
     __shared__ v8h frag[KS * 64];
     __shared__ float xfs[8 * G];
     __shared__ SV scale_lds[kStreamWaves * SLANES];
@@ -1799,8 +1801,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
     __syncthreads();
     for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
         const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
-        const unsigned word = v % (2 * kStreamLutCopies / 4) < kStreamLutCopies / 4 ? e.x : e.y;
-        reinterpret_cast<v4u *>(lut)[v] = v4u{word, word, word, word};
+        reinterpret_cast<v4u *>(lut)[v] = v4u{e.x, e.y, e.x, e.y};
     }
     if (former) {
         Nf4Block<1, 1, HALF> blk;
@@ -1827,7 +1828,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
     };
     const v8h *ap = frag + 16 * q + (row_read ? j : j % rp);
     // Byte 0 of the cell address: the lane's copy.
-    const unsigned copy_byte = 4 * (lane % kStreamLutCopies);
+    const unsigned copy_byte = 8 * (lane % kStreamLutCopies);
     const char *cells = reinterpret_cast<const char *>(lut);
     auto read_step = [&](int s, Step &st) {
         st.af = ap[s * 64];
@@ -1836,9 +1837,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
         for (int p = 0; p < 4; ++p) {
             // (code byte p) * 256 + copy_byte.
             const unsigned at = __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + p) << 8));
-            const unsigned *cell = reinterpret_cast<const unsigned *>(cells + at);
-            st.hi[p] = cell[0];
-            st.lo[p] = cell[kStreamLutCopies];
+            const uint2 e = *reinterpret_cast<const uint2 *>(cells + at);
+            st.hi[p] = e.x;
+            st.lo[p] = e.y;
         }
     };
     float accf[2] = {0.0f, 0.0f};
