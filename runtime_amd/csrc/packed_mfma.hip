@@ -53,7 +53,10 @@ typedef unsigned v4u __attribute__((ext_vector_type(4)));
 typedef _Float16 v8h __attribute__((ext_vector_type(8)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 
-__constant__ float kNf4Levels[16] = {
+// NF4 levels (kernels-simd/src/lib.rs:111-131 NF4_LEVELS), as literal constants:
+// table builders index them with compile-time indices only, so building a
+// table needs no memory access.
+constexpr float kNf4LevelValues[16] = {
     -1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f,
     -0.28444138f, -0.18477343f, -0.091050036f, 0.0f,
     0.0795803f,   0.1609302f,   0.2461123f,   0.33791524f,
@@ -1406,10 +1409,21 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
 constexpr uint32_t kLutCopies = 1;
 
 // Table entry for one code byte: x = hi halves of (low nibble, high nibble),
-// y = lo halves, each a packed f16 pair for consecutive k.
+// y = lo halves, each a packed f16 pair for consecutive k.  The levels are
+// literal constants picked by selects, so no memory access delays the
+// table: a per-lane constant-memory load issued after the weight loads
+// would wait for all of them (loads retire in order), and one issued before
+// them made every decode GEMV wait a memory round trip before its first
+// load.
 __device__ __forceinline__ uint2 nf4_lut_entry(uint32_t e)
 {
-    const float l0 = kNf4Levels[e & 15], l1 = kNf4Levels[e >> 4];
+    const float *lv = kNf4LevelValues;
+    float l0 = lv[0], l1 = lv[0];
+#pragma unroll
+    for (int c = 1; c < 16; ++c) {
+        l0 = (e & 15u) == uint32_t(c) ? lv[c] : l0;
+        l1 = (e >> 4) == uint32_t(c) ? lv[c] : l1;
+    }
     const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
     const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
     return uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
@@ -1439,6 +1453,19 @@ __device__ __forceinline__ void nf4_load(Nf4Block<T, S, HALF> &blk, const v4u *c
             blk.w[st][t] = wp[st][t][index * 64];
             blk.sc[st][t] = sp[st][t][index * 16];
         }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+        blk.af[ks] = ap.at(index * 4 + ks, 0, 1);
+    blk.xf[0] = xp[0][index];
+    blk.xf[1] = xp[1][index];
+}
+
+// The activation half of nf4_load (fragments and group factors), for a
+// block whose weights were loaded ahead of the in-kernel prologue.
+template <int T, int S, bool HALF, typename AP>
+__device__ __forceinline__ void nf4_load_a(Nf4Block<T, S, HALF> &blk, const AP &ap,
+                                           const float *const (&xp)[2], uint32_t index)
+{
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
         blk.af[ks] = ap.at(index * 4 + ks, 0, 1);
@@ -1587,10 +1614,13 @@ void gemv_nf4_kernel(MfmaArgs a)
     using ST = typename ScaleT<HALF>::type;
     // kLutCopies interleaved copies of the 256-entry table; lane l reads copy
     // l % kLutCopies, so the lanes of one LDS cycle spread over distinct banks.
+    // Built after the first loads are issued (it needs no memory access);
+    // a barrier orders it before the first product.
     __shared__ uint2 lut_all[256 * kLutCopies];
-    for (uint32_t i = threadIdx.x; i < 256 * kLutCopies; i += blockDim.x)
-        lut_all[i] = nf4_lut_entry(i / kLutCopies);
-    __syncthreads();
+    auto build_table = [&] {
+        for (uint32_t i = threadIdx.x; i < 256 * kLutCopies; i += blockDim.x)
+            lut_all[i] = nf4_lut_entry(i / kLutCopies);
+    };
     const uint2 *lut = lut_all + (threadIdx.x % kLutCopies);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -1648,6 +1678,8 @@ void gemv_nf4_kernel(MfmaArgs a)
             nf4_reg_load(rx0, xrow, live, a.k, s_begin, 0);
             nf4_load_w(buf0, wp, sp, 0);
         }
+        build_table();
+        __syncthreads();
         for (uint32_t i = 0; i < nblk; i += 2) {
             if (i + 1 < nblk) {
                 nf4_reg_load(rx1, xrow, live, a.k, s_begin, i + 1);
@@ -1672,6 +1704,11 @@ void gemv_nf4_kernel(MfmaArgs a)
         _Float16 *frag = reinterpret_cast<_Float16 *>(lds_dyn + size_t(waves) * S * T * 2 * 64);
         // Fragments: k_pad / 32 ksteps x 4 lane blocks x rp rows x 8 halves.
         float *fxf = reinterpret_cast<float *>(frag + size_t(a.k_pad) * rp);
+        // The first weights go out before the prologue's activation loads:
+        // their latencies overlap instead of adding up.
+        if (nblk > 0)
+            nf4_load_w(buf0, wp, sp, 0);
+        build_table();  // ordered before the products by the barrier below
         for (uint32_t i = a.m * groups + threadIdx.x; i < 8 * groups; i += blockDim.x)
             fxf[i] = 0.0f;
         block_prologue<XKind(PRO)>(a.xform, a.m, a.k, groups, rms_scratch,
@@ -1685,13 +1722,15 @@ void gemv_nf4_kernel(MfmaArgs a)
                                    j,
                                4 * rp, j < rp};
         if (nblk > 0)
-            nf4_load(buf0, wp, sp, lap, xp, 0);
+            nf4_load_a(buf0, lap, xp, 0);
         main_loop(lap);
     } else {
         const GlobalFrag<v8h> gap{reinterpret_cast<const v8h *>(a.afrag) + size_t(s_begin) * 64 +
                                   lane};
         if (nblk > 0)
             nf4_load(buf0, wp, sp, gap, xp, 0);
+        build_table();
+        __syncthreads();
         main_loop(gap);
     }
     const uint32_t batch[2] = {2 * q, 2 * q + 1};
@@ -1715,28 +1754,6 @@ void gemv_nf4_kernel(MfmaArgs a)
 // ---------------------------------------------------------------------------
 constexpr uint32_t kStreamLutCopies = 32;
 
-// nf4_lut_entry with the levels read by scalar loads and picked by selects:
-// a per-lane constant-memory load issued after the weight loads would wait
-// for all of them (loads retire in order).
-__device__ __forceinline__ uint2 nf4_lut_entry_uniform(uint32_t e)
-{
-    float lv[16];
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
-        lv[c] = kNf4Levels[c];
-    float l0 = lv[0], l1 = lv[0];
-#pragma unroll
-    for (int c = 1; c < 16; ++c) {
-        l0 = (e & 15u) == uint32_t(c) ? lv[c] : l0;
-        l1 = (e >> 4) == uint32_t(c) ? lv[c] : l1;
-    }
-    const _Float16 h0 = _Float16(l0), h1 = _Float16(l1);
-    const _Float16 r0 = _Float16(l0 - float(h0)), r1 = _Float16(l1 - float(h1));
-    return uint2{unsigned(__builtin_bit_cast(unsigned short, h0)) |
-                     (unsigned(__builtin_bit_cast(unsigned short, h1)) << 16),
-                 unsigned(__builtin_bit_cast(unsigned short, r0)) |
-                     (unsigned(__builtin_bit_cast(unsigned short, r1)) << 16)};
-}
 template <int G, bool HALF>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArgs a)
 {
@@ -1797,7 +1814,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
     const uint32_t rp = 2 * a.m;
     const bool row_read = j < rp;
     if (threadIdx.x < 256)
-        entries[threadIdx.x] = nf4_lut_entry_uniform(threadIdx.x);
+        entries[threadIdx.x] = nf4_lut_entry(threadIdx.x);
     __syncthreads();
     for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
         const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
