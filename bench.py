@@ -325,7 +325,9 @@ def profile_only(backend, args) -> int:
     if args.profile.startswith("lfm2-"):
         log(json.dumps(lfm2_decode(backend, args.profile[5:])))
         return 0
-    if args.profile == "gemm":
+    if args.profile in ("gemm", "gemm-single"):
+        # gemm-single: the opt-in single-half activations.
+        backend.set_gemm_activations(1 if args.profile == "gemm-single" else 0)
         n, k, m = 8192, 2048, 2048
         codes, scales16 = convert.packed_weights(n, k, "ternary", 0x5EED0101)
         scales = convert.f16_to_f32(scales16)
@@ -336,7 +338,7 @@ def profile_only(backend, args) -> int:
         for _ in range(6):
             backend.packed_linear(out, xb, cb, sb)
         backend.synchronize()
-        log(f"gemm ternary M={m} {n}x{k} x 6")
+        log(f"gemm ternary M={m} {n}x{k} x 6 ({args.profile})")
         return 0
     if args.profile == "copy":
         count = 64 << 20
@@ -426,10 +428,11 @@ def main() -> int:
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
     ap.add_argument("--profile", choices=["dominant", "head-ternary", "head-nf4", "copy",
-                                          "lfm2-350m", "lfm2-1.2b", "gemm"],
+                                          "lfm2-350m", "lfm2-1.2b", "gemm", "gemm-single"],
                     help="run only the dominant operation (or the 65536x2048 head of "
                          "another format, a 256 MiB device copy, the counter calibration, "
-                         "an LFM2 decode, or the ternary M=2048 x 8192x2048 prefill GEMM) "
+                         "an LFM2 decode, or the ternary M=2048 x 8192x2048 prefill GEMM, "
+                         "gemm-single with single-half activations) "
                          "for rocprofv3, and print no JSON line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
