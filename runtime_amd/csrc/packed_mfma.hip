@@ -658,11 +658,12 @@ __device__ __forceinline__ void i8_load_w(I8Block<F, T, S, NF, HALF> &blk,
         for (int t = 0; t < T; ++t) {
 #pragma unroll
             for (int l = 0; l < B::LOADS; ++l) {
-                // Large INT8 matrices (the 4-tile plan) stream once per
-                // launch: non-temporal loads measured about 10 % faster on
-                // the 65536-row head; ternary, NF4 and small fused shapes
-                // measured the same or slower with them.
-                if constexpr (F == Format::Int8 && T == 4)
+                // INT8 weights stream once per launch: non-temporal loads
+                // measured about 10 % faster on the 65536-row head and 2-4 %
+                // on 8192 x 2048 and 2048 x 8192 (B = 1 and 4), the same on
+                // the smaller shapes; ternary and NF4 measured the same or
+                // slower with them.
+                if constexpr (F == Format::Int8)
                     blk.w[st][t][l] =
                         __builtin_nontemporal_load(&wp[st][t][(index * B::LOADS + l) * 64]);
                 else
@@ -2003,6 +2004,9 @@ Plan plan_for(uint32_t n_tiles, uint32_t ksteps, uint32_t lb, int max_t, bool wi
 constexpr int kDeepWaves = 16;
 // Largest grid (blocks) that takes the two-part K split.
 constexpr uint32_t kSplitMaxBlocks = 128;
+// Row tiles from which an INT8 product at one or two rows is an LM head
+// (65536 rows: 4096 tiles) and streams one tile per block.
+constexpr uint32_t kHeadTiles = 4096;
 
 // Whether float ranges [a, a + na) and [b, b + nb) share memory.
 bool overlaps(const float *a, size_t na, const float *b, size_t nb)
@@ -2351,6 +2355,14 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
         pro = int(xform.kind);
     }
     plan.tiles_per_block = tiles_of(plan);
+    // The INT8 LM head at one or two rows takes one tile per block: 4096
+    // blocks of 4 waves, 8 KB of weights per wave, against 1024 blocks with
+    // 32 KB per wave in the 4-tile plan.  65536 x 2048 at B = 1: 25.1 ->
+    // 23.2 us; B = 2: 25.3 -> 23.7 us.  From four rows on the 4-tile plan is
+    // faster (B = 4: 24.9 against 25.8-26.5 us; B = 8 28.5 against 43-46).
+    if (F == Format::Int8 && pro == kRegPro && streams == 1 && !call.segments && call.m <= 2 &&
+        n_tiles >= kHeadTiles && plan.tiles_per_block == 4 && ksteps % (4 * Geo<F>::lb) == 0)
+        plan = Plan{1, 4};
     if ((pro < 0 || pro == kRegPro) && streams == 1 && nf == 1)
         plan = deepen(plan, n_tiles, ksteps, Geo<F>::lb);
     // Small grids with the separate prologue split K over two blocks per

@@ -1,5 +1,5 @@
-"""HIP events and stream capture over ctypes, for timing and replaying work
-queued on a backend's stream (`mfh_stream`).
+"""HIP events over ctypes, for timing work queued on a backend's stream
+(`mfh_stream`).
 
 Uses the same libamdhip64 the backend library links, so stream and event
 handles are shared with it.  Plumbing for benches and drivers; no compute.
@@ -24,12 +24,6 @@ def hip() -> ctypes.CDLL:
             "hipEventSynchronize": [P],
             "hipEventElapsedTime": [ctypes.POINTER(ctypes.c_float), P, P],
             "hipStreamSynchronize": [P],
-            "hipStreamBeginCapture": [P, ctypes.c_int],
-            "hipStreamEndCapture": [P, PP],
-            "hipGraphInstantiate": [PP, P, P, P, ctypes.c_size_t],
-            "hipGraphLaunch": [P, P],
-            "hipGraphExecDestroy": [P],
-            "hipGraphDestroy": [P],
             "hipGetErrorString": [ctypes.c_int],
         }
         for name, args in sigs.items():
@@ -66,35 +60,6 @@ class Event:
         try:
             if self.handle:
                 hip().hipEventDestroy(self.handle)
-        except Exception:
-            pass
-
-
-class Graph:
-    """Work captured from one stream, replayable with `launch`."""
-
-    def __init__(self, stream: int, record):
-        """Capture everything `record()` enqueues on `stream`."""
-        check(hip().hipStreamBeginCapture(stream, 2), "hipStreamBeginCapture")  # relaxed
-        try:
-            record()
-        finally:
-            g = ctypes.c_void_p()
-            err = hip().hipStreamEndCapture(stream, ctypes.byref(g))
-        check(err, "hipStreamEndCapture")
-        self.graph = g.value
-        e = ctypes.c_void_p()
-        check(hip().hipGraphInstantiate(ctypes.byref(e), self.graph, None, None, 0),
-              "hipGraphInstantiate")
-        self.exec = e.value
-
-    def launch(self, stream: int) -> None:
-        check(hip().hipGraphLaunch(self.exec, stream), "hipGraphLaunch")
-
-    def __del__(self):
-        try:
-            hip().hipGraphExecDestroy(self.exec)
-            hip().hipGraphDestroy(self.graph)
         except Exception:
             pass
 
