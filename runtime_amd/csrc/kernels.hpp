@@ -97,6 +97,11 @@ mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, u
 
 // Decode GEMV for m <= 8 on FP32 FMA units.
 void launch_gemv_fma(hipStream_t stream, const PackedCall &call);
+// f32 vector GEMV for wide contractions (one plain activation row, 4096 <=
+// k <= 8192, n <= 8192, one stream, canonical codes): enqueues it and
+// returns true, or returns false (nothing enqueued) where it does not serve
+// the call.  The matrix-core GEMV tries it first.
+bool try_vgemv(hipStream_t stream, const PackedCall &call);
 // Matrix-core decode GEMV for m <= 8 (needs `tiles` and `tiled_scales` on
 // every stream).  `scratch` holds gemv_mfma_scratch_bytes(call) bytes.
 bool gemv_mfma_supported(Format format);

@@ -2271,6 +2271,8 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
+    if (try_vgemv(stream, call))
+        return;
     if constexpr (F == Format::Ternary) {
         if (try_stream_ternary(stream, call, n_tiles))
             return;
@@ -2459,6 +2461,8 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t k_pad = pad_to(call.k, 128);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
+    if (try_vgemv(stream, call))
+        return;
     if (try_stream_nf4(stream, call, n_tiles))
         return;
     Scratch sc = carve(scratch, k_pad);

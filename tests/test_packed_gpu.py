@@ -254,6 +254,86 @@ def test_ternary_reserved_code_decodes_as_plus_two(backend, path):
         assert_close(got, oracle.packed_linear(x, codes, scales), 1e-4, 1e-4)
 
 
+# --- wide contractions at one or two rows (f32 vector GEMV) ------------------------
+# On the auto path one plain activation row with 4096 <= k <= 8192 and n <=
+# 8192 runs the f32 vector GEMV (one lane per 32-wide k slice, waves
+# splitting K); two rows, the other paths and SwiGLU-formed activations run
+# the matrix-core or FMA kernels on the same cases.
+
+WIDE_K_SHAPES = [(2048, 8192), (1024, 4608), (1001, 4096), (77, 8192), (8192, 4224), (3, 8192)]
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m", [1, 2])
+@pytest.mark.parametrize("n,k", WIDE_K_SHAPES)
+def test_wide_k_decode_gemv(backend, path, scheme, m, n, k):
+    say("wide k", scheme, path, m, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0500 + n + k)
+    x = convert.normal((m, k), 0xAC70500 + m + k)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear_threaded(x, codes, scales)
+    assert_close(got, want, 1e-4, 1e-4)
+    assert max_rel_err(got, want) <= 1e-3
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_wide_k_f32_scales_and_reserved_codes(backend, path, scheme):
+    """Scales that binary16 cannot hold (the kernels then read the f32
+    stream), ternary code 3 (+2) and the INT8 extremes +-127, at k = 8192."""
+    say("wide k f32 scales", scheme, path)
+    rng = np.random.default_rng(0x5151)
+    n, k = 640, 8192
+    codes, _ = make_weights(n, k, scheme, 0x5EED0510)
+    if scheme == "ternary":
+        codes[:, :16] = 0xFF
+    elif scheme == "int8":
+        codes[:, :64] = 0x7F
+        codes[:, 64:128] = 0x81
+    scales = rng.uniform(0.001, 0.05, (n, k // 128)).astype(np.float32)
+    scales[:, 0] = np.float32(0.0123456789)  # not exact in binary16
+    for m in (1, 2):
+        x = convert.normal((m, k), 0xAC70510 + m)
+        got = run_linear(backend, x, codes, scales)
+        want = oracle.packed_linear_threaded(x, codes, scales)
+        assert_close(got, want, 1e-4, 1e-4)
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_wide_k_non_finite_row(backend, path, scheme):
+    """A NaN or infinity in one activation row makes all of that row's
+    outputs non-finite; the other row matches the oracle."""
+    say("wide k non-finite", scheme, path)
+    n, k = 512, 8192
+    codes, scales = make_weights(n, k, scheme, 0x5EED0520)
+    x = convert.normal((2, k), 0xAC70520)
+    x[1, 4000] = np.inf
+    got = run_linear(backend, x, codes, scales)
+    assert not np.isfinite(got[1]).any()
+    want = oracle.packed_linear_threaded(x[:1], codes, scales)
+    assert_close(got[:1], want, 1e-4, 1e-4)
+    x[1, 4000] = np.nan
+    got = run_linear(backend, x, codes, scales)
+    assert not np.isfinite(got[1]).any()
+
+
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("n,k", [(2048, 8192), (1024, 4608)])
+def test_wide_k_swiglu_linear(backend, path, scheme, n, k):
+    """packed_swiglu_linear at the FFN down-projection shapes (the
+    activations formed by the matrix-core prologue or the staging kernel)."""
+    say("wide k swiglu", scheme, path, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0530 + k)
+    cb, sb = upload_weights(backend, codes, scales)
+    for m in (1, 2):
+        gate = convert.normal((m, k), 0xAC70531 + m)
+        up = convert.normal((m, k), 0xAC70532 + m)
+        gb_ = backend.upload_f32(gate.shape, gate)
+        ub_ = backend.upload_f32(up.shape, up)
+        out = backend.allocate_f32((m, n))
+        backend.packed_swiglu_linear(out, gb_, ub_, cb, sb)
+        assert_close(backend.read(out), oracle.packed_swiglu_linear(gate, up, codes, scales))
+
+
 def test_reference_ternary_fixture_through_the_gpu_gather(backend, golden_dir):
     """crates/executor-core/tests/fixtures/ternary-v1-001: the five rows'
     expected dequantization, bit for bit, from the HIP gather."""
