@@ -316,7 +316,8 @@ def profile_only(backend, args) -> int:
     """Launch sequences for rocprofv3: `dominant` builds the 65536x2048 INT8
     head (same seed as the sweep) on copies totalling 1 GiB and launches it
     100 times over them after one untimed pass per copy (`head-ternary` and
-    `head-nf4`: the same for that format's head); `copy` moves
+    `head-nf4`: the same for that format's head; `product`: the same for the
+    --product format, shape and batch); `copy` moves
     256 MiB with mfh_copy four times, the known-size reference for
     FETCH_SIZE and WRITE_SIZE."""
     from runtime_amd import convert
@@ -352,7 +353,14 @@ def profile_only(backend, args) -> int:
     fmt, (n, k), b = DOMINANT
     if args.profile.startswith("head-"):
         fmt = args.profile[5:]
-    codes, scales = sweep_weights(convert, fmt, n, k)
+    if args.profile == "product":
+        fmt, n, k, b = args.product.split(",")
+        n, k, b = int(n), int(k), int(b)
+    if (n, k) in SHAPES:
+        codes, scales = sweep_weights(convert, fmt, n, k)
+    else:
+        codes, scales16 = convert.packed_weights(n, k, fmt, 0x5EED0777)
+        scales = convert.f16_to_f32(scales16)
     copies = rotation(backend, codes, scales)
     x = backend.upload_f32((b, k), convert.normal((b, k), 0xAC70001 + b))
     out = backend.allocate_f32((b, n))
@@ -428,12 +436,15 @@ def main() -> int:
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
     ap.add_argument("--profile", choices=["dominant", "head-ternary", "head-nf4", "copy",
-                                          "lfm2-350m", "lfm2-1.2b", "gemm", "gemm-single"],
+                                          "lfm2-350m", "lfm2-1.2b", "gemm", "gemm-single",
+                                          "product"],
                     help="run only the dominant operation (or the 65536x2048 head of "
                          "another format, a 256 MiB device copy, the counter calibration, "
-                         "an LFM2 decode, or the ternary M=2048 x 8192x2048 prefill GEMM, "
-                         "gemm-single with single-half activations) "
-                         "for rocprofv3, and print no JSON line")
+                         "an LFM2 decode, the ternary M=2048 x 8192x2048 prefill GEMM, "
+                         "gemm-single with single-half activations, or the --product "
+                         "decode GEMV) for rocprofv3, and print no JSON line")
+    ap.add_argument("--product", default="ternary,2048,8192,1",
+                    help="format,n,k,batch of --profile product (1 GiB rotation, 100 launches)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build runs the packed GEMV path on a "
