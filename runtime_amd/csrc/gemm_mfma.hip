@@ -219,6 +219,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     constexpr int TJS = kTJ / S;                 // column tiles per stream per wave
     constexpr int BNS = kBN / S;                 // block columns per stream
     constexpr int SPC = Chunk<F>::stages;
+    // Raised wave priority over each half-stage's MFMAs, where it measured
+    // faster (M = 2048 x 8192 x 2048: ternary exact 165 -> 157-160 us, INT8
+    // exact 175-177 -> 170-175, NF4 single-half 161-163 -> 156-157); NF4
+    // exact (221 -> 250) and ternary single-half (108 -> 112) keep one level.
+    constexpr bool PRIO = LO ? F != Format::Nf4 : F == Format::Nf4;
     __shared__ _Float16 As[2][PA][kBM][kRow];  // [stage][hi, lo][row][k]
     __shared__ uint2 lut[F == Format::Nf4 ? 256 : 1];
 
@@ -372,6 +377,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
             if (h == 1 && (s + 1) % SPC == 0 && s + 1 < s_end)
                 load_chunk((s + 1) / SPC, cur);
             const int koff = F == Format::Nf4 ? 32 * h + 8 * lq : 16 * lq + 8 * h;
+            if constexpr (PRIO)
+                __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int i = 0; i < kTI; ++i) {
                 const int row = wm * 64 + i * 16 + li;
@@ -392,6 +399,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                     acc[i][jt] = c;
                 }
             }
+            if constexpr (PRIO)
+                __builtin_amdgcn_s_setprio(0);
         }
         if (!FIRST) {
             // Group epilogue: total += group_sum * scale[n].
