@@ -32,11 +32,13 @@
 // half h takes k = 16q + 8h + 0..7 of lane block q (INT8, ternary: the
 // tiles' byte order) or k = 32h + 8q + 0..7 (NF4: its 32-wide kstep).
 //
-// Tiling.  A 256-lane block (2 x 2 waves) computes a 128 (m) x 128 (n)
-// output tile, split over S weight streams of 128 / S columns each; a wave
-// owns 64 x 64 (4 x 4 MFMA tiles, 4 / S column tiles per stream), with a
-// group accumulator and a running total per MFMA tile.  The 74 KB of LDS
-// lets two blocks share a CU.
+// Tiling.  A 256-lane block (4 waves) computes a 128 (m) x 128 (n) output
+// tile, split over S weight streams of 128 / S columns each.  The waves lie
+// along n: each owns all 128 rows x 32 columns (8 x 2 MFMA tiles), so every
+// weight tile is decoded by one wave of the block; exact ternary keeps 2 x 2
+// waves of 64 x 64 (4 x 4 MFMA tiles), which reuse each activation fragment
+// over four column tiles.  A wave holds a group accumulator and a running
+// total per MFMA tile.  The 74 KB of LDS lets two blocks share a CU.
 //
 // Grid mapping.  Workgroups are dealt round-robin to the 8 XCDs.  Block b
 // computes tile (b % 8) * (tiles / 8) + b / 8, so each XCD's L2 holds a
@@ -64,8 +66,6 @@ constexpr int kBK = 64;        // k per stage
 // LDS row pitch in halves: kBK + 8 (144 bytes) puts the 16 rows read by one
 // lane group on distinct banks.
 constexpr int kRow = kBK + 8;
-constexpr int kTI = 4;  // 16-row MFMA tiles per wave
-constexpr int kTJ = 4;  // 16-column MFMA tiles per wave, all streams
 
 __constant__ float kLevels[16] = {
     -1.0f,        -0.6961928f,  -0.52507305f, -0.3949175f,
@@ -216,14 +216,21 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
 {
     constexpr int P = F == Format::Nf4 ? 2 : 1;  // weight level planes
     constexpr int PA = LO ? 2 : 1;               // activation planes (hi, lo)
-    constexpr int TJS = kTJ / S;                 // column tiles per stream per wave
+    // Waves along n (M = 2048 x 8192 x 2048 against 2 x 2: NF4 exact 218 ->
+    // 206 us, INT8 exact 172 -> 165, single-half 3-9 % faster; exact ternary
+    // 158 -> 159-160, so it keeps 2 x 2).
+    constexpr int WN = LO && F == Format::Ternary ? 2 : 4;
+    constexpr int WM = 4 / WN;
+    constexpr int TI = kBM / 16 / WM;            // 16-row MFMA tiles per wave
+    constexpr int TJ = kBN / 16 / WN;            // 16-column MFMA tiles per wave
+    constexpr int TJS = TJ / S;                  // column tiles per stream per wave
     constexpr int BNS = kBN / S;                 // block columns per stream
     constexpr int SPC = Chunk<F>::stages;
-    // Raised wave priority over each half-stage's MFMAs, where it measured
-    // faster (M = 2048 x 8192 x 2048: ternary exact 165 -> 157-160 us, INT8
-    // exact 175-177 -> 170-175, NF4 single-half 161-163 -> 156-157); NF4
-    // exact (221 -> 250) and ternary single-half (108 -> 112) keep one level.
-    constexpr bool PRIO = LO ? F != Format::Nf4 : F == Format::Nf4;
+    // Raised wave priority over each half-stage's MFMAs for exact ternary
+    // (165 -> 157-160 us); with the waves along n every other variant ran
+    // as fast or faster without it (INT8 exact 168.6 against 165.3 us, NF4
+    // single-half 150.7 against 144.1).
+    constexpr bool PRIO = LO && F == Format::Ternary;
     __shared__ _Float16 As[2][PA][kBM][kRow];  // [stage][hi, lo][row][k]
     __shared__ uint2 lut[F == Format::Nf4 ? 256 : 1];
 
@@ -250,7 +257,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     const int tid = threadIdx.x, lane = tid & 63;
     // Wave-uniform, so the tile addresses live in scalar registers.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     const int li = lane & 15, lq = lane >> 4;
     const uint32_t chunk_stages = g.k / kBK / g.chunks;
     const uint32_t s_begin = chunk * chunk_stages, s_end = s_begin + chunk_stages;
@@ -281,11 +288,11 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     };
 
     // The wave's weight tiles: column tile jt is tile tt of stream jt / TJS.
-    const v4u *wptr[kTJ];
-    const void *sptr[kTJ];
-    bool wlive[kTJ];
+    const v4u *wptr[TJ];
+    const void *sptr[TJ];
+    bool wlive[TJ];
 #pragma unroll
-    for (int jt = 0; jt < kTJ; ++jt) {
+    for (int jt = 0; jt < TJ; ++jt) {
         const int st = jt / TJS, tt = jt % TJS;
         const uint32_t t = n0 / 16 + wn * TJS + tt;
         wlive[jt] = t < g.n_tiles;
@@ -298,19 +305,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                                                     size_t(wlive[jt] ? t : 0) * g.groups_pad * 16 +
                                                     li);
     }
-    v4u cur[kTJ];
+    v4u cur[TJ];
     // Tiles past n read tile 0 (their columns are never stored).
-    auto load_chunk = [&](uint32_t c, v4u (&dst)[kTJ]) {
+    auto load_chunk = [&](uint32_t c, v4u (&dst)[TJ]) {
 #pragma unroll
-        for (int jt = 0; jt < kTJ; ++jt)
+        for (int jt = 0; jt < TJ; ++jt)
             dst[jt] = wptr[jt][size_t(c) * 64];
     };
 
-    v4f acc[kTI][kTJ], total[kTI][kTJ];
+    v4f acc[TI][TJ], total[TI][TJ];
 #pragma unroll
-    for (int i = 0; i < kTI; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
-        for (int jt = 0; jt < kTJ; ++jt) {
+        for (int jt = 0; jt < TJ; ++jt) {
             acc[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
             total[i][jt] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
         }
@@ -318,10 +325,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     // Each lane's weight scales of a group, kept in their stored form:
     // loaded when the group starts and used at its end, so the in-order load
     // counter never makes an early instruction wait for them.
-    typename std::conditional<HALF, unsigned short, float>::type gsc_raw[kTJ];
+    typename std::conditional<HALF, unsigned short, float>::type gsc_raw[TJ];
     auto load_group_constants = [&](uint32_t grp) {
 #pragma unroll
-        for (int jt = 0; jt < kTJ; ++jt) {
+        for (int jt = 0; jt < TJ; ++jt) {
             if constexpr (HALF)
                 gsc_raw[jt] = static_cast<const unsigned short *>(sptr[jt])[size_t(grp) * 16];
             else
@@ -352,9 +359,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
             load_group_constants(s / 2);
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            v8h bh[kTJ], bl[kTJ];
+            v8h bh[TJ], bl[TJ];
 #pragma unroll
-            for (int jt = 0; jt < kTJ; ++jt) {
+            for (int jt = 0; jt < TJ; ++jt) {
                 if constexpr (F == Format::Int8) {
                     bh[jt] = decode_i8(cur[jt], h);
                 } else if constexpr (F == Format::Ternary) {
@@ -380,12 +387,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
             if constexpr (PRIO)
                 __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-            for (int i = 0; i < kTI; ++i) {
-                const int row = wm * 64 + i * 16 + li;
+            for (int i = 0; i < TI; ++i) {
+                const int row = wm * (kBM / WM) + i * 16 + li;
                 const v8h ah = *reinterpret_cast<const v8h *>(&As[buf][0][row][koff]);
                 const v8h al = *reinterpret_cast<const v8h *>(&As[buf][PA - 1][row][koff]);
 #pragma unroll
-                for (int jt = 0; jt < kTJ; ++jt) {
+                for (int jt = 0; jt < TJ; ++jt) {
                     v4f c;
                     if (UNROLL && FIRST && h == 0)
                         c = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh[jt], v4f{}, 0, 0, 0);
@@ -404,18 +411,18 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
         }
         if (!FIRST) {
             // Group epilogue: total += group_sum * scale[n].
-            float gsc[kTJ];
+            float gsc[TJ];
 #pragma unroll
-            for (int jt = 0; jt < kTJ; ++jt) {
+            for (int jt = 0; jt < TJ; ++jt) {
                 if constexpr (HALF)
                     gsc[jt] = __half2float(__ushort_as_half(gsc_raw[jt]));
                 else
                     gsc[jt] = gsc_raw[jt];
             }
 #pragma unroll
-            for (int i = 0; i < kTI; ++i)
+            for (int i = 0; i < TI; ++i)
 #pragma unroll
-                for (int jt = 0; jt < kTJ; ++jt)
+                for (int jt = 0; jt < TJ; ++jt)
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         total[i][jt][r] = fmaf(acc[i][jt][r], gsc[jt], total[i][jt][r]);
@@ -438,19 +445,19 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     }
 
     // The rows' 2^e (rows past m read row 0; they are never stored).
-    float rowf[kTI][4];
+    float rowf[TI][4];
 #pragma unroll
-    for (int i = 0; i < kTI; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t mm = m0 + wm * 64 + i * 16 + lq * 4 + r;
+            const uint32_t mm = m0 + wm * (kBM / WM) + i * 16 + lq * 4 + r;
             rowf[i][r] = g.factor[mm < g.m ? mm : 0];
         }
 #pragma unroll
-    for (int i = 0; i < kTI; ++i)
+    for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t mm = m0 + wm * 64 + i * 16 + lq * 4 + r;
+            const uint32_t mm = m0 + wm * (kBM / WM) + i * 16 + lq * 4 + r;
             if (mm >= g.m)
                 continue;
 #pragma unroll
