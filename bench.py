@@ -330,7 +330,7 @@ def profile_only(backend, args) -> int:
         # gemm-single: the opt-in single-half activations.
         backend.set_gemm_activations(1 if args.profile == "gemm-single" else 0)
         n, k, m = 8192, 2048, 2048
-        codes, scales16 = convert.packed_weights(n, k, "ternary", 0x5EED0101)
+        codes, scales16 = convert.packed_weights(n, k, args.gemm_format, 0x5EED0101)
         scales = convert.f16_to_f32(scales16)
         cb = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
         sb = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
@@ -339,7 +339,7 @@ def profile_only(backend, args) -> int:
         for _ in range(6):
             backend.packed_linear(out, xb, cb, sb)
         backend.synchronize()
-        log(f"gemm ternary M={m} {n}x{k} x 6 ({args.profile})")
+        log(f"gemm {args.gemm_format} M={m} {n}x{k} x 6 ({args.profile})")
         return 0
     if args.profile == "copy":
         count = 64 << 20
@@ -440,9 +440,11 @@ def main() -> int:
                                           "product"],
                     help="run only the dominant operation (or the 65536x2048 head of "
                          "another format, a 256 MiB device copy, the counter calibration, "
-                         "an LFM2 decode, the ternary M=2048 x 8192x2048 prefill GEMM, "
+                         "an LFM2 decode, the M=2048 x 8192x2048 prefill GEMM, "
                          "gemm-single with single-half activations, or the --product "
                          "decode GEMV) for rocprofv3, and print no JSON line")
+    ap.add_argument("--gemm-format", choices=["ternary", "int8", "nf4"], default="ternary",
+                    help="weight format of --profile gemm / gemm-single")
     ap.add_argument("--product", default="ternary,2048,8192,1",
                     help="format,n,k,batch of --profile product (1 GiB rotation, 100 launches)")
     args = ap.parse_args()
