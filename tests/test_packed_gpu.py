@@ -365,9 +365,11 @@ def test_prefill_gemm(backend, path, scheme, m):
 
 # Ragged prefill shapes: partial 128-row and 64-column output tiles, K that
 # ends inside a 256-wide ternary chunk, a single group, and shapes where the
-# contraction is split across workgroups.
+# contraction is split across workgroups into 3, 4, 5, 16 and 18 runs of whole
+# groups (3 and 5 start runs inside a ternary tile load, which spans two
+# groups).
 GEMM_EDGE_SHAPES = [(9, 37, 384), (130, 200, 640), (257, 70, 1152), (33, 1000, 128),
-                    (129, 4608, 1024), (12, 64, 4096)]
+                    (129, 4608, 1024), (12, 64, 4096), (100, 1024, 4608), (140, 300, 1920)]
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
