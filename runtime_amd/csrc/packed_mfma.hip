@@ -2340,7 +2340,9 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     // Preference: the register prologue (norm or plain), then the LDS one,
     // then the separate prologue kernel.  For plain activations the register
     // prologue measured 13-46 % faster than the LDS one wherever both apply
-    // (4608 x 1024 at two rows: ternary 7.49 -> 4.01 us, INT8 5.52 -> 3.61).
+    // (4608 x 1024 at two rows: ternary 7.49 -> 4.01 us, INT8 5.52 -> 3.61);
+    // for the add + norm, taking the LDS one wherever it applies made decode
+    // slower (1.2B shape 1596 -> 1548 tok/s, 350M 2376 -> 2143).
     // The 8-wave plan takes the norm only with one tile per block: the 4-tile
     // norm kernel holds two waves per SIMD, too few for the LM head's 8-wave
     // blocks (1.2B-shape decode 1389 -> 1355 tok/s).
