@@ -492,6 +492,33 @@ def test_pair_and_swiglu_variants(backend, path, scheme, m):
     assert_close(backend.read(out), oracle.packed_swiglu_linear(gate, up, c2, s2))
 
 
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_pair_ffn_shape(backend, path, scheme, m):
+    # The LFM2-1.2B FFN gate/up shape: 8192 rows per stream at K = 2048, where
+    # the plain pair takes the 8-wave register-prologue plan.
+    say("pair ffn shape", scheme, path, m)
+    n, k = 8192, 2048
+    ca, sa = make_weights(n, k, scheme, 0x5EED0410)
+    cb, sb = make_weights(n, k, scheme, 0x5EED0411)
+    x = convert.normal((m, k), 0xAC70410 + m)
+    ga, gsa = upload_weights(backend, ca, sa)
+    gb, gsb = upload_weights(backend, cb, sb)
+    xb = backend.upload_f32(x.shape, x)
+    out_a = backend.allocate_f32((m, n))
+    out_b = backend.allocate_f32((m, n))
+    backend.packed_linear_pair(out_a, out_b, xb, ga, gsa, gb, gsb)
+    want_a = oracle.packed_linear_threaded(x, ca, sa)
+    want_b = oracle.packed_linear_threaded(x, cb, sb)
+    assert_close(backend.read(out_a), want_a)
+    assert_close(backend.read(out_b), want_b)
+    fused = backend.allocate_f32((m, n))
+    backend.packed_swiglu_pair(fused, xb, ga, gsa, gb, gsb)
+    assert_close(backend.read(fused), oracle.packed_swiglu_pair(x, ca, sa, cb, sb))
+    for buf in (ga, gsa, gb, gsb, xb, out_a, out_b, fused):
+        buf.release()
+
+
 # --- gather -----------------------------------------------------------------------
 
 @pytest.mark.parametrize("scheme", SCHEMES)
