@@ -12,23 +12,31 @@
 // kernel: two dependent launches per product.  This kernel reads the f32
 // activations as they are, in one launch; at one row its arithmetic (about
 // 2.5 vector instructions per weight) stays below the launch and memory
-// latency it replaces.  Measured against the two launches, one row:
+// latency it replaces.  Measured against the two launches, one row (with
+// 32-wide slices):
 // 1024 x 4608 ternary 6.9 -> 4.2 us, 2048 x 8192 7.2 -> 7.05 us (INT8 8.0 ->
 // 7.6, NF4 8.1 -> 7.6); LFM2 decode 350M shape 2172 -> 2376 tok/s, 1.2B
 // 1567 -> 1596.  Two rows measured slower (2048 x 8192 ternary 9.1 us), and
-// so did forming SwiGLU activations here: every block would recompute them
-// for all of K.
+// so did forming SwiGLU activations here, which every block would recompute
+// for all of K (1.2B-shape op-by-op decode, whose down projections take
+// packed_swiglu_linear, 1254 -> 1170 tok/s).
 //
-// Layout.  Lane L of wave w owns the 32-wide k slice s = 64 w + L for every
-// row of the block: it holds its 32 activations in registers
-// and reads the slice's codes of each row from the canonical row-major
-// stream (8, 16 or 32 bytes: ternary, NF4, INT8), so a wave reads 512 B - 2 KB
-// of one row contiguously.  Four lanes make a 128-group: their partial sums
-// add over the lane quad (DPP), the sum is scaled, and the groups add across
-// the wave (shuffles) and across the block's waves (LDS, in wave order).
-// A block holds R rows (R = 4 from 2048 rows, else 2: at least 512 blocks;
-// 2048 x 8192 with R = 1, 2, 8 took 10.2, 7.2, 8.8 us against 7.05, 1024 x
-// 4608 with R = 4 5.3 against 4.2) and ceil(K / 2048) waves.
+// Layout.  Lane L of wave w owns the SL-wide k slice s = 64 w + L for every
+// row of the block: it holds its SL activations in registers and reads the
+// slice's codes of each row from the canonical row-major stream (SL / 4,
+// SL / 2 or SL bytes: ternary, NF4, INT8), so a wave reads 64 SL / 4 to 64 SL
+// bytes of one row contiguously.  128 / SL lanes make a 128-group: their
+// partial sums add over the lane quad (DPP) and shuffles, the sum is scaled,
+// and the groups add across the wave (shuffles) and across the block's waves
+// (LDS, in wave order).  A block holds R rows (R = 4 from 2048 rows, else
+// 2: at least 512 blocks; 2048 x 8192 with R = 1, 2, 8 took 10.2, 7.2, 8.8
+// us against 7.05, 1024 x 4608 with R = 4 5.3 against 4.2) and
+// ceil(K / (64 SL)) waves.  SL = 16 from 2048 rows, else 8: shorter slices
+// halve each lane's dependent arithmetic and spread it over more waves.
+// Inside the LFM2 decode chain SL = 32 / 16 / 8 measured 1593 / 1635 / 1629
+// tok/s for the 1.2B shape (2048 x 8192 down projections) and 2370 / 2424 /
+// 2440 for the 350M shape (1024 x 4608); back to back at 2048 x 8192, one
+// row, ternary 7.0 / 6.2 / 6.4 us, INT8 7.5 / 6.6 / 6.9, NF4 7.6 / 7.3 / 7.8.
 //
 // Decode (crates/kernels-simd/src/lib.rs:31-57,113-130,145-183):
 //   ternary  level = c - 1, c = 2-bit field (code 3 gives +2, as on the CPU):
@@ -44,10 +52,9 @@
 namespace mfh {
 namespace {
 
-constexpr int kSlice = 32;                // k per lane
-constexpr uint32_t kWaveK = 64 * kSlice;  // k per wave
 constexpr uint32_t kMinK = 4096;
-constexpr uint32_t kMaxK = 4 * kWaveK;  // four waves
+constexpr uint32_t kMaxK = 8192;
+constexpr int kMaxWaves = 16;  // K = 8192 at SL = 8
 // Widest weight matrix served; wider ones (LM heads) stream better on the
 // matrix cores.
 constexpr uint32_t kMaxRows = 8192;
@@ -68,25 +75,36 @@ struct VArgs {
     uint32_t n, k;
 };
 
-// Code bytes of one row's 32-k slice.
-template <Format F> struct SliceCodes;
-template <> struct SliceCodes<Format::Ternary> { uint2 v; };
-template <> struct SliceCodes<Format::Nf4> { uint4 v; };
-template <> struct SliceCodes<Format::Int8> { uint4 v[2]; };
+// Code words of one row's SL-wide slice: N words of EB bytes each (a slice
+// of two bytes, ternary at SL = 8, is one half-filled word).
+template <Format F, int SL>
+struct Slice {
+    static constexpr int bytes = SL / weights_per_byte(F);
+    static constexpr int N = bytes >= 4 ? bytes / 4 : 1;
+    static constexpr int EB = bytes >= 4 ? 4 : bytes;
+};
 
-template <Format F>
-__device__ __forceinline__ SliceCodes<F> load_slice(const uint8_t *p)
+template <int N, int EB>
+__device__ __forceinline__ void load_slice(const uint8_t *p, unsigned (&w)[N])
 {
-    SliceCodes<F> c;
-    if constexpr (F == Format::Ternary) {
-        c.v = *reinterpret_cast<const uint2 *>(p);
-    } else if constexpr (F == Format::Nf4) {
-        c.v = *reinterpret_cast<const uint4 *>(p);
+    if constexpr (EB == 2) {
+        w[0] = *reinterpret_cast<const unsigned short *>(p);
+    } else if constexpr (N == 1) {
+        w[0] = *reinterpret_cast<const unsigned *>(p);
+    } else if constexpr (N == 2) {
+        const uint2 v = *reinterpret_cast<const uint2 *>(p);
+        w[0] = v.x;
+        w[1] = v.y;
     } else {
-        c.v[0] = reinterpret_cast<const uint4 *>(p)[0];
-        c.v[1] = reinterpret_cast<const uint4 *>(p)[1];
+#pragma unroll
+        for (int h = 0; h < N / 4; ++h) {
+            const uint4 v = reinterpret_cast<const uint4 *>(p)[h];
+            w[4 * h] = v.x;
+            w[4 * h + 1] = v.y;
+            w[4 * h + 2] = v.z;
+            w[4 * h + 3] = v.w;
+        }
     }
-    return c;
 }
 
 // Byte e of a word as f32 (one v_cvt_f32_ubyte).
@@ -97,49 +115,37 @@ __device__ __forceinline__ float byte_f(unsigned w, int e)
 
 // The lane's partial dot over its slice: sum level(code) * x, before the
 // ternary / INT8 offset correction (applied by the caller from sum x).
-template <Format F>
-__device__ __forceinline__ float slice_dot(const SliceCodes<F> &c, const float (&x)[kSlice],
+template <Format F, int SL, int N, int EB>
+__device__ __forceinline__ float slice_dot(const unsigned (&c)[N], const float (&x)[SL],
                                            const float2 *pairs)
 {
     float dot = 0.0f;
-    if constexpr (F == Format::Ternary) {
-        // Word q holds k = 16q + 4e + f at byte e, field f.
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const unsigned d = q ? c.v.y : c.v.x;
+    for (int q = 0; q < N; ++q) {
+        if constexpr (F == Format::Ternary) {
+            // Word q holds k = 16q + 4e + f at byte e, field f.
 #pragma unroll
             for (int f = 0; f < 4; ++f) {
-                const unsigned t = (d >> (2 * f)) & 0x03030303u;
+                const unsigned t = (c[q] >> (2 * f)) & 0x03030303u;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
+                for (int e = 0; e < EB; ++e)
                     dot = fmaf(byte_f(t, e), x[16 * q + 4 * e + f], dot);
             }
-        }
-    } else if constexpr (F == Format::Nf4) {
-        // Byte j = 4q + e holds k = 2j (low nibble) and 2j + 1 (high).
+        } else if constexpr (F == Format::Nf4) {
+            // Byte e of word q holds k = 8q + 2e (low nibble) and 8q + 2e + 1.
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            const unsigned d = q == 0 ? c.v.x : q == 1 ? c.v.y : q == 2 ? c.v.z : c.v.w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const float2 lv = pairs[(d >> (8 * e)) & 0xFFu];
+            for (int e = 0; e < EB; ++e) {
+                const float2 lv = pairs[(c[q] >> (8 * e)) & 0xFFu];
                 dot = fmaf(lv.x, x[8 * q + 2 * e], dot);
                 dot = fmaf(lv.y, x[8 * q + 2 * e + 1], dot);
             }
+        } else {
+            // Word q holds k = 4q + e at byte e.
+            const unsigned d = c[q] ^ 0x80808080u;
+#pragma unroll
+            for (int e = 0; e < EB; ++e)
+                dot = fmaf(byte_f(d, e), x[4 * q + e], dot);
         }
-    } else {
-        // Word q of the 32 bytes holds k = 4q + e at byte e.
-#pragma unroll
-        for (int h = 0; h < 2; ++h)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const uint4 &u = c.v[h];
-                const unsigned d =
-                    (q == 0 ? u.x : q == 1 ? u.y : q == 2 ? u.z : u.w) ^ 0x80808080u;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    dot = fmaf(byte_f(d, e), x[16 * h + 4 * q + e], dot);
-            }
     }
     return dot;
 }
@@ -150,17 +156,19 @@ __device__ __forceinline__ float quad_add(float v)
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <Format F, int R>
-__global__ __launch_bounds__(256) void vgemv_kernel(VArgs a)
+template <Format F, int R, int SL>
+__global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
 {
+    using SC = Slice<F, SL>;
+    constexpr int LPG = 128 / SL;  // lanes per 128-group
     __shared__ float2 pairs[F == Format::Nf4 ? 256 : 1];
-    __shared__ float red[4][R];
+    __shared__ float red[kMaxWaves][R];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if constexpr (F == Format::Nf4) {
         for (int e = tid; e < 256; e += blockDim.x)
             pairs[e] = float2{kLevelsV[e & 15], kLevelsV[e >> 4]};
     }
-    const uint32_t slices = a.k / kSlice;
+    const uint32_t slices = a.k / SL;
     const uint32_t slice = uint32_t(wave) * 64 + lane;
     const bool live = slice < slices;
     const uint32_t sl = live ? slice : 0;  // dead lanes read slice 0, contribute 0
@@ -171,30 +179,30 @@ __global__ __launch_bounds__(256) void vgemv_kernel(VArgs a)
 
     // Loads in the order they are needed: activations (from L2), then every
     // row's codes and group scale.
-    float x[kSlice];
-    const float4 *xp = reinterpret_cast<const float4 *>(a.x + sl * kSlice);
+    float x[SL];
+    const float4 *xp = reinterpret_cast<const float4 *>(a.x + sl * SL);
 #pragma unroll
-    for (int q = 0; q < kSlice / 4; ++q) {
+    for (int q = 0; q < SL / 4; ++q) {
         const float4 v = xp[q];
         x[4 * q] = v.x;
         x[4 * q + 1] = v.y;
         x[4 * q + 2] = v.z;
         x[4 * q + 3] = v.w;
     }
-    SliceCodes<F> codes[R];
+    unsigned codes[R][SC::N];
     float scale[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
         const uint32_t row = row0 + r < a.n ? row0 + r : a.n - 1;
-        codes[r] = load_slice<F>(a.codes + row * row_bytes + size_t(sl) * (kSlice / wpb));
-        const size_t si = size_t(row) * groups + sl / 4;
+        load_slice<SC::N, SC::EB>(a.codes + row * row_bytes + size_t(sl) * SC::bytes, codes[r]);
+        const size_t si = size_t(row) * groups + sl / LPG;
         scale[r] = a.scales16 ? __half2float(reinterpret_cast<const __half *>(a.scales16)[si])
                               : a.scales[si];
     }
     // Offset correction: sum x over the slice (ternary, INT8).
     float xsum = 0.0f;
 #pragma unroll
-    for (int j = 0; j < kSlice; ++j)
+    for (int j = 0; j < SL; ++j)
         xsum += x[j];
     xsum = F == Format::Ternary ? xsum : F == Format::Int8 ? 128.0f * xsum : 0.0f;
     if constexpr (F == Format::Nf4)
@@ -203,15 +211,17 @@ __global__ __launch_bounds__(256) void vgemv_kernel(VArgs a)
     float val[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        float v = slice_dot<F>(codes[r], x, pairs) - xsum;
-        // Group sum over the lane quad (all four lanes end equal), then the
-        // group's scale.
+        float v = slice_dot<F, SL, SC::N, SC::EB>(codes[r], x, pairs) - xsum;
+        // Group sum over its lanes (all end equal), then the group's scale.
         v = quad_add<0xB1>(v);  // quad_perm [1, 0, 3, 2]
         v = quad_add<0x4E>(v);  // quad_perm [2, 3, 0, 1]
-        v = live ? v * scale[r] : 0.0f;
-        // The wave's 16 groups.
 #pragma unroll
-        for (int off = 4; off < 64; off <<= 1)
+        for (int off = 4; off < LPG; off <<= 1)
+            v += __shfl_xor(v, off, 64);
+        v = live ? v * scale[r] : 0.0f;
+        // The wave's groups.
+#pragma unroll
+        for (int off = LPG; off < 64; off <<= 1)
             v += __shfl_xor(v, off, 64);
         val[r] = v;
     }
@@ -232,14 +242,20 @@ __global__ __launch_bounds__(256) void vgemv_kernel(VArgs a)
     }
 }
 
+template <Format F, int R, int SL>
+void launch_shape(hipStream_t stream, const VArgs &args)
+{
+    const unsigned waves = (args.k + 64 * SL - 1) / (64 * SL);
+    vgemv_kernel<F, R, SL><<<(args.n + R - 1) / R, 64 * waves, 0, stream>>>(args);
+}
+
 template <Format F>
 void launch_format_v(hipStream_t stream, const VArgs &args)
 {
-    const unsigned threads = 64 * ((args.k + kWaveK - 1) / kWaveK);
     if (args.n >= 2048)
-        vgemv_kernel<F, 4><<<(args.n + 3) / 4, threads, 0, stream>>>(args);
+        launch_shape<F, 4, 16>(stream, args);
     else
-        vgemv_kernel<F, 2><<<(args.n + 1) / 2, threads, 0, stream>>>(args);
+        launch_shape<F, 2, 8>(stream, args);
 }
 
 bool aligned16(const void *p)
