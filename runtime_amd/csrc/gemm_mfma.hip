@@ -93,6 +93,7 @@ __device__ __forceinline__ float wave_max(float v)
 // x * 2^-e (the lo half only where `xl` is non-null).  K is a multiple of
 // 128.
 constexpr int kSplitThreads = 256;
+constexpr uint32_t kSplitHeld = 8;  // float4 per lane: K <= 8192
 
 __global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__restrict__ x,
                                                               uint32_t k,
@@ -104,12 +105,28 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__res
     const uint32_t row = blockIdx.x, tid = threadIdx.x;
     const float4 *src = reinterpret_cast<const float4 *>(x + size_t(row) * k);
     const uint32_t vecs = k / 4;
+    // Rows of up to kSplitHeld vectors per lane stay in registers between the
+    // maximum and the split (one read of the row instead of two).
+    const bool held = vecs <= kSplitHeld * kSplitThreads;
+    float4 keep[kSplitHeld];
     // A non-finite value makes the row's maximum +inf.
     float mx = 0.0f;
-    for (uint32_t i = tid; i < vecs; i += kSplitThreads) {
-        const float4 v = src[i];
-        for (float c : {v.x, v.y, v.z, v.w})
-            mx = fmaxf(mx, isfinite(c) ? fabsf(c) : __builtin_inff());
+    if (held) {
+#pragma unroll
+        for (uint32_t u = 0; u < kSplitHeld; ++u) {
+            const uint32_t i = tid + u * kSplitThreads;
+            keep[u] = i < vecs ? src[i] : float4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+#pragma unroll
+        for (uint32_t u = 0; u < kSplitHeld; ++u)
+            for (float c : {keep[u].x, keep[u].y, keep[u].z, keep[u].w})
+                mx = fmaxf(mx, isfinite(c) ? fabsf(c) : __builtin_inff());
+    } else {
+        for (uint32_t i = tid; i < vecs; i += kSplitThreads) {
+            const float4 v = src[i];
+            for (float c : {v.x, v.y, v.z, v.w})
+                mx = fmaxf(mx, isfinite(c) ? fabsf(c) : __builtin_inff());
+        }
     }
     mx = wave_max(mx);
     if ((tid & 63) == 0)
@@ -125,8 +142,7 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__res
     typedef _Float16 h4 __attribute__((ext_vector_type(4)));
     h4 *dh = reinterpret_cast<h4 *>(xh + size_t(row) * k);
     h4 *dl = reinterpret_cast<h4 *>(xl + size_t(row) * k);
-    for (uint32_t i = tid; i < vecs; i += kSplitThreads) {
-        const float4 v = src[i];
+    auto split = [&](uint32_t i, const float4 &v) {
         h4 hi, lo;
         int t = 0;
         for (float c : {v.x, v.y, v.z, v.w}) {
@@ -138,6 +154,17 @@ __global__ __launch_bounds__(kSplitThreads) void split_kernel(const float *__res
         dh[i] = hi;
         if (xl)
             dl[i] = lo;
+    };
+    if (held) {
+#pragma unroll
+        for (uint32_t u = 0; u < kSplitHeld; ++u) {
+            const uint32_t i = tid + u * kSplitThreads;
+            if (i < vecs)
+                split(i, keep[u]);
+        }
+    } else {
+        for (uint32_t i = tid; i < vecs; i += kSplitThreads)
+            split(i, src[i]);
     }
 }
 
