@@ -38,6 +38,14 @@
 // 2440 for the 350M shape (1024 x 4608); back to back at 2048 x 8192, one
 // row, ternary 7.0 / 6.2 / 6.4 us, INT8 7.5 / 6.6 / 6.9, NF4 7.6 / 7.3 / 7.8.
 //
+// Norm variant (NF4, 2048 <= K <= 8192, one row, optionally segmented
+// into up to three weight streams): each lane adds the right-hand row to its
+// slice, the block sums the squares (its waves cover all of K), and the
+// activations become (s * reciprocal) * weight as in the reference's
+// add_row_rms_norm (backend-cpu/src/normalization_rotary.rs:223); block 0 also
+// writes the sum row.  It serves the LFM2 decode step's norm-fed NF4
+// products (conv in-projections, grouped q/k/v).
+//
 // Decode (crates/kernels-simd/src/lib.rs:31-57,113-130,145-183):
 //   ternary  level = c - 1, c = 2-bit field (code 3 gives +2, as on the CPU):
 //            sum (c - 1) x = sum c x - sum x, with c converted by byte;
@@ -73,6 +81,20 @@ struct VArgs {
     const uint16_t *scales16;  // binary16 copy of scales, or null
     float *out;  // [n]
     uint32_t n, k;
+    // Norm variant: x = ((x + right) * reciprocal) * weight, the sum row
+    // written to `side` (if set) by block 0.
+    const float *right, *weight;
+    float *side;
+    float epsilon;
+    // Norm variant: blocks [seg_first[i], seg_first[i + 1]) run stream i
+    // (0 segments: the single stream above).
+    uint32_t segments;
+    uint32_t seg_first[kMaxSegments];
+    const uint8_t *seg_codes[kMaxSegments];
+    const float *seg_scales[kMaxSegments];
+    const uint16_t *seg_scales16[kMaxSegments];
+    float *seg_out[kMaxSegments];
+    uint32_t seg_n[kMaxSegments];
 };
 
 // Code words of one row's SL-wide slice: N words of EB bytes each (a slice
@@ -156,14 +178,38 @@ __device__ __forceinline__ float quad_add(float v)
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <Format F, int R, int SL>
+template <Format F, int R, int SL, bool NORM>
 __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
 {
     using SC = Slice<F, SL>;
     constexpr int LPG = 128 / SL;  // lanes per 128-group
     __shared__ float2 pairs[F == Format::Nf4 ? 256 : 1];
     __shared__ float red[kMaxWaves][R];
+    __shared__ float squares_of[NORM ? kMaxWaves : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The block's weight stream (compile-time segment indices only: a
+    // dynamic index into the argument arrays would copy them to scratch).
+    uint32_t block = blockIdx.x;
+    const uint8_t *codes_of = a.codes;
+    const float *scales_of = a.scales;
+    const uint16_t *scales16_of = a.scales16;
+    float *out = a.out;
+    uint32_t n = a.n;
+    if constexpr (NORM) {
+        uint32_t first = 0;
+#pragma unroll
+        for (uint32_t sg = 0; sg < kMaxSegments; ++sg) {
+            if (sg < a.segments && block >= a.seg_first[sg]) {
+                codes_of = a.seg_codes[sg];
+                scales_of = a.seg_scales[sg];
+                scales16_of = a.seg_scales16[sg];
+                out = a.seg_out[sg];
+                n = a.seg_n[sg];
+                first = a.seg_first[sg];
+            }
+        }
+        block -= first;
+    }
     if constexpr (F == Format::Nf4) {
         for (int e = tid; e < 256; e += blockDim.x)
             pairs[e] = float2{kLevelsV[e & 15], kLevelsV[e >> 4]};
@@ -172,7 +218,7 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
     const uint32_t slice = uint32_t(wave) * 64 + lane;
     const bool live = slice < slices;
     const uint32_t sl = live ? slice : 0;  // dead lanes read slice 0, contribute 0
-    const uint32_t row0 = blockIdx.x * R;
+    const uint32_t row0 = block * R;
     constexpr int wpb = weights_per_byte(F);
     const size_t row_bytes = a.k / wpb;
     const uint32_t groups = a.k / 128;
@@ -189,15 +235,59 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
         x[4 * q + 2] = v.z;
         x[4 * q + 3] = v.w;
     }
+    if constexpr (NORM) {
+        // s = x + right over the slice, the row's squares summed over the
+        // block (its waves cover all of K), then the reference's
+        // (s * reciprocal) * weight.
+        const float4 *rp = reinterpret_cast<const float4 *>(a.right + sl * SL);
+        const float4 *wp = reinterpret_cast<const float4 *>(a.weight + sl * SL);
+        float w[SL];
+#pragma unroll
+        for (int q = 0; q < SL / 4; ++q) {
+            const float4 v = rp[q], u = wp[q];
+            x[4 * q] += v.x;
+            x[4 * q + 1] += v.y;
+            x[4 * q + 2] += v.z;
+            x[4 * q + 3] += v.w;
+            w[4 * q] = u.x;
+            w[4 * q + 1] = u.y;
+            w[4 * q + 2] = u.z;
+            w[4 * q + 3] = u.w;
+        }
+        float squares = 0.0f;
+#pragma unroll
+        for (int j = 0; j < SL; ++j)
+            squares += x[j] * x[j];
+        squares = live ? squares : 0.0f;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1)
+            squares += __shfl_xor(squares, off, 64);
+        if (lane == 0)
+            squares_of[wave] = squares;
+        if (blockIdx.x == 0 && live && a.side) {
+            float4 *sp = reinterpret_cast<float4 *>(a.side + sl * SL);
+#pragma unroll
+            for (int q = 0; q < SL / 4; ++q)
+                sp[q] = float4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+        }
+        __syncthreads();
+        float total = 0.0f;
+        for (int wv = 0; wv < int(blockDim.x >> 6); ++wv)
+            total += squares_of[wv];
+        const float reciprocal = 1.0f / sqrtf(total / float(a.k) + a.epsilon);
+#pragma unroll
+        for (int j = 0; j < SL; ++j)
+            x[j] = (x[j] * reciprocal) * w[j];
+    }
     unsigned codes[R][SC::N];
     float scale[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-        const uint32_t row = row0 + r < a.n ? row0 + r : a.n - 1;
-        load_slice<SC::N, SC::EB>(a.codes + row * row_bytes + size_t(sl) * SC::bytes, codes[r]);
+        const uint32_t row = row0 + r < n ? row0 + r : n - 1;
+        load_slice<SC::N, SC::EB>(codes_of + row * row_bytes + size_t(sl) * SC::bytes, codes[r]);
         const size_t si = size_t(row) * groups + sl / LPG;
-        scale[r] = a.scales16 ? __half2float(reinterpret_cast<const __half *>(a.scales16)[si])
-                              : a.scales[si];
+        scale[r] = scales16_of ? __half2float(reinterpret_cast<const __half *>(scales16_of)[si])
+                              : scales_of[si];
     }
     // Offset correction: sum x over the slice (ternary, INT8).
     float xsum = 0.0f;
@@ -237,8 +327,8 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
         for (int w = 1; w < waves; ++w)
             sum += red[w][tid];
         const uint32_t row = row0 + tid;
-        if (row < a.n)
-            a.out[row] = sum;
+        if (row < n)
+            out[row] = sum;
     }
 }
 
@@ -246,7 +336,15 @@ template <Format F, int R, int SL>
 void launch_shape(hipStream_t stream, const VArgs &args)
 {
     const unsigned waves = (args.k + 64 * SL - 1) / (64 * SL);
-    vgemv_kernel<F, R, SL><<<(args.n + R - 1) / R, 64 * waves, 0, stream>>>(args);
+    vgemv_kernel<F, R, SL, false><<<(args.n + R - 1) / R, 64 * waves, 0, stream>>>(args);
+}
+
+// The norm variant: four rows per block and 16-wide slices; `blocks`
+// covers every segment (each a multiple of four rows).
+void launch_norm(hipStream_t stream, const VArgs &args, unsigned blocks)
+{
+    const unsigned waves = (args.k + 64 * 16 - 1) / (64 * 16);
+    vgemv_kernel<Format::Nf4, 4, 16, true><<<blocks, 64 * waves, 0, stream>>>(args);
 }
 
 template <Format F>
@@ -265,8 +363,66 @@ bool aligned16(const void *p)
 
 }  // namespace
 
+namespace {
+
+// NF4 products whose activations are add + RMS norm of two rows, at
+// 2048 <= K <= 8192 (the LFM2-1.2B conv in-projections and the grouped
+// q/k/v launch): the norm variant.  Against the matrix-core GEMV with its
+// LDS norm prologue, 1.2B-shape decode 1631 -> 1656 tok/s; at one plain row
+// NF4 6144 x 2048 took 6.3 against 7.5-7.7 us, while the other formats at
+// K <= 2048 were as fast or faster on the matrix cores.
+constexpr uint32_t kNormMinK = 2048;
+
+bool try_norm(hipStream_t stream, const PackedCall &call)
+{
+    const XForm &t = call.xform;
+    if (call.format != Format::Nf4 || t.kind != XKind::AddRms || call.separate_prologue ||
+        call.epilogue != Epilogue::Single || call.m != 1 || call.k < kNormMinK ||
+        call.k > kMaxK || call.k % 128 || !t.a || !t.b || !t.w || !aligned16(t.a) ||
+        !aligned16(t.b) || !aligned16(t.w) || (t.side && !aligned16(t.side)))
+        return false;
+    VArgs args{};
+    args.x = t.a;
+    args.right = t.b;
+    args.weight = t.w;
+    args.side = t.side;
+    args.epsilon = t.epsilon;
+    args.k = call.k;
+    unsigned blocks = 0;
+    if (call.segments) {
+        for (uint32_t i = 0; i < call.segments; ++i) {
+            if (call.seg_n[i] == 0 || call.seg_n[i] % 4 || !call.seg[i].codes ||
+                !call.seg[i].scales)
+                return false;
+            args.seg_first[i] = blocks;
+            args.seg_codes[i] = call.seg[i].codes;
+            args.seg_scales[i] = call.seg[i].scales;
+            args.seg_scales16[i] = call.seg[i].scales16;
+            args.seg_out[i] = call.seg_out[i];
+            args.seg_n[i] = call.seg_n[i];
+            blocks += call.seg_n[i] / 4;
+        }
+        args.segments = call.segments;
+    } else {
+        if (call.n == 0 || call.n > kMaxRows || !call.a.codes || !call.a.scales)
+            return false;
+        args.codes = call.a.codes;
+        args.scales = call.a.scales;
+        args.scales16 = call.a.scales16;
+        args.out = call.out_a;
+        args.n = call.n;
+        blocks = (call.n + 3) / 4;
+    }
+    launch_norm(stream, args, blocks);
+    return true;
+}
+
+}  // namespace
+
 bool try_vgemv(hipStream_t stream, const PackedCall &call)
 {
+    if (try_norm(stream, call))
+        return true;
     const float *x = call.xform.kind == XKind::Plain ? call.x : nullptr;
     if (call.separate_prologue || call.segments || call.epilogue != Epilogue::Single ||
         call.m != 1 || call.k < kMinK || call.k > kMaxK || call.k % 128 || call.n == 0 ||
