@@ -424,8 +424,12 @@ bool try_vgemv(hipStream_t stream, const PackedCall &call)
     if (try_norm(stream, call))
         return true;
     const float *x = call.xform.kind == XKind::Plain ? call.x : nullptr;
+    // NF4 from K = 2048 (its matrix-core GEMV carries the table decode and
+    // hi/lo products): 1.2B-shape decode 1662 -> 1667 tok/s, op by op 1297 ->
+    // 1320, where the 2048 x 2048 and 6144 x 2048 products move here.
+    const uint32_t min_k = call.format == Format::Nf4 ? kNormMinK : kMinK;
     if (call.separate_prologue || call.segments || call.epilogue != Epilogue::Single ||
-        call.m != 1 || call.k < kMinK || call.k > kMaxK || call.k % 128 || call.n == 0 ||
+        call.m != 1 || call.k < min_k || call.k > kMaxK || call.k % 128 || call.n == 0 ||
         call.n > kMaxRows || !call.a.codes || !call.a.scales || !x || !aligned16(x))
         return false;
     VArgs args{};
