@@ -1,5 +1,6 @@
 // f32 vector-ALU decode GEMV for wide contractions: one activation row,
-// 4096 <= K <= 8192 (the FFN down projections, 2048 x 8192 and 1024 x 4608).
+// 4096 <= K <= 8192 (the FFN down projections, 2048 x 8192 and 1024 x 4608),
+// NF4 from K = 2048 (the LFM2-1.2B attention and convolution projections).
 //
 // out[b, n] = sum_g scale[n, g] * sum_{k in g} x[b, k] * level(code[n, k])
 // in f32, the reference's group-then-scale order
