@@ -82,8 +82,8 @@ struct VArgs {
     const uint16_t *scales16;  // binary16 copy of scales, or null
     float *out;  // [n]
     uint32_t n, k;
-    // Norm variant: x = ((x + right) * reciprocal) * weight, the sum row
-    // written to `side` (if set) by block 0.
+    // Norm variant: x = ((x + right) * reciprocal) * weight (right may be
+    // null), the sum row written to `side` (if set) by block 0.
     const float *right, *weight;
     float *side;
     float epsilon;
@@ -179,7 +179,7 @@ __device__ __forceinline__ float quad_add(float v)
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <Format F, int R, int SL, bool NORM>
+template <Format F, int R, int SL, int NORM>
 __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
 {
     using SC = Slice<F, SL>;
@@ -240,16 +240,21 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
         // s = x + right over the slice, the row's squares summed over the
         // block (its waves cover all of K), then the reference's
         // (s * reciprocal) * weight.
+        // NORM == 2: no right-hand row (the first layer's block input); a
+        // separate instantiation, so that no load waits behind a branch.
         const float4 *rp = reinterpret_cast<const float4 *>(a.right + sl * SL);
         const float4 *wp = reinterpret_cast<const float4 *>(a.weight + sl * SL);
         float w[SL];
 #pragma unroll
         for (int q = 0; q < SL / 4; ++q) {
-            const float4 v = rp[q], u = wp[q];
-            x[4 * q] += v.x;
-            x[4 * q + 1] += v.y;
-            x[4 * q + 2] += v.z;
-            x[4 * q + 3] += v.w;
+            const float4 u = wp[q];
+            if constexpr (NORM == 1) {
+                const float4 v = rp[q];
+                x[4 * q] += v.x;
+                x[4 * q + 1] += v.y;
+                x[4 * q + 2] += v.z;
+                x[4 * q + 3] += v.w;
+            }
             w[4 * q] = u.x;
             w[4 * q + 1] = u.y;
             w[4 * q + 2] = u.z;
@@ -337,7 +342,7 @@ template <Format F, int R, int SL>
 void launch_shape(hipStream_t stream, const VArgs &args)
 {
     const unsigned waves = (args.k + 64 * SL - 1) / (64 * SL);
-    vgemv_kernel<F, R, SL, false><<<(args.n + R - 1) / R, 64 * waves, 0, stream>>>(args);
+    vgemv_kernel<F, R, SL, 0><<<(args.n + R - 1) / R, 64 * waves, 0, stream>>>(args);
 }
 
 // The norm variant: four rows per block and 16-wide slices; `blocks`
@@ -345,7 +350,10 @@ void launch_shape(hipStream_t stream, const VArgs &args)
 void launch_norm(hipStream_t stream, const VArgs &args, unsigned blocks)
 {
     const unsigned waves = (args.k + 64 * 16 - 1) / (64 * 16);
-    vgemv_kernel<Format::Nf4, 4, 16, true><<<blocks, 64 * waves, 0, stream>>>(args);
+    if (args.right)
+        vgemv_kernel<Format::Nf4, 4, 16, 1><<<blocks, 64 * waves, 0, stream>>>(args);
+    else
+        vgemv_kernel<Format::Nf4, 4, 16, 2><<<blocks, 64 * waves, 0, stream>>>(args);
 }
 
 template <Format F>
@@ -379,8 +387,8 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
     const XForm &t = call.xform;
     if (call.format != Format::Nf4 || t.kind != XKind::AddRms || call.separate_prologue ||
         call.epilogue != Epilogue::Single || call.m != 1 || call.k < kNormMinK ||
-        call.k > kMaxK || call.k % 128 || !t.a || !t.b || !t.w || !aligned16(t.a) ||
-        !aligned16(t.b) || !aligned16(t.w) || (t.side && !aligned16(t.side)))
+        call.k > kMaxK || call.k % 128 || !t.a || !t.w || !aligned16(t.a) ||
+        (t.b && !aligned16(t.b)) || !aligned16(t.w) || (t.side && !aligned16(t.side)))
         return false;
     VArgs args{};
     args.x = t.a;
