@@ -1,6 +1,7 @@
 // f32 vector-ALU decode GEMV for wide contractions: one activation row,
 // 4096 <= K <= 8192 (the FFN down projections, 2048 x 8192 and 1024 x 4608),
-// NF4 from K = 2048 (the LFM2-1.2B attention and convolution projections).
+// NF4 from K = 2048 (the LFM2-1.2B attention and convolution projections),
+// ternary below 2048 rows from K = 1024 (the LFM2-350M ones).
 //
 // out[b, n] = sum_g scale[n, g] * sum_{k in g} x[b, k] * level(code[n, k])
 // in f32, the reference's group-then-scale order
@@ -39,13 +40,13 @@
 // 2440 for the 350M shape (1024 x 4608); back to back at 2048 x 8192, one
 // row, ternary 7.0 / 6.2 / 6.4 us, INT8 7.5 / 6.6 / 6.9, NF4 7.6 / 7.3 / 7.8.
 //
-// Norm variant (NF4, 2048 <= K <= 8192, one row, optionally segmented
-// into up to three weight streams): each lane adds the right-hand row to its
+// Norm variant (NF4 at 2048 <= K <= 8192, ternary from K = 1024; one row,
+// optionally segmented into up to three weight streams): each lane adds the right-hand row to its
 // slice, the block sums the squares (its waves cover all of K), and the
 // activations become (s * reciprocal) * weight as in the reference's
 // add_row_rms_norm (backend-cpu/src/normalization_rotary.rs:223); block 0 also
-// writes the sum row.  It serves the LFM2 decode step's norm-fed NF4
-// products (conv in-projections, grouped q/k/v).
+// writes the sum row.  It serves the LFM2 decode step's norm-fed NF4 and
+// ternary products (conv in-projections, grouped q/k/v).
 //
 // Decode (crates/kernels-simd/src/lib.rs:31-57,113-130,145-183):
 //   ternary  level = c - 1, c = 2-bit field (code 3 gives +2, as on the CPU):
@@ -348,13 +349,14 @@ void launch_shape(hipStream_t stream, const VArgs &args)
 // The norm variant: four rows per block and 8-wide slices (16-wide measured
 // 1665 against 1681 tok/s for 1.2B-shape decode); `blocks` covers every
 // segment (each a multiple of four rows).
+template <Format F>
 void launch_norm(hipStream_t stream, const VArgs &args, unsigned blocks)
 {
     const unsigned waves = (args.k + 64 * 8 - 1) / (64 * 8);
     if (args.right)
-        vgemv_kernel<Format::Nf4, 4, 8, 1><<<blocks, 64 * waves, 0, stream>>>(args);
+        vgemv_kernel<F, 4, 8, 1><<<blocks, 64 * waves, 0, stream>>>(args);
     else
-        vgemv_kernel<Format::Nf4, 4, 8, 2><<<blocks, 64 * waves, 0, stream>>>(args);
+        vgemv_kernel<F, 4, 8, 2><<<blocks, 64 * waves, 0, stream>>>(args);
 }
 
 template <Format F>
@@ -375,19 +377,22 @@ bool aligned16(const void *p)
 
 namespace {
 
-// NF4 products whose activations are add + RMS norm of two rows, at
+// Products whose activations are add + RMS norm of two rows: NF4 at
 // 2048 <= K <= 8192 (the LFM2-1.2B conv in-projections and the grouped
-// q/k/v launch): the norm variant.  Against the matrix-core GEMV with its
-// LDS norm prologue, 1.2B-shape decode 1631 -> 1656 tok/s; at one plain row
-// NF4 6144 x 2048 took 6.3 against 7.5-7.7 us, while the other formats at
-// K <= 2048 were as fast or faster on the matrix cores.
+// q/k/v launch) and ternary from K = 1024 (the same roles at the 350M
+// shape) take the norm variant.  Against the matrix-core GEMV with its norm
+// prologue: 1.2B-shape decode 1631 -> 1656 tok/s (NF4, LDS prologue), 350M
+// 2450 -> 2499 (ternary, register prologue).  INT8 stays on the matrix
+// cores, which were as fast or faster at one plain row for K <= 2048.
 constexpr uint32_t kNormMinK = 2048;
+constexpr uint32_t kTernaryMinK = 1024;
 
 bool try_norm(hipStream_t stream, const PackedCall &call)
 {
     const XForm &t = call.xform;
-    if (call.format != Format::Nf4 || t.kind != XKind::AddRms || call.separate_prologue ||
-        call.epilogue != Epilogue::Single || call.m != 1 || call.k < kNormMinK ||
+    const uint32_t min_k = call.format == Format::Ternary ? kTernaryMinK : kNormMinK;
+    if (call.format == Format::Int8 || t.kind != XKind::AddRms || call.separate_prologue ||
+        call.epilogue != Epilogue::Single || call.m != 1 || call.k < min_k ||
         call.k > kMaxK || call.k % 128 || !t.a || !t.w || !aligned16(t.a) ||
         (t.b && !aligned16(t.b)) || !aligned16(t.w) || (t.side && !aligned16(t.side)))
         return false;
@@ -423,7 +428,10 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
         args.n = call.n;
         blocks = (call.n + 3) / 4;
     }
-    launch_norm(stream, args, blocks);
+    if (call.format == Format::Ternary)
+        launch_norm<Format::Ternary>(stream, args, blocks);
+    else
+        launch_norm<Format::Nf4>(stream, args, blocks);
     return true;
 }
 
@@ -437,7 +445,13 @@ bool try_vgemv(hipStream_t stream, const PackedCall &call)
     // NF4 from K = 2048 (its matrix-core GEMV carries the table decode and
     // hi/lo products): 1.2B-shape decode 1662 -> 1667 tok/s, op by op 1297 ->
     // 1320, where the 2048 x 2048 and 6144 x 2048 products move here.
-    const uint32_t min_k = call.format == Format::Nf4 ? kNormMinK : kMinK;
+    // Ternary from K = 1024 below 2048 rows (the 350M-shape output
+    // projections, 1024 x 1024): 350M decode 2499 -> 2582 tok/s; at 2048 x
+    // 2048 and 4608 x 1024 the matrix cores stayed faster (4.2 against
+    // 4.7-4.9 us).
+    const uint32_t min_k = call.format == Format::Nf4 ? kNormMinK
+                           : call.format == Format::Ternary && call.n < 2048 ? kTernaryMinK
+                                                                            : kMinK;
     if (call.separate_prologue || call.segments || call.epilogue != Epilogue::Single ||
         call.m != 1 || call.k < min_k || call.k > kMaxK || call.k % 128 || call.n == 0 ||
         call.n > kMaxRows || !call.a.codes || !call.a.scales || !x || !aligned16(x))

@@ -256,12 +256,13 @@ def test_ternary_reserved_code_decodes_as_plus_two(backend, path):
 
 # --- wide contractions at one or two rows (f32 vector GEMV) ------------------------
 # On the auto path one plain activation row with 4096 <= k <= 8192 (NF4 from
-# k = 2048) and n <= 8192 runs the f32 vector GEMV (lanes own 16- or 8-wide k
+# k = 2048, ternary below 2048 rows from k = 1024) and n <= 8192 runs the f32
+# vector GEMV (lanes own 16- or 8-wide k
 # slices, waves splitting K); two rows, the other paths and SwiGLU-formed
 # activations run the matrix-core or FMA kernels on the same cases.
 
 WIDE_K_SHAPES = [(2048, 8192), (1024, 4608), (1001, 4096), (77, 8192), (8192, 4224), (3, 8192),
-                 (1001, 2048), (6144, 3072)]
+                 (1001, 2048), (6144, 3072), (1001, 1024), (2048, 1152)]
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
