@@ -31,7 +31,9 @@
 // partial sums add over the lane quad (DPP) and shuffles, the sum is scaled,
 // and the groups add across the wave (shuffles) and across the block's waves
 // (LDS, in wave order).  A block holds R rows (R = 4 from 2048 rows, else
-// 2: at least 512 blocks; 2048 x 8192 with R = 1, 2, 8 took 10.2, 7.2, 8.8
+// 2, at least 512 blocks; ternary rows below 2048 at K < 4096 take one and
+// the norm variant four for NF4, two for ternary, as measured in the decode
+// chain; 2048 x 8192 with R = 1, 2, 8 took 10.2, 7.2, 8.8
 // us against 7.05, 1024 x 4608 with R = 4 5.3 against 4.2) and
 // ceil(K / (64 SL)) waves.  SL = 16 from 2048 rows, else 8: shorter slices
 // halve each lane's dependent arithmetic and spread it over more waves.
@@ -346,22 +348,34 @@ void launch_shape(hipStream_t stream, const VArgs &args)
     vgemv_kernel<F, R, SL, 0><<<(args.n + R - 1) / R, 64 * waves, 0, stream>>>(args);
 }
 
-// The norm variant: four rows per block and 8-wide slices (16-wide measured
-// 1665 against 1681 tok/s for 1.2B-shape decode); `blocks` covers every
-// segment (each a multiple of four rows).
+// The norm variant: 8-wide slices (16-wide measured 1665 against 1681 tok/s
+// for 1.2B-shape decode) and norm_rows(F) rows per block (ternary 2: 350M
+// decode 2583 -> 2635 against 4); `blocks` covers every segment (each a
+// multiple of that many rows).
+constexpr uint32_t norm_rows(Format f)
+{
+    return f == Format::Ternary ? 2 : 4;
+}
+
 template <Format F>
 void launch_norm(hipStream_t stream, const VArgs &args, unsigned blocks)
 {
+    constexpr int R = int(norm_rows(F));
     const unsigned waves = (args.k + 64 * 8 - 1) / (64 * 8);
     if (args.right)
-        vgemv_kernel<F, 4, 8, 1><<<blocks, 64 * waves, 0, stream>>>(args);
+        vgemv_kernel<F, R, 8, 1><<<blocks, 64 * waves, 0, stream>>>(args);
     else
-        vgemv_kernel<F, 4, 8, 2><<<blocks, 64 * waves, 0, stream>>>(args);
+        vgemv_kernel<F, R, 8, 2><<<blocks, 64 * waves, 0, stream>>>(args);
 }
 
 template <Format F>
 void launch_format_v(hipStream_t stream, const VArgs &args)
 {
+    // Ternary rows below 2048 at K < 4096 (the 350M-shape output
+    // projections): one row per block (350M decode 2583 -> 2600 against two;
+    // four measured 2516).
+    if (F == Format::Ternary && args.n < 2048 && args.k < 4096)
+        return launch_shape<F, 1, 8>(stream, args);
     if (args.n >= 2048)
         launch_shape<F, 4, 16>(stream, args);
     else
@@ -396,6 +410,7 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
         call.k > kMaxK || call.k % 128 || !t.a || !t.w || !aligned16(t.a) ||
         (t.b && !aligned16(t.b)) || !aligned16(t.w) || (t.side && !aligned16(t.side)))
         return false;
+    const uint32_t rows = norm_rows(call.format);
     VArgs args{};
     args.x = t.a;
     args.right = t.b;
@@ -406,7 +421,7 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
     unsigned blocks = 0;
     if (call.segments) {
         for (uint32_t i = 0; i < call.segments; ++i) {
-            if (call.seg_n[i] == 0 || call.seg_n[i] % 4 || !call.seg[i].codes ||
+            if (call.seg_n[i] == 0 || call.seg_n[i] % rows || !call.seg[i].codes ||
                 !call.seg[i].scales)
                 return false;
             args.seg_first[i] = blocks;
@@ -415,7 +430,7 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
             args.seg_scales16[i] = call.seg[i].scales16;
             args.seg_out[i] = call.seg_out[i];
             args.seg_n[i] = call.seg_n[i];
-            blocks += call.seg_n[i] / 4;
+            blocks += call.seg_n[i] / rows;
         }
         args.segments = call.segments;
     } else {
@@ -426,7 +441,7 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
         args.scales16 = call.a.scales16;
         args.out = call.out_a;
         args.n = call.n;
-        blocks = (call.n + 3) / 4;
+        blocks = (call.n + rows - 1) / rows;
     }
     if (call.format == Format::Ternary)
         launch_norm<Format::Ternary>(stream, args, blocks);
