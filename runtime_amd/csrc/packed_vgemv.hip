@@ -350,8 +350,9 @@ void launch_shape(hipStream_t stream, const VArgs &args)
 
 // The norm variant: 8-wide slices (16-wide measured 1665 against 1681 tok/s
 // for 1.2B-shape decode) and norm_rows(F) rows per block (ternary 2: 350M
-// decode 2583 -> 2635 against 4); `blocks` covers every segment (each a
-// multiple of that many rows).
+// decode 2583 -> 2635 against 4; NF4 keeps 4, 1679 against 1654 tok/s for
+// the 1.2B shape with 2); `blocks` covers every segment (each a multiple of
+// that many rows).
 constexpr uint32_t norm_rows(Format f)
 {
     return f == Format::Ternary ? 2 : 4;
