@@ -155,13 +155,14 @@ mfh_status mfh_identity(const mfh_ctx *ctx, mfh_backend_identity *out);
 /* InferenceOps::capabilities (inference.rs:47). */
 mfh_status mfh_capabilities(const mfh_ctx *ctx, mfh_backend_capabilities *out);
 /* InferenceOps::resource_report (inference.rs:48).  Counts physical bytes,
- * like the reference's wgpu backend (backend-wgpu/src/lib.rs:340-370): each
- * live buffer's device block and its backend-private derived copies (the
- * binary16 scale shadow, repacked code tiles, tiled scales) under the
- * buffer's class; context scratch and idle pooled blocks under scratch;
- * pinned staging of unpolled readbacks as pending bytes.  The sum is the
- * context's device footprint plus that staging, and every allocation that
- * would take it past max_total_bytes fails with MFH_RESOURCE_LIMIT. */
+ * like the reference's wgpu backend (backend-wgpu/src/lib.rs:340-370): the
+ * byte extent of each live buffer and of its backend-private derived copies
+ * (the binary16 scale shadow, repacked code tiles, tiled scales) under the
+ * buffer's class; the rest of the device memory the context holds (pool
+ * bucket slack, context scratch, idle pooled blocks) under scratch; pinned
+ * staging of unpolled readbacks as pending bytes.  The sum is the context's
+ * device footprint plus that staging, and every allocation that would take
+ * it past max_total_bytes fails with MFH_RESOURCE_LIMIT. */
 mfh_status mfh_resource_report(const mfh_ctx *ctx, mfh_report *out);
 /* InferenceOps::peak_accounted_bytes (inference.rs:52-56): the highest
  * such total since mfh_create. */

@@ -7,6 +7,7 @@
 #include <initializer_list>
 #include <map>
 #include <memory>
+#include <unordered_map>
 #include <unordered_set>
 #include <vector>
 
@@ -66,12 +67,15 @@ struct mfh_ctx {
     hipStream_t stream = nullptr;
     mfh_backend_identity identity{};
     mfh_limits limits{};
-    // Device bytes held per allocation class: each live buffer's block plus
-    // its backend-private derived copies (binary16 shadow, repacked tiles,
-    // tiled scales), charged to the buffer's class.  Context scratch and
-    // idle pooled blocks are the rest of the pool's reserve and count as
-    // scratch.
+    // Logical device bytes held per allocation class: each live buffer's
+    // byte extent plus the sizes of its backend-private derived copies
+    // (binary16 shadow, repacked tiles, tiled scales), charged to the
+    // buffer's class.  The rest of the pool's reserve (bucket slack, context
+    // scratch, idle pooled blocks) counts as scratch.
     uint64_t held_by_class[4] = {0, 0, 0, 0};
+    // The logical bytes charged for each pool block a buffer holds (its own
+    // storage or a derived copy), uncharged when the block is released.
+    std::unordered_map<void *, uint64_t> charged;
     uint64_t peak_bytes = 0;
     uint64_t pending_result_bytes = 0;
     uint32_t pending_operations = 0;
@@ -167,16 +171,25 @@ mfh_status check_operation(mfh_ctx *ctx, mfh_operation op);
 // Drop derived copies of a buffer whose contents an operation overwrites.
 void mark_written(mfh_buf *buf);
 
-// Make the context's device current for the scope of one call.
+// Make the context's device current for the scope of one call.  When it
+// already is (the common case: one device per process), the call costs one
+// hipGetDevice and nothing is restored.
 struct DeviceGuard {
-    int previous = 0;
+    int previous = -1;
     explicit DeviceGuard(int device)
     {
-        (void)hipGetDevice(&previous);
-        if (previous != device)
+        int current = device;
+        (void)hipGetDevice(&current);
+        if (current != device) {
+            previous = current;
             (void)hipSetDevice(device);
+        }
     }
-    ~DeviceGuard() { (void)hipSetDevice(previous); }
+    ~DeviceGuard()
+    {
+        if (previous >= 0)
+            (void)hipSetDevice(previous);
+    }
 };
 
 inline bool same_shape(const mfh_buf *a, const mfh_buf *b)

@@ -988,7 +988,10 @@ mfh_status mfl_load_safetensors(mfl_model *m, const mfs_file *file)
     for (size_t i = 0; i < mfs_tensor_count(file); ++i)
         if (!consumed.count(mfs_tensor_name(file, i)))
             return fail(c, MFH_UNEXPECTED_TENSOR, "undeclared tensor is present");
-    // 2. Upload and attach.
+    // 2. Upload every role, with its private tile copies, before attaching
+    // any: a failure here releases what this load uploaded and leaves the
+    // model's weights as they were.
+    std::vector<std::unique_ptr<Owned>> staged;  // [tensor, scales or null] per role
     for (size_t r = 0; r < plan.size(); ++r) {
         const RolePlan &rp = plan[r];
         mfh_status s;
@@ -1002,20 +1005,42 @@ mfh_status mfl_load_safetensors(mfl_model *m, const mfs_file *file)
                 t->buf->dims[1] = rp.dims[2];
                 t->buf->dims[2] = 0;
             }
-            if ((s = mfl_set_weight(m, rp.role, rp.layer, t->buf, nullptr)))
-                return s;
-            m->loaded.push_back(std::move(t));
+            staged.push_back(std::move(t));
+            staged.push_back(nullptr);
         } else {
             auto codes = std::make_unique<Owned>(), scales = std::make_unique<Owned>();
             if ((s = mfs_upload_packed(c, file, rp.name.c_str(), MFH_CLASS_WEIGHT, &codes->buf,
                                        &scales->buf)))
                 return load_error(c, s);
-            if ((s = mfl_set_weight(m, rp.role, rp.layer, codes->buf, scales->buf)))
+            if ((s = prepare_packed(c, codes->buf, scales->buf)))
                 return s;
-            m->loaded.push_back(std::move(codes));
-            m->loaded.push_back(std::move(scales));
+            staged.push_back(std::move(codes));
+            staged.push_back(std::move(scales));
         }
     }
+    // 3. Attach.  Step 1 checked every role against the layer kinds and the
+    // copies are prepared, so this cannot fail short of a broken plan; if it
+    // does, the previous weights are put back.
+    const Weight embedding = m->embedding, embedding_norm = m->embedding_norm;
+    const std::vector<LayerWeights> layers = m->layers;
+    for (size_t r = 0; r < plan.size(); ++r) {
+        const Owned *t = staged[2 * r].get(), *sc = staged[2 * r + 1].get();
+        const mfh_status s =
+            mfl_set_weight(m, plan[r].role, plan[r].layer, t->buf, sc ? sc->buf : nullptr);
+        if (s) {
+            m->embedding = embedding;
+            m->embedding_norm = embedding_norm;
+            m->layers = layers;
+            return s;
+        }
+    }
+    // Every role of the plan now holds this load's buffers, so an earlier
+    // load's are released (into the stream-ordered pool: passes already
+    // queued still read them safely).
+    m->loaded.clear();
+    for (auto &o : staged)
+        if (o)
+            m->loaded.push_back(std::move(o));
     return MFH_OK;
 }
 

@@ -136,8 +136,10 @@ mfh_status acquire(mfh_ctx *ctx, size_t bytes, void **out, size_t *capacity)
 mfh_status acquire_for(mfh_ctx *ctx, mfh_buf *owner, size_t bytes, void **out, size_t *capacity)
 {
     mfh_status s = acquire(ctx, bytes, out, capacity);
-    if (!s)
-        ctx->held_by_class[owner->cls] += *capacity;
+    if (!s) {
+        ctx->held_by_class[owner->cls] += bytes;
+        ctx->charged[*out] = bytes;
+    }
     return s;
 }
 
@@ -145,8 +147,13 @@ void release_block(mfh_ctx *ctx, mfh_buf *owner, void *ptr, size_t capacity)
 {
     if (!ptr)
         return;
-    if (owner)
-        ctx->held_by_class[owner->cls] -= capacity;
+    if (owner) {
+        auto it = ctx->charged.find(ptr);
+        if (it != ctx->charged.end()) {
+            ctx->held_by_class[owner->cls] -= it->second;
+            ctx->charged.erase(it);
+        }
+    }
     ctx->pool->release(ptr, capacity);
 }
 
@@ -339,7 +346,10 @@ mfh_status make_buffer(mfh_ctx *ctx, const uint64_t *dims, uint32_t rank, mfh_dt
         }
     }
     ctx->live_buffers.insert(buf);
-    ctx->held_by_class[cls] += buf->capacity;
+    if (buf->dev) {
+        ctx->held_by_class[cls] += bytes;
+        ctx->charged[buf->dev] = bytes;
+    }
     *out = buf;
     return MFH_OK;
 }
@@ -481,9 +491,11 @@ mfh_status mfh_resource_report(const mfh_ctx *ctx, mfh_report *out)
 {
     if (!ctx || !out)
         return MFH_INVALID_ARGUMENT;
-    // Every pooled device byte is reported once: live buffers and their
-    // derived copies under the buffer's class, everything else the pool
-    // holds (context scratch, idle blocks) as scratch.  The total is the
+    // Every pooled device byte is reported once: the logical bytes of live
+    // buffers and their derived copies under the buffer's class, everything
+    // else the pool holds (bucket slack, context scratch, idle blocks) as
+    // scratch, as backend-wgpu/src/lib.rs:340-370 charges byte extents per
+    // class and the physical remainder as scratch.  The total is the
     // context's device footprint plus pending readback staging.
     const uint64_t *held = ctx->held_by_class;
     const uint64_t attributed = held[0] + held[1] + held[2] + held[3];
@@ -800,9 +812,17 @@ mfh_status mfh_read_f32_async(mfh_ctx *ctx, const mfh_buf *buf, mfh_readback **o
         return s;
     DeviceGuard guard(ctx->device);
     // The staging the completion owns until it is polled counts against the
-    // total limit like device blocks do.
-    const uint64_t owned = ctx->pool->reserved() + ctx->pending_result_bytes;
-    if (owned + buf->bytes > ctx->limits.max_total_bytes)
+    // total limit like device blocks do.  As for a device allocation, the
+    // idle pooled blocks are returned to the driver before a request that
+    // does not fit is refused (backend-wgpu/src/device.rs:657-676 clears its
+    // free pools before the budget check of readback staging).
+    auto fits = [&] {
+        const uint64_t owned = ctx->pool->reserved() + ctx->pending_result_bytes;
+        return owned + buf->bytes >= owned && owned + buf->bytes <= ctx->limits.max_total_bytes;
+    };
+    if (!fits())
+        evict(ctx);
+    if (!fits())
         return fail(ctx, MFH_RESOURCE_LIMIT, "allocation exceeds configured total resource limit");
     auto *rb = new (std::nothrow) mfh_readback();
     if (!rb)

@@ -23,7 +23,7 @@ from dense_fixtures import (close, conv_operands, f32, gqa_operands, head_rms_op
                             rotary_operands, sentinels)
 from runtime_amd.backend import (CacheLength, ExecutorError, GatedShortConvSpec, GqaSpec,
                                  PackedHeadSpec, RectCopy2d, RotarySpec)
-from tests.conftest import assert_close
+from tests.conftest import assert_close, max_rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -270,6 +270,27 @@ def test_causal_gqa(backend, tokens, start, cap, qh, kvh, d):
     out, kc2, vc2, length = run_gqa(backend, q, k, v, kc, vc, start, qh, kvh, d)
     want, want_kc, want_vc, want_len = oracle.causal_gqa(q, k, v, kc, vc, start, qh, kvh, d)
     assert length == want_len == start + tokens
+    assert_close(out, want)
+    assert bits_equal(kc2, want_kc) and bits_equal(vc2, want_vc)
+
+
+def test_causal_gqa_prefill_at_2048_tokens(backend):
+    """The 1.2B-shape prefill attention at its full depth: 2048 tokens of
+    32 query / 8 key-value heads of width 64 on an empty cache, against the
+    score-cached oracle (bitwise equal to the literal restatement, since
+    gqa_score is pure: attention_convolution.rs:190-216)."""
+    tokens, qh, kvh, d = 2048, 32, 8, 64
+    say("causal_gqa prefill", tokens, qh, kvh, d)
+    seed = 0x6A2048
+    q = rng_f32(seed, (tokens, qh * d))
+    k, v = rng_f32(seed + 1, (tokens, kvh * d)), rng_f32(seed + 2, (tokens, kvh * d))
+    kc = np.zeros((tokens, kvh * d), dtype=np.float32)
+    vc = np.zeros((tokens, kvh * d), dtype=np.float32)
+    out, kc2, vc2, length = run_gqa(backend, q, k, v, kc, vc, 0, qh, kvh, d)
+    want, want_kc, want_vc, want_len = oracle.causal_gqa(q, k, v, kc, vc, 0, qh, kvh, d,
+                                                         threads=16)
+    assert length == want_len == tokens
+    assert max_rel_err(out, want) <= 1e-3
     assert_close(out, want)
     assert bits_equal(kc2, want_kc) and bits_equal(vc2, want_vc)
 

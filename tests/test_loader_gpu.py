@@ -174,3 +174,62 @@ def test_lfm2_bundle_inventory_rejects(backend, tmp_path):
     key = name[(5, 0)] + ".codes"  # CONV_IN of layer 0
     width[key] = np.zeros((768, 64), np.uint8)
     expect(width, "InvalidShape")
+
+
+def test_lfm2_reload_releases_and_a_failed_load_changes_nothing(tmp_path):
+    """Loading a bundle again replaces the previous load's buffers instead of
+    keeping them charged; a load that fails partway (a resource limit hit
+    while uploading) leaves the model's weights as they were, and a fresh
+    model then loads within the same limit."""
+    say("loader: reload and failed load")
+    from runtime_amd.backend import HipBackend, Limits
+    cfg = tiny_cfg()
+    host = {(r, l): a for r, l, a in synthetic_host_weights(cfg, seed=0x5EED1F30,
+                                                            norms="random")}
+    path = tmp_path / "model.safetensors"
+    write_lfm2_bundle(path, cfg, host)
+    prompt = convert.token_ids(12, 0x7043_0011, cfg.vocab)
+
+    probe = HipBackend(0)
+    try:
+        model = Lfm2Model(probe, cfg)
+        with SafetensorsFile(path) as f:
+            load_lfm2(model, f)
+        weights = probe.resource_report().resident_weight_bytes
+        model.append(prompt)
+        want = probe.read(model.logits)
+        footprint = total(probe.resource_report())
+        for _ in range(2):  # reloads keep one load's weights resident
+            with SafetensorsFile(path) as f:
+                load_lfm2(model, f)
+            assert probe.resource_report().resident_weight_bytes == weights
+        model.reset()
+        model.append(prompt)
+        assert probe.read(model.logits).tobytes() == want.tobytes()
+        model.close()
+    finally:
+        probe.close()
+
+    backend = HipBackend(0, limits=Limits(max_total_bytes=footprint + weights // 2))
+    try:
+        model = Lfm2Model(backend, cfg)
+        with SafetensorsFile(path) as f:
+            load_lfm2(model, f)
+        model.append(prompt)
+        assert backend.read(model.logits).tobytes() == want.tobytes()
+        with SafetensorsFile(path) as f, pytest.raises(ExecutorError) as e:
+            load_lfm2(model, f)  # needs a second set of weights beside the first
+        assert e.value.variant == "ResourceLimit"
+        assert backend.resource_report().resident_weight_bytes == weights
+        model.reset()
+        model.append(prompt)
+        assert backend.read(model.logits).tobytes() == want.tobytes()
+        model.close()
+        fresh = Lfm2Model(backend, cfg)
+        with SafetensorsFile(path) as f:
+            load_lfm2(fresh, f)
+        fresh.append(prompt)
+        assert backend.read(fresh.logits).tobytes() == want.tobytes()
+        fresh.close()
+    finally:
+        backend.close()

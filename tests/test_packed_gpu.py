@@ -227,6 +227,50 @@ def test_prefill_gemm_config_shapes(backend, gemm_path, scheme, n, k, m):
     assert_close(got[rows], want, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("m,n,k", [(512, 8192, 2048), (2048, 8192, 2048), (2048, 4608, 1024)])
+@pytest.mark.parametrize("gemm_path", ["auto", "fma"])
+def test_prefill_pair_and_swiglu_pair_unsplit(backend, gemm_path, scheme, m, n, k):
+    """The two-stream GEMM at the prefill depths where it runs without a
+    K split (at least 512 output tiles of 128 x 64 per stream): the FFN
+    gate/up pair of both model shapes, in full (all N columns) on a seeded
+    subset of rows, against the row-parallel oracle
+    (packed_pair_validation.rs:169-208: the pair equals two singles, and
+    SwiGLU of the pair equals swiglu_pair, both bitwise in the oracle)."""
+    say("prefill pair unsplit", scheme, gemm_path, m, n, k)
+    from tests.conftest import PATHS
+    ca, sa = make_weights(n, k, scheme, 0x5EED0610 + n + k)
+    cb, sb = make_weights(n, k, scheme, 0x5EED0611 + n + k)
+    x = convert.normal((m, k), 0xAC70610 + m + k)
+    ga, gsa = upload_weights(backend, ca, sa)
+    gb, gsb = upload_weights(backend, cb, sb)
+    xb = backend.upload_f32(x.shape, x)
+    out_a = backend.allocate_f32((m, n))
+    out_b = backend.allocate_f32((m, n))
+    fused = backend.allocate_f32((m, n))
+    previous = backend.set_kernel_path(PATHS[gemm_path])
+    try:
+        backend.packed_linear_pair(out_a, out_b, xb, ga, gsa, gb, gsb)
+        backend.packed_swiglu_pair(fused, xb, ga, gsa, gb, gsb)
+        got_a, got_b, got_f = backend.read(out_a), backend.read(out_b), backend.read(fused)
+    finally:
+        backend.set_kernel_path(previous)
+    rng = np.random.default_rng(0x6E46 + m + n + k)
+    rows = np.unique(np.concatenate([[0, 127, 128, m - 1], rng.choice(m, 60, replace=False)]))
+    want_a = oracle.packed_linear_threaded(x[rows], ca, sa)
+    want_b = oracle.packed_linear_threaded(x[rows], cb, sb)
+    for got, want in ((got_a, want_a), (got_b, want_b)):
+        assert np.all(np.isfinite(got))
+        assert max_rel_err(got[rows], want) <= 1e-3
+        assert_close(got[rows], want, 1e-4, 1e-4)
+    want_f = oracle.swiglu(want_a, want_b)
+    assert np.all(np.isfinite(got_f))
+    assert max_rel_err(got_f[rows], want_f) <= 1e-3
+    assert_close(got_f[rows], want_f, 1e-4, 1e-4)
+    for buf in (ga, gsa, gb, gsb, xb, out_a, out_b, fused):
+        buf.release()
+
+
 # --- reserved ternary code 3 ----------------------------------------------------
 
 def test_ternary_reserved_code_decodes_as_plus_two(backend, path):
