@@ -193,6 +193,68 @@ struct Json {
         *v = r;
         return true;
     }
+    // Any JSON value (RFC 8259); its text is kept only when it is a string.
+    bool value(std::string *text, bool *is_string, int depth = 0)
+    {
+        space();
+        if (p >= end)
+            return invalid();
+        *is_string = *p == '"';
+        if (*is_string)
+            return string(text);
+        if (depth > 64)
+            return invalid();
+        std::string skip;
+        bool nested = false;
+        if (eat('{')) {
+            if (eat('}'))
+                return true;
+            do {
+                if (!string(&skip) || !eat(':') || !value(&skip, &nested, depth + 1))
+                    return invalid();
+            } while (eat(','));
+            return eat('}') ? true : invalid();
+        }
+        if (eat('[')) {
+            if (eat(']'))
+                return true;
+            do {
+                if (!value(&skip, &nested, depth + 1))
+                    return false;
+            } while (eat(','));
+            return eat(']') ? true : invalid();
+        }
+        for (const char *word : {"true", "false", "null"}) {
+            const size_t n = std::strlen(word);
+            if (size_t(end - p) >= n && std::memcmp(p, word, n) == 0) {
+                p += n;
+                return true;
+            }
+        }
+        // -?(0|[1-9][0-9]*)(.[0-9]+)?([eE][+-]?[0-9]+)?
+        auto digits = [&] {
+            const char *q = p;
+            while (p < end && *p >= '0' && *p <= '9')
+                ++p;
+            return p > q;
+        };
+        if (p < end && *p == '-')
+            ++p;
+        if (p < end && *p == '0')
+            ++p;
+        else if (!digits())
+            return invalid();
+        if (p < end && *p == '.' && (++p, !digits()))
+            return invalid();
+        if (p < end && (*p == 'e' || *p == 'E')) {
+            ++p;
+            if (p < end && (*p == '+' || *p == '-'))
+                ++p;
+            if (!digits())
+                return invalid();
+        }
+        return true;
+    }
     bool u64_array(std::vector<uint64_t> *out)
     {
         if (!eat('['))
@@ -551,30 +613,46 @@ mfh_status mfs_matmul_scheme(const mfs_file *file, const char *name, mfs_scheme 
         else
             return fail_s(MFH_UNSUPPORTED, "unrecognized LFM2 weight format");
     }
-    // parse_lfm2_tensor_quantization (weights.rs:92-130): a JSON-encoded
-    // string map in the metadata.
+    // parse_lfm2_tensor_quantization (weights.rs:92-135): a JSON-encoded map
+    // in the metadata, every entry of which must name a known level (a
+    // string) before any is used.  A repeated name keeps its last entry, as
+    // a JSON map deserialized into serde_json::Map does.
     auto map = file->metadata.find("tensor_quantization");
     if (map != file->metadata.end()) {
         const std::string &text = map->second;
         Json j{text.data(), text.data() + text.size()};
-        std::map<std::string, std::string> levels;
-        if (!parse_metadata(j, &levels) || (j.space(), j.p != j.end))
+        std::map<std::string, mfs_scheme> levels;
+        bool level_error = false;
+        bool ok = j.eat('{');
+        if (ok && !j.eat('}')) {
+            do {
+                std::string key, level;
+                bool is_string = false;
+                if (!(ok = j.string(&key) && j.eat(':') && j.value(&level, &is_string)))
+                    break;
+                mfs_scheme scheme = MFS_SCHEME_DENSE;
+                if (is_string && level == "ternary-v1")
+                    scheme = MFS_SCHEME_TERNARY;
+                else if (is_string && level == "nf4-v1")
+                    scheme = MFS_SCHEME_NF4;
+                else if (is_string && level == "int8-v1")
+                    scheme = MFS_SCHEME_INT8;
+                else if (!(is_string && (level == "dense" || level == "bf16" || level == "f16" ||
+                                         level == "f32")))
+                    level_error = true;
+                levels[key] = scheme;
+            } while (j.eat(','));
+            ok = ok && j.eat('}');
+        }
+        if (!ok || (j.space(), j.p != j.end))
             return fail_s(MFH_INVALID_ARGUMENT, "tensor_quantization metadata is not valid JSON");
+        if (level_error)
+            return fail_s(MFH_INVALID_ARGUMENT,
+                          "tensor_quantization level must be ternary-v1, nf4-v1, int8-v1, or a "
+                          "dense dtype");
         auto it = levels.find(name);
         if (it != levels.end()) {
-            const std::string &level = it->second;
-            if (level == "ternary-v1")
-                *out = MFS_SCHEME_TERNARY;
-            else if (level == "nf4-v1")
-                *out = MFS_SCHEME_NF4;
-            else if (level == "int8-v1")
-                *out = MFS_SCHEME_INT8;
-            else if (level == "dense" || level == "bf16" || level == "f16" || level == "f32")
-                *out = MFS_SCHEME_DENSE;
-            else
-                return fail_s(MFH_INVALID_ARGUMENT,
-                              "tensor_quantization level must be ternary-v1, nf4-v1, int8-v1, "
-                              "or a dense dtype");
+            *out = it->second;
             return MFH_OK;
         }
     }

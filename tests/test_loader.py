@@ -155,12 +155,35 @@ def test_tensor_quantization_overrides(tmp_path):
     with scheme_file(tmp_path, {"format": "minifield.ternary.v1",
                                 "tensor_quantization": json.dumps({"a": "f32"})}) as f:
         assert (f.matmul_scheme("a"), f.matmul_scheme("b")) == ("dense", "ternary")
-    for bad in ("not json", json.dumps({"a": "q4"}), json.dumps({"a": 1})):
+    for bad in ("not json", json.dumps({"a": "q4"}), json.dumps({"a": 1}), "[]",
+                '{"a": "nf4-v1",}', '{"a": "nf4-v1"} x'):
         with scheme_file(tmp_path, {"format": "minifield.mixed.v1",
                                     "tensor_quantization": bad}) as f:
             with pytest.raises(ExecutorError) as e:
                 f.matmul_scheme("a")
             assert e.value.variant == "InvalidArgument"
+
+
+@pytest.mark.parametrize("levels", [{"a": "nf4-v1", "b": "q4"}, {"a": "nf4-v1", "b": 1},
+                                    {"a": "nf4-v1", "b": None},
+                                    {"a": "nf4-v1", "b": {"nested": [1, 2.5e-3, True]}}])
+def test_tensor_quantization_checks_every_entry(tmp_path, levels):
+    """quantization_from_entries (weights.rs:116-135) rejects the whole map
+    when any entry is not a known level string, whichever tensor is looked
+    up; a non-string level gets the level message, not a JSON error."""
+    with scheme_file(tmp_path, {"format": "minifield.mixed.v1",
+                                "tensor_quantization": json.dumps(levels)}) as f:
+        for name in ("a", "b", "z"):
+            with pytest.raises(ExecutorError) as e:
+                f.matmul_scheme(name)
+            assert e.value.variant == "InvalidArgument"
+            assert "level must be ternary-v1" in str(e.value)
+
+
+def test_tensor_quantization_repeated_name_keeps_the_last(tmp_path):
+    with scheme_file(tmp_path, {"format": "minifield.mixed.v1",
+                                "tensor_quantization": '{"a": "nf4-v1", "a": "int8-v1"}'}) as f:
+        assert f.matmul_scheme("a") == "int8"
 
 
 def test_bundle_writer_layout(tmp_path):

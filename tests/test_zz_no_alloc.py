@@ -72,6 +72,35 @@ def test_noalloc_equals_packed_linear_twice(be, scheme):
         assert_close(got, oracle.packed_linear_threaded(x, codes, scales))
 
 
+@pytest.mark.parametrize("scheme", SCHEMES)
+def test_noalloc_first_on_a_fresh_context_takes_no_memory(scheme):
+    """On a context whose pooled GEMV scratch has never been grown, the
+    allocation-free call leaves the footprint (and its scratch part)
+    unchanged; packed_linear afterwards gives the same bits."""
+    say("noalloc fresh", scheme)
+    fresh = HipBackend(0)
+    try:
+        m, n, k = 8, 8192, 2048
+        codes, scales, cb, sb = weights(fresh, n, k, scheme, 0x5EED0A20)
+        x = convert.normal((m, k), 0xAC70A20)
+        xb = fresh.upload_f32(x.shape, x)
+        got_buf = fresh.allocate_f32((m, n))
+        want_buf = fresh.allocate_f32((m, n))
+        fresh.prepare_packed(cb, sb)
+        fresh.synchronize()
+        before = fresh.resource_report()
+        fresh.packed_linear_noalloc(got_buf, xb, cb, sb)
+        fresh.synchronize()
+        after = fresh.resource_report()
+        assert total(after) == total(before)
+        assert after.scratch_bytes == before.scratch_bytes
+        got = fresh.read(got_buf)
+        fresh.packed_linear(want_buf, xb, cb, sb)
+        assert got.tobytes() == fresh.read(want_buf).tobytes()
+    finally:
+        fresh.close()
+
+
 def test_noalloc_rejects_what_it_cannot_serve(be):
     say("noalloc rejects")
     codes, scales, cb, sb = weights(be, 64, 16512, "int8", 0x5EED0A10)
