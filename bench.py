@@ -24,6 +24,13 @@ duration across back-to-back launches on rotating copies, against the
 8 TB/s HBM peak.  Its `traffic` is measured by this run: two rocprofv3
 --pmc child runs of the dominant launch (FETCH_SIZE, then WRITE_SIZE, KiB per
 dispatch) each scaled by the same counter over a 256 MiB device copy.
+
+CPU baselines (the oracle: the C restatement of the reference's
+single-threaded backend-cpu path, admission scans included, pinned to one
+host core) sit beside each throughput: `cpu_baseline` for the sweep,
+`prefill_gemm.cpu_baseline` (GFLOP/s per GEMM case from a row sample) and
+`lfm2.<shape>.cpu_baseline` (decode tok/s and per-operation time at the
+workload's context from a few sampled steps).
 """
 from __future__ import annotations
 
@@ -65,6 +72,21 @@ def host_cpu() -> dict:
         pass
     return {"cpu_model": model, "nproc": os.cpu_count(),
             "allowed_cpus": len(os.sched_getaffinity(0))}
+
+
+class one_core:
+    """Pin this process to one allowed host core for the duration (the
+    reference CPU path is single-threaded, crates/backend-cpu/src/lib.rs:3-4)."""
+
+    def __enter__(self):
+        self.allowed = os.sched_getaffinity(0)
+        self.core = min(self.allowed)
+        os.sched_setaffinity(0, {self.core})
+        return self.core
+
+    def __exit__(self, *exc):
+        os.sched_setaffinity(0, self.allowed)
+        return False
 
 
 def cpu_baseline(weights, xs) -> dict:
@@ -178,7 +200,7 @@ MFMA_PASSES = {"ternary": 2, "int8": 2, "nf4": 3}
 MFMA_PASSES_SINGLE = {"ternary": 1, "int8": 1, "nf4": 2}
 
 
-def prefill_gemm(backend, reps: int = 5) -> dict:
+def prefill_gemm(backend, reps: int = 5, cpu: bool = True) -> dict:
     """Packed GEMM at M in {512, 2048} x {8192x2048, 2048x8192} x 3 formats
     on the matrix-core kernel (exact hi + lo activations, the default, and
     the opt-in single-half activations) and on the FP32-FMA kernel (seeded
@@ -224,8 +246,54 @@ def prefill_gemm(backend, reps: int = 5) -> dict:
                 row["fma_util"] = round(row["fma_TFLOPs"] / FP32_PEAK_TFLOPS, 4)
                 cases[f"{fmt}:M{m}:{n}x{k}"] = row
     best = max(cases.items(), key=lambda kv: kv[1]["mfma_TFLOPs"])
-    return {"workload": "packed GEMM M{512,2048} x {8192x2048,2048x8192} x {ternary,nf4,int8}",
-            "peak_f16_TFLOPs": F16_MFMA_PEAK_TFLOPS, "best": best[0], "cases": cases}
+    out = {"workload": "packed GEMM M{512,2048} x {8192x2048,2048x8192} x {ternary,nf4,int8}",
+           "peak_f16_TFLOPs": F16_MFMA_PEAK_TFLOPS, "best": best[0], "cases": cases}
+    if cpu:
+        out["cpu_baseline"] = gemm_cpu_baseline(cases)
+    return out
+
+
+GEMM_CPU_ROWS = 4
+
+
+def gemm_cpu_baseline(cases: dict) -> dict:
+    """The oracle's packed_linear (the single-threaded backend-cpu
+    restatement, finite and INT8 reserved-code scans included) on the first
+    GEMM_CPU_ROWS activation rows of every GEMM case, pinned to one host core.
+    Rows are independent, so a case's time is M / GEMM_CPU_ROWS times the
+    sample's; GFLOP/s counts 2*N*K per row."""
+    import oracle
+    from runtime_amd import convert
+
+    by_case = {}
+    seconds = 0.0
+    with one_core() as core:
+        for fmt in FORMATS:
+            for si, (n, k) in enumerate(GEMM_SHAPES):
+                codes, scales16 = convert.packed_weights(n, k, fmt, 0x5EED0101 + si)
+                scales = convert.f16_to_f32(scales16)
+                x = convert.normal((GEMM_CPU_ROWS, k), 0xAC70101 + GEMM_MS[0])
+                oracle.packed_linear(x[:1], codes, scales)
+                t0 = time.perf_counter()
+                oracle.packed_linear(x, codes, scales)
+                dt = time.perf_counter() - t0
+                seconds += dt
+                per_row = dt / GEMM_CPU_ROWS
+                for m in GEMM_MS:
+                    key = f"{fmt}:M{m}:{n}x{k}"
+                    by_case[key] = {"s_extrapolated": round(per_row * m, 3),
+                                    "GFLOPs": round(2 * n * k / per_row / 1e9, 3),
+                                    "gpu_speedup": round(per_row * m /
+                                                         (cases[key]["mfma_us"] / 1e6), 1)}
+    values = sorted(v["GFLOPs"] for v in by_case.values())
+    out = {"value": values[len(values) // 2], "unit": "GFLOP/s", "cores": 1, "kind": "port",
+           "statistic": "median over the 12 cases",
+           "sample": f"oracle packed_linear on the first {GEMM_CPU_ROWS} rows of each case "
+                     f"({seconds:.1f} s in all) pinned to host core {core}; each case's time "
+                     f"extrapolated linearly to its M rows",
+           "admission_scans": "included", "by_case": by_case}
+    out.update(host_cpu())
+    return out
 
 
 # LFM2 workloads: (config, prompt tokens, greedy decode steps).
@@ -235,7 +303,7 @@ LFM2_WORKLOADS = {
 }
 
 
-def lfm2_decode(backend, name: str) -> dict:
+def lfm2_decode(backend, name: str, cpu: bool = False) -> dict:
     """Random-init model of the named shape (seeded N(0, 0.02) weights
     quantized per role, unit norm weights), a uniform-random prompt
     (seed 0x7043_0001) prefilled as one token pass and kept as a stored
@@ -251,7 +319,7 @@ def lfm2_decode(backend, name: str) -> dict:
     cfg = getattr(lfm2, factory)(max_tokens=prompt_len + steps + 1)
     t0 = time.perf_counter()
     model = lfm2.Lfm2Model(backend, cfg)
-    lfm2.synthetic_weights(model)
+    host = lfm2.synthetic_weights(model, keep_host=cpu)
     weight_bytes = sum(
         int(np.prod(shape)) * BITS[cfg.formats[lfm2._role_group(role)]] // 8
         + int(np.prod(shape)) // 128 * 2
@@ -309,6 +377,78 @@ def lfm2_decode(backend, name: str) -> dict:
     out["op_by_op_tokens_equal"] = bool(np.array_equal(tokens["fused"], tokens["op_by_op"]))
     prefix.close()
     model.close()
+    if cpu:
+        out["cpu_baseline"] = lfm2_cpu_baseline(cfg, host, prompt_len, steps,
+                                                out["decode_tok_s"])
+    return out
+
+
+# Single-core samples of the LFM2 workloads: decode steps at the workload's
+# context, and (350M shape) a short prompt pass for the per-token prefill cost.
+LFM2_CPU_STEPS = {"lfm2_350m": 12, "lfm2_1_2b": 4}
+LFM2_CPU_PROMPT = 8
+
+
+def lfm2_cpu_baseline(cfg, host: dict, prompt_len: int, steps: int, gpu_tok_s: float) -> dict:
+    """The oracle model of the reference executor's token pass
+    (oracle/lfm2_model.py) single-threaded, every operation the backend-cpu
+    restatement with its admission scans, pinned to one host core.  Decode:
+    greedy steps (sample + one-token append) from a state at the workload's
+    context -- the prompt's key/value rows and convolution histories filled
+    with N(0, 1) values, since a single-core prompt pass of 2048 tokens would
+    take hours (literal O(T^2) attention, attention_convolution.rs:139-164)
+    and the cost of a step does not depend on the cached values -- timed per
+    step and per operation kind.  Prefill (350M shape only): a prompt pass of
+    LFM2_CPU_PROMPT tokens from an empty state, per token."""
+    from oracle.lfm2_model import OracleLfm2
+    from runtime_amd import convert
+
+    factory = "lfm2_350m" if cfg.hidden == 1024 else "lfm2_1_2b"
+    weights = {key: arrays for key, arrays in host.items()}
+    rng = np.random.default_rng(0xC0DE)
+    with one_core() as core:
+        out = {"cores": 1, "kind": "port", "unit": "tok/s", "admission_scans": "included"}
+        if factory == "lfm2_350m":
+            ref = OracleLfm2(cfg, weights, threads=1)
+            prompt = convert.token_ids(LFM2_CPU_PROMPT, 0x7043_0001, cfg.vocab)
+            t0 = time.perf_counter()
+            ref.append(prompt)
+            prefill_s = (time.perf_counter() - t0) / LFM2_CPU_PROMPT
+            out["prefill_tok_s"] = round(1.0 / prefill_s, 3)
+        timings = {}
+        ref = OracleLfm2(cfg, weights, threads=1, timings=timings)
+        for index in ref.key:
+            ref.key[index][:prompt_len] = rng.standard_normal(
+                (prompt_len, cfg.kv_width)).astype(np.float32)
+            ref.value[index][:prompt_len] = rng.standard_normal(
+                (prompt_len, cfg.kv_width)).astype(np.float32)
+            ref.cache_len[index] = prompt_len
+        for index in ref.history:
+            ref.history[index][:] = rng.standard_normal(ref.history[index].shape)
+        ref.length = prompt_len
+        ref.append(convert.token_ids(1, 0x7043_0002, cfg.vocab))  # logits of the last row
+        timings.clear()
+        n = LFM2_CPU_STEPS[factory]
+        t0 = time.perf_counter()
+        for _ in range(n):
+            ref.append([int(ref.sample())])
+        step_s = (time.perf_counter() - t0) / n
+    out["value"] = round(1.0 / step_s, 4)
+    out["decode_ms_per_step"] = round(step_s * 1e3, 1)
+    out["per_op_ms_per_step"] = {kind: round(t / n * 1e3, 2)
+                                 for kind, t in sorted(timings.items(), key=lambda kv: -kv[1])}
+    out["gpu_speedup"] = round(gpu_tok_s * step_s, 1)
+    sample = (f"{n} greedy decode steps at context {prompt_len + 1}..{prompt_len + n} "
+              f"(key/value rows and convolution histories of the {prompt_len}-token prefix "
+              f"filled with N(0,1) values), pinned to host core {core}")
+    if factory == "lfm2_350m":
+        full = prompt_len / out["prefill_tok_s"] + steps * step_s
+        out["full_workload_s_extrapolated"] = round(full, 1)
+        sample += (f"; prefill per token from a {LFM2_CPU_PROMPT}-token prompt pass; the "
+                   f"{prompt_len} + {steps} workload extrapolated as {prompt_len} prompt tokens "
+                   f"at that rate plus {steps} steps at the sampled step time")
+    out["sample"] = sample
+    out.update(host_cpu())
     return out
 
 
@@ -637,11 +777,11 @@ def main() -> int:
     del dev_w, dev_x, dev_out, weights
     if not args.no_gemm:
         log("prefill GEMM")
-        result["prefill_gemm"] = prefill_gemm(backend)
+        result["prefill_gemm"] = prefill_gemm(backend, cpu=not args.no_cpu)
     if args.lfm2 != "none":
         result["lfm2"] = {}
         for name in (["350m", "1.2b"] if args.lfm2 == "both" else [args.lfm2]):
-            result["lfm2"][name] = lfm2_decode(backend, name)
+            result["lfm2"][name] = lfm2_decode(backend, name, cpu=not args.no_cpu)
     print(json.dumps(result))
     backend.close()
     return 0

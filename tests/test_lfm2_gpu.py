@@ -1,5 +1,5 @@
 """GPU parity of the LFM2 token pass (runtime_amd/csrc/lfm2.cpp) against the
-CPU oracle of the reference executor's pass (tests/lfm2_reference.py).
+CPU oracle of the reference executor's pass (oracle/lfm2_model.py).
 
 Small models of the LFM2 layout (convolution and attention blocks, tied
 embedding) in several weight-format mixes: the prefill logits, then greedy
@@ -15,7 +15,7 @@ import sys
 import numpy as np
 import pytest
 
-from lfm2_reference import OracleLfm2
+from oracle.lfm2_model import OracleLfm2
 from runtime_amd import convert
 from runtime_amd.lfm2 import ATTENTION, CONV, Lfm2Config, Lfm2Model, synthetic_weights
 from tests.conftest import assert_close, max_rel_err

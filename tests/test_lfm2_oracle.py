@@ -1,4 +1,4 @@
-"""Pins the LFM2 pass oracle (tests/lfm2_reference.py) on the CPU.
+"""Pins the LFM2 pass oracle (oracle/lfm2_model.py) on the CPU.
 
 1. An independent float64 numpy forward over dequantized weights: written
    from the model definition (pre-norm blocks, B*V gated short convolution,
@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
-from lfm2_reference import OracleLfm2
+from oracle.lfm2_model import OracleLfm2
 from runtime_amd import convert
 from runtime_amd.lfm2 import (ATTENTION, CONV, CONV_IN, CONV_KERNEL, CONV_OUT, EMBEDDING_NORM,
                               FFN_NORM, FFN_W1, FFN_W2, FFN_W3, KEY, KEY_NORM, OPERATOR_NORM,
@@ -161,3 +161,28 @@ def test_oracle_detects_a_miswired_residual():
     finally:
         oracle.add_row_rms_norm = original
     assert np.max(np.abs(bad - good)) / np.max(np.abs(good)) > 1e-3
+
+
+def test_single_threaded_pass_equals_the_parallel_one():
+    """threads=1 (the CPU baseline: every operation single-threaded, scans
+    included, literal attention) gives the parallel pass's bits, prefill and
+    decode, and its per-operation timings cover every operation kind."""
+    cfg = tiny()
+    w = oracle_weights(host_weights(cfg))
+    ids = convert.token_ids(7, 0x7043_0050, cfg.vocab)
+    timings = {}
+    single = OracleLfm2(cfg, w, threads=1, timings=timings)
+    parallel = OracleLfm2(cfg, w, threads=4)
+    for model in (single, parallel):
+        model.append(ids)
+    assert single.logits.tobytes() == parallel.logits.tobytes()
+    for _ in range(3):
+        tokens = [single.sample(), parallel.sample()]
+        assert tokens[0] == tokens[1]
+        single.append([int(tokens[0])])
+        parallel.append([int(tokens[1])])
+        assert single.logits.tobytes() == parallel.logits.tobytes()
+    assert {"embedding gather", "norms", "conv in projection", "short convolution",
+            "conv out projection", "q/k/v projections", "qk norm + rope", "attention",
+            "attention out projection", "ffn gate/up", "swiglu", "ffn down", "lm head",
+            "argmax"} <= set(timings)

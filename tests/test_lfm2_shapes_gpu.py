@@ -4,7 +4,7 @@
   (hidden 2048, NF4 convolution/attention, ternary FFN, INT8 tied head):
   a prompt pass (past 96 rows, so the fused FFN pair runs), then greedy
   decode teacher-forced with the GPU's tokens, every step's logits against the oracle model of the reference executor
-  (tests/lfm2_reference.py) within max|d|/max|cpu| <= 1e-3 and the device
+  (oracle/lfm2_model.py) within max|d|/max|cpu| <= 1e-3 and the device
   rule |d| <= 1e-4 + 1e-4|cpu|.
 - The 1.2B shape past 2048 tokens, where no CPU oracle is affordable:
   the fused decode step (decode-attention kernel over 40 key ranges, K-split
@@ -24,7 +24,7 @@ import sys
 import numpy as np
 import pytest
 
-from lfm2_reference import OracleLfm2
+from oracle.lfm2_model import OracleLfm2
 from runtime_amd import convert
 from runtime_amd.backend import HipBackend
 from runtime_amd.lfm2 import Lfm2Model, attach, lfm2_1_2b, lfm2_350m, synthetic_host_weights
