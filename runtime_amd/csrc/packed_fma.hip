@@ -251,7 +251,6 @@ template <Format F, Epilogue E>
 __global__ __launch_bounds__(256) void gemm_fma_kernel(PackedCall call)
 {
     constexpr int S = (E == Epilogue::Single) ? 1 : 2;
-    constexpr int CB = ChunkBytes<F>::value;
     __shared__ float xs[kSlice][kTile + 4];
     __shared__ float ws[S][kSlice][kTile + 4];
     __shared__ float lut[16];

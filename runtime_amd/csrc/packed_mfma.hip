@@ -39,6 +39,7 @@
 // Scales: [tile][group][16] as binary16 when every scale is exact in it,
 // otherwise f32.
 #include <type_traits>
+#include <utility>
 
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
@@ -63,19 +64,19 @@ constexpr float kNf4LevelValues[16] = {
     0.44070983f,  0.562617f,    0.72295684f,  1.0f,
 };
 
-// Per-format geometry.
+// Per-format geometry:
 //   kstep: k covered by one MFMA;  kpl: ksteps per 16-byte lane load;
-//   spg: ksteps per 128-weight group;  lb: ksteps per loop block;
-//   align: K padding of the tile layout.
+//   lb: ksteps per loop block (integer-MFMA formats);  align: K padding of
+//   the tile layout (integer-MFMA formats; NF4 pads to 128, align_of).
 template <Format F> struct Geo;
 template <> struct Geo<Format::Ternary> {
-    static constexpr int kstep = 64, kpl = 4, spg = 2, lb = 4, align = 256;
+    static constexpr int kstep = 64, kpl = 4, lb = 4, align = 256;
 };
 template <> struct Geo<Format::Int8> {
-    static constexpr int kstep = 64, kpl = 1, spg = 2, lb = 2, align = 128;
+    static constexpr int kstep = 64, kpl = 1, lb = 2, align = 128;
 };
 template <> struct Geo<Format::Nf4> {
-    static constexpr int kstep = 32, kpl = 4, spg = 4, lb = 4, align = 128;
+    static constexpr int kstep = 32, kpl = 4;
 };
 
 __host__ __device__ inline uint32_t pad_to(uint32_t v, uint32_t a) { return (v + a - 1) / a * a; }
@@ -1400,6 +1401,274 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// Streaming ternary GEMV for one or two activation rows (MB = m), the LM
+// head's decode case.  Two changes to stream_ternary_kernel remove work that
+// the four-row layout wastes when fewer rows are live:
+// - Prologue: lane 16q + 4 slot + p forms the digits of one (batch row,
+//   kstep) slot -- slot = kstep offset (MB = 1) or kstep offset + 2 * batch
+//   (MB = 2) -- so one pass of the register prologue's arithmetic forms four
+//   ksteps (MB = 1) or two ksteps of both rows (MB = 2) where the four-row
+//   layout formed one.  The two ksteps of a 128-group are the slots that
+//   differ in lane bit 2, so a group's exponent and correction reduce over
+//   the lane quad, that bit (DPP row_half_mirror) and the lane blocks.  The
+//   bytes are emit_group's.
+// - Products: IL = 4 / MB consecutive groups accumulate into one MFMA result,
+//   group g in A rows [4 MB (g % IL), +4 MB) (the other rows zero), so lane
+//   block q' of the result holds the digit sums of group base + q' / MB,
+//   batch row q' % MB, and the digit combine runs once per IL groups.  A lane
+//   reads its fragment rows for the groups of its own row block and zeros
+//   (an all-zero LDS region at the same offsets) for the others.
+// Each lane accumulates its groups in order; the IL partial sums of a row
+// are added at the end (row-swap exchanges), which reorders the f32
+// additions over groups but not the exact in-group sums.
+// ---------------------------------------------------------------------------
+// Calls f(integral_constant<int, i>) for i = 0 .. N-1 in order, so every
+// index f derives from i is a compile-time constant.
+template <typename F, int... I>
+__device__ __forceinline__ void unroll_each(F &&f, std::integer_sequence<int, I...>)
+{
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void unroll_groups(F &&f)
+{
+    unroll_each(f, std::make_integer_sequence<int, N>{});
+}
+
+// Reductions across lane rows on the VALU (gfx950 v_permlane16/32_swap):
+// after the swap of two copies, lane l holds (value of l, value of l ^ 16)
+// (or ^ 32) in some order, the same order for both lanes of the pair, so a
+// commutative combine gives both lanes the identical result.
+__device__ __forceinline__ unsigned max_xor16(unsigned v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return max(unsigned(r[0]), unsigned(r[1]));
+}
+__device__ __forceinline__ unsigned max_xor32(unsigned v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max(unsigned(r[0]), unsigned(r[1]));
+}
+__device__ __forceinline__ long long sum_xor16(long long v)
+{
+    const auto lo = __builtin_amdgcn_permlane16_swap(unsigned(v), unsigned(v), false, false);
+    const auto hi = __builtin_amdgcn_permlane16_swap(unsigned(v >> 32), unsigned(v >> 32), false,
+                                                      false);
+    return ((static_cast<long long>(hi[0]) << 32) | unsigned(lo[0])) +
+           ((static_cast<long long>(hi[1]) << 32) | unsigned(lo[1]));
+}
+__device__ __forceinline__ long long sum_xor32(long long v)
+{
+    const auto lo = __builtin_amdgcn_permlane32_swap(unsigned(v), unsigned(v), false, false);
+    const auto hi = __builtin_amdgcn_permlane32_swap(unsigned(v >> 32), unsigned(v >> 32), false,
+                                                      false);
+    return ((static_cast<long long>(hi[0]) << 32) | unsigned(lo[0])) +
+           ((static_cast<long long>(hi[1]) << 32) | unsigned(lo[1]));
+}
+__device__ __forceinline__ float sum_xor16(float v)
+{
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float sum_xor32(float v)
+{
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ unsigned half_mirror(unsigned v)
+{
+    // DPP row_half_mirror: lane i of each 8-lane half reads lane 7 - i.
+    return unsigned(__builtin_amdgcn_mov_dpp(int(v), 0x141, 0xF, 0xF, false));
+}
+
+template <int MB, int KL, bool HALF, int W>
+__global__ __launch_bounds__(64 * W) void stream_ternary_rows_kernel(StreamArgs a)
+{
+    using ST = typename ScaleT<HALF>::type;
+    constexpr int IL = 4 / MB;          // groups per MFMA accumulation
+    constexpr int RB = 4 * MB;          // A rows of one group's block
+    constexpr int G = 2 * KL;           // 128-groups of K
+    constexpr int KS = 4 * KL;          // 64-wide ksteps
+    constexpr int PASS_KS = 4 / MB;     // ksteps one prologue pass forms
+    constexpr int PASSES = KS / PASS_KS;
+    static_assert(G % IL == 0, "whole accumulations");
+    typedef typename std::conditional<HALF, uint2, v4u>::type SV;
+    constexpr int SLANES = G * 16 * (HALF ? 2 : 4) / int(sizeof(SV));
+    // Fragments [kstep][lane block][row 4b + p] (16 B each), records
+    // [batch][group], each wave's scale block.
+    __shared__ v4i frag[KS * 4 * RB];
+    __shared__ v4i zeros[KS * 4 * RB];
+    __shared__ StreamRecord rec[MB * G];
+    __shared__ SV scale_lds[W * SLANES];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15, p = lane & 3, slot = (lane >> 2) & 3;
+    const uint32_t tile_id = blockIdx.x * W + wave;
+    const uint32_t tile = tile_id < a.n_tiles ? tile_id : a.n_tiles - 1;
+
+    // 1. The tile's scale block.
+    SV sv{};
+    if (lane < uint32_t(SLANES))
+        sv = reinterpret_cast<const SV *>(a.scales)[size_t(tile) * SLANES + lane];
+    __builtin_amdgcn_sched_barrier(0);
+    // 2. The values of this wave's prologue passes (wave w takes passes w,
+    // w + W, ...): slot -> (batch b, kstep s).
+    constexpr int PER = (PASSES + W - 1) / W;
+    const uint32_t pb = MB == 1 ? 0 : slot >> 1;
+    v4f xv[PER];
+#pragma unroll
+    for (int pi = 0; pi < PER; ++pi) {
+        const uint32_t pass = wave + W * pi < uint32_t(PASSES) ? wave + W * pi : 0;
+        const uint32_t ps = pass * PASS_KS + (MB == 1 ? slot : slot & 1);
+        const uint32_t kx = 64 * ps + 16 * q + 4 * p;
+        xv[pi] = *reinterpret_cast<const v4f *>(a.x + size_t(pb) * a.k + (kx < a.k ? kx : 0));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // 3. The first weight loads of the tile.
+    v4u w[KL];
+    const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * KL * 64 + lane;
+    constexpr int AHEAD = KL < kStreamTernaryAhead ? KL : kStreamTernaryAhead;
+#pragma unroll
+    for (int l = 0; l < AHEAD; ++l)
+        w[l] = __builtin_nontemporal_load(&wp[l * 64]);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 4. The prologue passes (the register prologue's arithmetic, per slot),
+    // then the scale block, into LDS.
+#pragma unroll
+    for (int pi = 0; pi < PER; ++pi) {
+        const uint32_t pass = wave + W * pi;
+        if (pass >= uint32_t(PASSES))
+            continue;
+        const uint32_t ps = pass * PASS_KS + (MB == 1 ? slot : slot & 1);
+        const bool inb = 64 * ps + 16 * q + 4 * p < a.k;
+        float v[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            v[t] = inb ? xv[pi][t] : 0.0f;
+        unsigned mb = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
+        mb = max(mb, quad_xor1(mb));
+        mb = max(mb, quad_xor2(mb));
+        mb = max(mb, half_mirror(mb));
+        mb = max_xor16(mb);
+        mb = max_xor32(mb);
+        const bool bad = mb >= 0x7F800000u;
+        int e = 0;
+        if (!bad && mb)
+            frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+        const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
+        long long corr = 0;
+        unsigned vp[4];
+        int u_prev = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            int val = bad ? 0 : int(rintf(ldexpf(v[t], 30 - e)));
+            // Field t of the nested masks (see the operand-field note).
+            const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
+            val = t == 0 ? u : u - u_prev;
+            u_prev = u;
+            corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
+                          : -(static_cast<long long>(u) << 6);
+            vp[t] = unsigned(val + 0x808080);
+        }
+        unsigned d[4], wd[4];
+        byte_transpose<true>(vp, d);
+        quad_transpose(d, p);
+        byte_transpose<false>(d, wd);
+        const unsigned flip = p ? 0x80808080u : 0u;
+        frag[(ps * 4 + q) * RB + 4 * pb + p] =
+            v4i{int(wd[0] ^ flip), int(wd[1] ^ flip), int(wd[2] ^ flip), int(wd[3] ^ flip)};
+        corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
+                (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
+        corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
+                (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
+        corr += static_cast<long long>(half_mirror(unsigned(corr))) |
+                (static_cast<long long>(half_mirror(unsigned(corr >> 32))) << 32);
+        corr = sum_xor16(corr);
+        corr = sum_xor32(corr);
+        // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
+        const long long lo = ((corr + 32768) & 65535) - 32768;
+        const int hi = int((corr - lo) >> 16);
+        if (lane < 16 && p == 0 && (slot & 1) == 0)
+            rec[pb * G + ps / 2] = StreamRecord{int2{hi, int(lo)}, factor, 0.0f};
+    }
+    for (uint32_t i = threadIdx.x; i < uint32_t(KS * 4 * RB); i += 64 * W)
+        zeros[i] = v4i{0, 0, 0, 0};
+    if (lane < uint32_t(SLANES))
+        scale_lds[wave * SLANES + lane] = sv;
+    __syncthreads();
+
+    // 5. The tile's products.  Lane (q, i) supplies A row i: row block
+    // i / RB takes the groups g with g % IL == i / RB.
+    const uint32_t phase = j / RB;
+    const ST *scl = reinterpret_cast<const ST *>(scale_lds + wave * SLANES) + j;
+    // Per phase, the lane's fragment base: its own compact rows for its row
+    // block's phase, the zero region (same offsets) for the others.  Every
+    // read is then one unconditional 16-byte LDS load.
+    const v4i *abase[IL];
+#pragma unroll
+    for (int ph = 0; ph < IL; ++ph)
+        abase[ph] = (phase == uint32_t(ph) ? frag : zeros) + q * RB + j % RB;
+    v4i cur[2], next[2];
+    auto read_group = [&](auto g_tag, v4i (&av)[2]) {
+        constexpr int g = decltype(g_tag)::value;
+        av[0] = abase[g % IL][(2 * g) * 4 * RB];
+        av[1] = abase[g % IL][(2 * g + 1) * 4 * RB];
+    };
+    // Lane block q' of each accumulation holds group base + q' / MB, batch
+    // row q' % MB.
+    const uint32_t my_group = q / MB, my_batch = q % MB;
+    float accf = 0.0f;
+    v4i acci = v4i{0, 0, 0, 0};
+    read_group(std::integral_constant<int, 0>{}, cur);
+    unroll_groups<G>([&](auto g_tag) {
+        constexpr int g = decltype(g_tag)::value;
+        if constexpr (g % 2 == 0 && g / 2 + AHEAD < KL)
+            w[g / 2 + AHEAD] = __builtin_nontemporal_load(&wp[(g / 2 + AHEAD) * 64]);
+        if constexpr (g + 1 < G)
+            read_group(std::integral_constant<int, g + 1>{}, next);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+            const int s = 2 * g + kk;
+            const unsigned word = w[s / 4][s % 4];
+            const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
+                               int(word & 0xC0C0C0C0u)};
+            acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[kk], bw, acci, 0, 0, 0);
+        }
+        cur[0] = next[0];
+        cur[1] = next[1];
+        if constexpr (g % IL == IL - 1) {
+            const uint32_t gg = uint32_t(g - (IL - 1)) + my_group;
+            const StreamRecord r = rec[my_batch * G + gg];
+            const float scale = to_f32<HALF>(scl[gg * 16]);
+            // |d.x| < 2^21, so the pairs combine exactly in int32.
+            const int hi = (acci.x << 8) + acci.y - r.corr.x;
+            const int lo = (acci.z << 8) + acci.w - r.corr.y;
+            const float gsum = float(hi) * 65536.0f + float(lo);
+            accf += gsum * (scale * r.xf);
+            // Keep the accumulation here: otherwise it sinks into the
+            // guarded store below and every group's MFMA results stay live.
+            asm volatile("" : "+v"(accf));
+            acci = v4i{0, 0, 0, 0};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    });
+    // The IL partial sums of each batch row: lane blocks q' with equal
+    // q' % MB.
+    if constexpr (MB == 1)
+        accf = sum_xor16(accf);
+    accf = sum_xor32(accf);
+    const uint32_t row = tile_id * 16 + j;
+    if (q < uint32_t(MB) && tile_id < a.n_tiles && q < a.m && row < a.n)
+        a.out[size_t(q) * a.n + row] = accf;
+}
+
+// ---------------------------------------------------------------------------
 // NF4 GEMV on f16 MFMA.  One loop block = one 16-byte lane load per tile =
 // four 32-wide ksteps = one 128-weight group.
 // ---------------------------------------------------------------------------
@@ -2230,6 +2499,26 @@ void launch_stream_ternary(hipStream_t stream, const StreamArgs &args, bool half
         go(std::integral_constant<int, 4>{});
 }
 
+template <int MB, int KL>
+void launch_stream_ternary_rows(hipStream_t stream, const StreamArgs &args, bool half)
+{
+    // Waves per block as launch_stream_ternary.
+    auto go = [&](auto w_tag) {
+        constexpr int W = decltype(w_tag)::value;
+        const unsigned blocks = (args.n_tiles + W - 1) / W;
+        if (half)
+            stream_ternary_rows_kernel<MB, KL, true, W><<<blocks, 64 * W, 0, stream>>>(args);
+        else
+            stream_ternary_rows_kernel<MB, KL, false, W><<<blocks, 64 * W, 0, stream>>>(args);
+    };
+    if (args.n_tiles >= 16 * kStreamMinBlocks)
+        go(std::integral_constant<int, 16>{});
+    else if (args.n_tiles >= 8 * kStreamMinBlocks)
+        go(std::integral_constant<int, 8>{});
+    else
+        go(std::integral_constant<int, 4>{});
+}
+
 // Serves the call with the streaming kernel when it applies; false leaves
 // it to the K-split plans.
 bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
@@ -2258,10 +2547,23 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
         else
             launch_stream_ternary<NF, 8>(stream, args, half);
     };
-    if (call.m <= 4)
+    if (call.m <= 2) {
+        auto rows = [&](auto mb_tag) {
+            constexpr int MB = decltype(mb_tag)::value;
+            if (kl == 4)
+                launch_stream_ternary_rows<MB, 4>(stream, args, half);
+            else
+                launch_stream_ternary_rows<MB, 8>(stream, args, half);
+        };
+        if (call.m == 1)
+            rows(std::integral_constant<int, 1>{});
+        else
+            rows(std::integral_constant<int, 2>{});
+    } else if (call.m <= 4) {
         go(std::integral_constant<int, 1>{});
-    else
+    } else {
         go(std::integral_constant<int, 2>{});
+    }
     return true;
 }
 
