@@ -31,6 +31,11 @@ host core) sit beside each throughput: `cpu_baseline` for the sweep,
 `prefill_gemm.cpu_baseline` (GFLOP/s per GEMM case from a row sample) and
 `lfm2.<shape>.cpu_baseline` (decode tok/s and per-operation time at the
 workload's context from a few sampled steps).
+
+`read_ceiling` is the control for the heads: a plain read of each head's
+algorithmic bytes, timed the same way over 15 launch shapes
+(runtime_amd/libminifield_probe.so); `roofline_by_format` gives each head's
+fraction of it.
 """
 from __future__ import annotations
 
@@ -48,6 +53,9 @@ SHAPES = [(1024, 1024), (4608, 1024), (2048, 2048), (8192, 2048), (2048, 8192), 
 BATCHES = [1, 2, 4, 8]
 HBM_PEAK_GBS = 8000.0
 DOMINANT = ("int8", (65536, 2048), 1)
+# Kernel names that serve a packed decode product (the dominant launch takes
+# wide_row_kernel), as name fragments separated by "|".
+DOMINANT_KERNELS = "wide_row_kernel|gemv_|stream_"
 # Weight bytes each shape of the per-launch table rotates over.
 ROTATE_BYTES = 1 << 30
 COPY_BYTES = 256 << 20  # the calibration copy of the traffic counters
@@ -122,6 +130,45 @@ def cpu_baseline(weights, xs) -> dict:
     return out
 
 
+# The streaming-read ceiling: plain reads of the three heads' algorithmic
+# bytes (runtime_amd/csrc/probe), every (KB per wave, waves per block) pair.
+READ_CEILING_KB = [1, 2, 4, 8, 16]
+READ_CEILING_WAVES = [4, 8, 16]
+
+
+def read_ceiling(launches: int = 100) -> dict:
+    """Average time per launch of a plain read of each 65536x2048 head's
+    algorithmic bytes at B=1, rotating over copies totalling at least 1 GiB
+    (as the heads are timed), for 15 launch shapes; `best` is the ceiling a
+    head's streaming is compared with."""
+    import ctypes
+    import pathlib
+
+    lib = ctypes.CDLL(str(pathlib.Path(__file__).resolve().parent / "runtime_amd" /
+                          "libminifield_probe.so"))
+    fn = lib.mfp_read_ceiling
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                   ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    pairs = [(kb, w) for kb in READ_CEILING_KB for w in READ_CEILING_WAVES]
+    kbs = (ctypes.c_int * len(pairs))(*[kb for kb, _ in pairs])
+    wpb = (ctypes.c_int * len(pairs))(*[w for _, w in pairs])
+    out = {}
+    for fmt in FORMATS:
+        nbytes = algorithmic_bytes(65536, 2048, 1, fmt) // 1024 * 1024
+        us = (ctypes.c_double * len(pairs))()
+        if fn(nbytes, kbs, wpb, len(pairs), launches, us) != 0:
+            raise RuntimeError(f"read ceiling probe failed at {nbytes} bytes")
+        table = {f"{kb}KB/wave x{w}": round(us[i], 2) for i, (kb, w) in enumerate(pairs)}
+        best = min(range(len(pairs)), key=lambda i: us[i])
+        out[fmt] = {"bytes": nbytes, "best_us": round(us[best], 2),
+                    "best_shape": f"{pairs[best][0]} KB per wave, {pairs[best][1]} waves per block",
+                    "GBs": round(nbytes / us[best] / 1e3, 1),
+                    "frac_of_peak": round(nbytes / us[best] / 1e3 / HBM_PEAK_GBS, 4),
+                    "us_by_shape": table}
+    return out
+
+
 def measure_traffic() -> dict:
     """HBM bytes per dominant launch from two rocprofv3 --pmc runs
     (FETCH_SIZE, then WRITE_SIZE, in KiB per dispatch) of `--profile
@@ -164,7 +211,7 @@ def measure_traffic() -> dict:
                                "where counter_name = ?", (counter,)).fetchall()
         per = {}
         for d, name, v in rows:
-            if kernel in name:
+            if any(part in name for part in kernel.split("|")):
                 per[d] = per.get(d, 0.0) + v
         values = sorted(per.values())
         if not values:
@@ -177,7 +224,7 @@ def measure_traffic() -> dict:
         for counter in ("FETCH_SIZE", "WRITE_SIZE"):
             log(f"  {counter}: calibration copy, then the dominant launch")
             copy_kib = per_dispatch(counter, "copy", "copy_kernel")
-            dom_kib = per_dispatch(counter, "dominant", "gemv")
+            dom_kib = per_dispatch(counter, "dominant", DOMINANT_KERNELS)
             scale = (COPY_BYTES / 1024) / copy_kib  # real KiB per counted KiB
             out[counter] = {"dominant_kib": round(dom_kib, 1), "copy_kib": round(copy_kib, 1),
                             "scale": round(scale, 4)}
@@ -481,6 +528,9 @@ def profile_only(backend, args) -> int:
         backend.synchronize()
         log(f"gemm {args.gemm_format} M={m} {n}x{k} x 6 ({args.profile})")
         return 0
+    if args.profile == "read-ceiling":
+        log(json.dumps(read_ceiling()))
+        return 0
     if args.profile == "copy":
         count = 64 << 20
         src = backend.allocate_f32((count,))
@@ -576,11 +626,12 @@ def main() -> int:
     ap.add_argument("--lfm2", choices=["none", "350m", "1.2b", "both"], default="both",
                     help="also time greedy decode of the LFM2 model shapes")
     ap.add_argument("--profile", choices=["dominant", "head-ternary", "head-nf4", "copy",
+                                          "read-ceiling",
                                           "lfm2-350m", "lfm2-1.2b", "gemm", "gemm-single",
                                           "product"],
                     help="run only the dominant operation (or the 65536x2048 head of "
                          "another format, a 256 MiB device copy, the counter calibration, "
-                         "an LFM2 decode, the M=2048 x 8192x2048 prefill GEMM, "
+                         "the streaming-read ceiling of the three heads' bytes, an LFM2 decode, the M=2048 x 8192x2048 prefill GEMM, "
                          "gemm-single with single-half activations, or the --product "
                          "decode GEMV) for rocprofv3, and print no JSON line")
     ap.add_argument("--gemm-format", choices=["ternary", "int8", "nf4"], default="ternary",
@@ -721,12 +772,16 @@ def main() -> int:
                     "us": round(us, 2),
                     "GBs": round(algorithmic_bytes(n_i, k_i, b_i, fmt_i) / (us / 1e6) / 1e9, 1)}
             del copies
+    log("streaming-read ceiling")
+    ceiling = read_ceiling()
     heads = {}
     for fmt_i in FORMATS:
         entry = detail[f"{fmt_i}:65536x2048:B1"]
         heads[fmt_i] = {"us": entry["us"], "achieved": entry["GBs"],
                         "frac": round(entry["GBs"] / HBM_PEAK_GBS, 4),
-                        "algorithmic_bytes": algorithmic_bytes(65536, 2048, 1, fmt_i)}
+                        "algorithmic_bytes": algorithmic_bytes(65536, 2048, 1, fmt_i),
+                        "read_ceiling_us": ceiling[fmt_i]["best_us"],
+                        "frac_of_read_ceiling": round(ceiling[fmt_i]["best_us"] / entry["us"], 4)}
 
     result = {
         "metric": "packed GEMV HBM GB/s (% of 8 TB/s peak); LFM2 batch-1 decode tok/s",
@@ -766,6 +821,7 @@ def main() -> int:
             "rotating_copies": len(dom_copies),
         },
         "roofline_by_format": heads,
+        "read_ceiling": ceiling,
         "detail": detail,
         "detail_method": {"reps": args.reps, "rotating_copies": rotations,
                           "prime_launches": prime_count},

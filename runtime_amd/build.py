@@ -1,7 +1,9 @@
 """Build the gfx950 HIP backend library in-tree.
 
 Compiles every source under runtime_amd/csrc with hipcc for gfx950 into
-runtime_amd/_build/*.o (in parallel) and links runtime_amd/libminifield_hip.so.
+runtime_amd/_build/*.o (in parallel) and links runtime_amd/libminifield_hip.so;
+then builds the streaming-read probe (csrc/probe) as
+runtime_amd/libminifield_probe.so.
 Run as `python -m runtime_amd.build` or through __graft_entry__.build().
 """
 from __future__ import annotations
@@ -17,6 +19,9 @@ PACKAGE = pathlib.Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libminifield_hip.so"
+# The streaming-read ceiling probe (a measurement tool, not the backend).
+PROBE_SRC = CSRC / "probe" / "read_ceiling.hip"
+PROBE_LIBRARY = PACKAGE / "libminifield_probe.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops: no v_pk_{add,mul,fma}_f32 generation (wrong results seen
@@ -70,6 +75,12 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIBRARY)
+    tmp = PROBE_LIBRARY.with_suffix(".so.tmp")
+    cmd = [HIPCC, *COMMON, "-shared", "-o", str(tmp), str(PROBE_SRC)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{proc.stdout}\n{proc.stderr}")
+    os.replace(tmp, PROBE_LIBRARY)
     return LIBRARY
 
 

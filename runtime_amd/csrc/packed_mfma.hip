@@ -2166,6 +2166,315 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
 }
 
 // ---------------------------------------------------------------------------
+// Wide-matrix GEMV at one activation row (the LM heads at decode): each wave
+// owns one 256-wide slice of K ("part" p of P = K / 256) and streams that
+// slice of R tiles, so a block of 16 waves covers TS = 16 / P tiles per
+// round, R rounds: 16 contiguous KB of codes per round for ternary, 32 for
+// NF4, 64 for INT8.  The activation operand never goes through LDS:
+// - One pass of the register prologue's arithmetic over the slice gives
+//   lane 16q + j exactly the A operand row j it supplies for one kstep:
+//   integer formats: lane 16q + 4s + p holds digit p of kstep s (s = 0..3,
+//   two 128-groups); NF4: lane 16q + 2s + h holds half h of kstep s
+//   (s = 0..7, two groups).  For kstep s the wave feeds A = (own kstep == s
+//   ? own fragment : 0), so row j of the MFMA result holds kstep s's sums
+//   in rows 4s + p (2s + h): one accumulation covers the whole slice.
+// - The group exponents, factors and ternary corrections reduce over the
+//   lanes of a group (quad, half-row mirror, row swaps) once per wave, for
+//   all of its R tiles.
+// Per tile, lane block q' holds ksteps q' (2q', 2q' + 1 for NF4); a row swap
+// adds the two halves of each group, the group sum is scaled as elsewhere
+// (digit combine or hi + lo, times scale * factor), and a second swap adds
+// the slice's two groups.  The slices' partial sums meet in LDS and are
+// added in slice order once every wave is done.  The in-group sums are
+// exact as in the other kernels; only the order of the f32 additions over
+// groups differs.
+// ---------------------------------------------------------------------------
+constexpr int kWideAhead = 3;  // 16-byte lane loads in flight per wave
+
+template <Format F>
+struct WideGeo {
+    // Lane loads per (tile, slice) and ksteps per lane load.
+    static constexpr int loads = F == Format::Ternary ? 1 : F == Format::Nf4 ? 2 : 4;
+    static constexpr int ksteps_per_load = F == Format::Int8 ? 1 : 4;
+    static constexpr int ksteps = loads * ksteps_per_load;  // 4, 8, 4
+};
+
+template <Format F, bool HALF, int P, int R>
+__global__ __launch_bounds__(1024) void wide_row_kernel(StreamArgs a)
+{
+    using ST = typename ScaleT<HALF>::type;
+    constexpr int W = 16;
+    constexpr int TS = W / P;                      // tiles per round
+    constexpr int L = WideGeo<F>::loads;
+    constexpr int KPL = WideGeo<F>::ksteps_per_load;
+    constexpr int KSU = WideGeo<F>::ksteps;
+    constexpr int NL = R * L;                       // lane loads per wave
+    constexpr int AH = NL < kWideAhead ? NL : kWideAhead;
+    constexpr int G = 2 * P;                        // 128-groups per tile
+    constexpr bool NF4 = F == Format::Nf4;
+    __shared__ float partial[TS * R * P * 16];
+    __shared__ unsigned lut[NF4 ? 256 * 2 * kStreamLutCopies : 1];
+    __shared__ uint2 entries[NF4 ? 256 : 1];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t part = wave % P, tslot = wave / P;
+    const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
+    auto tile_of = [&](int i) {
+        const uint32_t t = tile0 + uint32_t(TS * i);
+        return t < a.n_tiles ? t : a.n_tiles - 1;
+    };
+
+    // 1. The slice's activations: one float4 per lane.
+    const uint32_t kx = NF4 ? 256 * part + 32 * ((lane >> 1) & 7) + 8 * q + 4 * (lane & 1)
+                            : 256 * part + 64 * ((lane >> 2) & 3) + 16 * q + 4 * (lane & 3);
+    const bool inb = kx < a.k;
+    const v4f xv = *reinterpret_cast<const v4f *>(a.x + (inb ? kx : 0));
+    // 2. Every tile's group scale for this lane's combine (group 2p + q'/2,
+    // row j), then the first weight loads.
+    const uint32_t my_group = 2 * part + (q >> 1);
+    ST sc[R];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+        sc[i] = reinterpret_cast<const ST *>(a.scales)[(size_t(tile_of(i)) * G + my_group) * 16 + j];
+    __builtin_amdgcn_sched_barrier(0);
+    v4u w[NL];
+    auto issue = [&](auto n_tag) {
+        constexpr int n = decltype(n_tag)::value;
+        const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
+                         (size_t(tile_of(n / L)) * (P * L) + part * L + n % L) * 64 + lane;
+        w[n] = __builtin_nontemporal_load(src);
+    };
+    unroll_groups<AH>(issue);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. NF4: the code-byte table (as stream_nf4_kernel's).
+    if constexpr (NF4) {
+        if (threadIdx.x < 256)
+            entries[threadIdx.x] = nf4_lut_entry(threadIdx.x);
+        __syncthreads();
+        for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
+            const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
+            reinterpret_cast<v4u *>(lut)[v] = v4u{e.x, e.y, e.x, e.y};
+        }
+    }
+
+    // 4. The slice's operands and group constants.
+    float v[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        v[t] = inb ? xv[t] : 0.0f;
+    unsigned mb = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
+    // Group lanes: integer formats bits 0-2 (digit p, kstep bit 0) and the
+    // lane blocks; NF4 bits 0-2 (half, kstep bits 0-1) and the lane blocks.
+    mb = max(mb, quad_xor1(mb));
+    mb = max(mb, quad_xor2(mb));
+    mb = max(mb, half_mirror(mb));
+    mb = max_xor16(mb);
+    mb = max_xor32(mb);
+    const bool bad = mb >= 0x7F800000u;
+    int e = 0;
+    if (!bad && mb)
+        frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+    typedef typename std::conditional<NF4, v8h, v4i>::type AT;
+    AT af;
+    float factor;
+    int2 cv = int2{0, 0};
+    if constexpr (NF4) {
+        factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+        const uint32_t h = lane & 1;
+        unsigned mine[2], recv[2];
+#pragma unroll
+        for (int pr = 0; pr < 2; ++pr) {
+            const float v0 = bad ? 0.0f : ldexpf(v[2 * pr], -e);
+            const float v1 = bad ? 0.0f : ldexpf(v[2 * pr + 1], -e);
+            const _Float16 h0 = _Float16(v0), h1 = _Float16(v1);
+            const _Float16 l0 = _Float16(v0 - float(h0)), l1 = _Float16(v1 - float(h1));
+            const unsigned hi_pair = pack_halves(h0, h1), lo_pair = pack_halves(l0, l1);
+            mine[pr] = h ? lo_pair : hi_pair;
+            recv[pr] = quad_xor1(h ? hi_pair : lo_pair);  // the partner's half h
+        }
+        const v4u d = h ? v4u{recv[0], recv[1], mine[0], mine[1]}
+                        : v4u{mine[0], mine[1], recv[0], recv[1]};
+        af = __builtin_bit_cast(v8h, d);
+    } else {
+        factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
+        const uint32_t p = lane & 3;
+        long long corr = 0;
+        unsigned vp[4];
+        int u_prev = 0;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            int val = bad ? 0 : int(rintf(ldexpf(v[t], 30 - e)));
+            if constexpr (F == Format::Ternary) {
+                // Field t of the nested masks (see the operand-field note).
+                const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
+                val = t == 0 ? u : u - u_prev;
+                u_prev = u;
+                corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
+                              : -(static_cast<long long>(u) << 6);
+            }
+            vp[t] = unsigned(val + 0x808080);
+        }
+        unsigned d[4], wd[4];
+        byte_transpose<true>(vp, d);
+        quad_transpose(d, p);
+        if constexpr (F == Format::Ternary) {
+            byte_transpose<false>(d, wd);
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                wd[i] = d[i];
+        }
+        const unsigned flip = p ? 0x80808080u : 0u;
+        af = v4i{int(wd[0] ^ flip), int(wd[1] ^ flip), int(wd[2] ^ flip), int(wd[3] ^ flip)};
+        if constexpr (F == Format::Ternary) {
+            corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
+                    (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
+            corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
+                    (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
+            corr += static_cast<long long>(half_mirror(unsigned(corr))) |
+                    (static_cast<long long>(half_mirror(unsigned(corr >> 32))) << 32);
+            corr = sum_xor16(corr);
+            corr = sum_xor32(corr);
+            // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
+            const long long lo = ((corr + 32768) & 65535) - 32768;
+            cv = int2{int((corr - lo) >> 16), int(lo)};
+        }
+    }
+    // The combine of lane block q' uses group q' / 2 of the slice, whose
+    // constants lanes 8 (q' / 2) .. hold.
+    const int src_lane = 8 * int(q >> 1);
+    const float my_factor = __shfl(factor, src_lane, 64);
+    const int2 my_corr = int2{__shfl(cv.x, src_lane, 64), __shfl(cv.y, src_lane, 64)};
+    // Operands per kstep: own fragment for the lane's kstep, zero otherwise.
+    // NF4 takes two per kstep, in the k-slot order of nf4_entries: slots
+    // (hi, lo) of code byte 2c and of byte 2c + 1 for operand c, so the A
+    // operand repeats each activation pair for its hi and lo slots.
+    // NF4 selects them per kstep from the lane's own pair (registers).
+    const uint32_t own = NF4 ? j >> 1 : j >> 2;
+    constexpr int OPS = NF4 ? 2 : 1;
+    const v4u dq = __builtin_bit_cast(v4u, af);
+    const v4u own0 = NF4 ? v4u{dq.x, dq.x, dq.y, dq.y} : dq;
+    const v4u own1 = v4u{dq.z, dq.z, dq.w, dq.w};
+    auto operand = [&](int s2, int o) {
+        const v4u z{0, 0, 0, 0};
+        return __builtin_bit_cast(AT, own == uint32_t(s2) ? (o == 0 ? own0 : own1) : z);
+    };
+    AT as[NF4 ? 1 : KSU][1];
+    if constexpr (!NF4) {
+#pragma unroll
+        for (int s2 = 0; s2 < KSU; ++s2)
+            as[s2][0] = operand(s2, 0);
+    }
+    if constexpr (NF4)
+        __syncthreads();  // the table
+    const unsigned copy_byte = 8 * (lane % kStreamLutCopies);
+    const char *cells = reinterpret_cast<const char *>(lut);
+
+    // NF4 B operands of one kstep's code word: the table entries (hi pair,
+    // lo pair) of code bytes 0, 1 and of bytes 2, 3, each operand exactly
+    // the two 8-byte reads (no register moves).
+    auto nf4_entries = [&](unsigned word, v4u &b0, v4u &b1) {
+        uint2 ent[4];
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            // (code byte b) * 256 + copy_byte.
+            const unsigned at =
+                __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + b) << 8));
+            ent[b] = *reinterpret_cast<const uint2 *>(cells + at);
+        }
+        b0 = v4u{ent[0].x, ent[0].y, ent[1].x, ent[1].y};
+        b1 = v4u{ent[2].x, ent[2].y, ent[3].x, ent[3].y};
+    };
+    v4u nb0{}, nb1{};
+    if constexpr (NF4)
+        nf4_entries(w[0][0], nb0, nb1);
+
+    // 5. The tiles: products of the slice, then the combine.
+    typedef typename std::conditional<NF4, v4f, v4i>::type CT;
+    unroll_groups<R>([&](auto i_tag) {
+        constexpr int i = decltype(i_tag)::value;
+        CT acc = CT{};
+        unroll_groups<L>([&](auto l_tag) {
+            constexpr int l = decltype(l_tag)::value;
+            constexpr int n = i * L + l;
+            if constexpr (n + AH < NL)
+                issue(std::integral_constant<int, n + AH>{});
+#pragma unroll
+            for (int ks = 0; ks < KPL; ++ks) {
+                const int s2 = l * KPL + ks;  // kstep within the slice
+                if constexpr (F == Format::Int8) {
+                    const v4u wv = w[n];
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        as[s2][0], v4i{int(wv.x), int(wv.y), int(wv.z), int(wv.w)}, acc, 0, 0, 0);
+                } else if constexpr (F == Format::Ternary) {
+                    const unsigned word = w[n][ks];
+                    const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu),
+                                       int(word & 0xF0F0F0F0u), int(word & 0xC0C0C0C0u)};
+                    acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[s2][0], bw, acc, 0, 0, 0);
+                } else {
+                    // The table entries of this kstep were read ahead (with
+                    // the previous kstep's products); read the next one's
+                    // now, while these products run.
+                    const v4u b0 = nb0, b1 = nb1;
+                    if (ks + 1 < KPL) {
+                        nf4_entries(w[n][ks + 1], nb0, nb1);
+                    } else if constexpr (n + 1 < NL) {
+                        nf4_entries(w[n + 1][0], nb0, nb1);
+                    }
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        operand(s2, 0), __builtin_bit_cast(v8h, b0), acc, 0, 0, 0);
+                    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                        operand(s2, OPS - 1), __builtin_bit_cast(v8h, b1), acc, 0, 0, 0);
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        float gsum;
+        if constexpr (NF4) {
+            // Rows 4q' + r: kstep 2q' + r / 2, half r % 2.  Add the group's
+            // other two ksteps (lane block q' ^ 1).
+            gsum = sum_xor16((acc.x + acc.y) + (acc.z + acc.w));
+        } else {
+            // Rows 4q' + r: digit r of kstep q'.  The group's two ksteps are
+            // lane blocks q' and q' ^ 1; integer sums combine exactly.
+            int d[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const auto pr = __builtin_amdgcn_permlane16_swap(unsigned(acc[r]), unsigned(acc[r]),
+                                                                 false, false);
+                d[r] = int(pr[0]) + int(pr[1]);
+            }
+            // |d[0]| < 2^21, so the pairs combine exactly in int32.
+            const int hi = (d[0] << 8) + d[1] - my_corr.x;
+            const int lo = (d[2] << 8) + d[3] - my_corr.y;
+            gsum = float(hi) * 65536.0f + float(lo);
+        }
+        float total = gsum * (to_f32<HALF>(sc[i]) * my_factor);
+        total = sum_xor32(total);  // the slice's two groups
+        if (q == 0)
+            partial[((tslot + TS * i) * P + part) * 16 + j] = total;
+    });
+
+    // 6. The slices of each tile, added in order.
+    __syncthreads();
+    if (threadIdx.x < uint32_t(TS * R * 16)) {
+        const uint32_t tl = threadIdx.x / 16, r = threadIdx.x % 16;
+        float sum = partial[(tl * P) * 16 + r];
+#pragma unroll
+        for (int pp = 1; pp < P; ++pp)
+            sum += partial[(tl * P + pp) * 16 + r];
+        const uint32_t t = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
+        const uint32_t row = t * 16 + r;
+        if (t < a.n_tiles && row < a.n)
+            a.out[row] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // Repack canonical codes into tiles, and scales into [tile][group][16].
 // ---------------------------------------------------------------------------
 template <Format F>
@@ -2567,6 +2876,57 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
     return true;
 }
 
+// Tiles per wave (R) of wide_row_kernel, measured at 65536 rows, one row
+// (us per launch, 1 GiB rotation): INT8 K = 2048 R = 4 21.8-22.4 against
+// R = 8 22.3-22.7 (the four-tile K-split plan 24.2-29.0); K = 1024 R = 2-4
+// 12.1-12.5.  NF4 K = 2048 R = 8 14.8-20.4 against R = 4 18.6-22.3 (two
+// blocks per CU do not fit its registers) and the streaming kernel
+// 18.4-21.8; K = 1024 R = 4 8.9-10.5 against 10.9-12.1.  Ternary K = 1024
+// R = 4 5.6-5.9 against the rows kernel's 5.9-6.2; at K = 2048 the rows
+// kernel (7.5 us) beats R = 8 (8.1-8.6), which keeps it.
+template <Format F, bool HALF, int P>
+void launch_wide_row(hipStream_t stream, const StreamArgs &args)
+{
+    constexpr int R = F == Format::Nf4 && P == 8 ? 8 : 4;
+    constexpr int TS = 16 / P;
+    const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
+    wide_row_kernel<F, HALF, P, R><<<blocks, 1024, 0, stream>>>(args);
+}
+
+// Serves a one-row product of a wide matrix (the LM heads at decode) with
+// wide_row_kernel; false leaves it to the other plans.
+template <Format F>
+bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
+{
+    if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
+        call.epilogue != Epilogue::Single || call.m != 1 || n_tiles < kHeadTiles ||
+        (call.k != 1024 && call.k != 2048) || (F == Format::Ternary && call.k != 1024) ||
+        reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
+        return false;
+    StreamArgs args{};
+    args.x = call.x;
+    args.tiles = call.a.tiles;
+    args.scales = call.a.tiled_scales;
+    args.out = call.out_a;
+    args.m = call.m;
+    args.n = call.n;
+    args.k = call.k;
+    args.n_tiles = n_tiles;
+    const bool half = call.a.tiled_half;
+    if (call.k == 2048) {
+        if (half)
+            launch_wide_row<F, true, 8>(stream, args);
+        else
+            launch_wide_row<F, false, 8>(stream, args);
+    } else {
+        if (half)
+            launch_wide_row<F, true, 4>(stream, args);
+        else
+            launch_wide_row<F, false, 4>(stream, args);
+    }
+    return true;
+}
+
 template <Format F>
 void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
 {
@@ -2574,6 +2934,8 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
     if (try_vgemv(stream, call))
+        return;
+    if (try_wide_row<F>(stream, call, n_tiles))
         return;
     if constexpr (F == Format::Ternary) {
         if (try_stream_ternary(stream, call, n_tiles))
@@ -2770,6 +3132,8 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
     if (try_vgemv(stream, call))
+        return;
+    if (try_wide_row<Format::Nf4>(stream, call, n_tiles))
         return;
     if (try_stream_nf4(stream, call, n_tiles))
         return;

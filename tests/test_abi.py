@@ -66,3 +66,20 @@ def test_library_is_built_for_gfx950():
     # The embedded offload bundle names its target triple.
     data = _ffi.LIBRARY_PATH.read_bytes()
     assert b"amdgcn-amd-amdhsa--gfx950" in data
+
+
+def test_read_ceiling_probe_loads_and_rejects_bad_sizes():
+    """The measurement probe (runtime_amd/libminifield_probe.so) exports its
+    one entry point and refuses arguments it cannot time before touching the
+    device."""
+    import ctypes
+    probe = ctypes.CDLL(str(ROOT / "runtime_amd" / "libminifield_probe.so"))
+    fn = probe.mfp_read_ceiling
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
+                   ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    kb, wpb, us = (ctypes.c_int * 1)(1), (ctypes.c_int * 1)(16), (ctypes.c_double * 1)()
+    assert fn(1000, kb, wpb, 1, 10, us) == -1          # not a multiple of 1 KB
+    assert fn(1 << 20, kb, wpb, 0, 10, us) == -1       # no launch shape
+    bad_waves = (ctypes.c_int * 1)(3)
+    assert fn(1 << 20, kb, bad_waves, 1, 10, us) == -1
