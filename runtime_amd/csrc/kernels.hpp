@@ -70,6 +70,18 @@ struct PackedCall {
     uint32_t seg_n[kMaxSegments] = {};
 };
 
+// One token of the gated short convolution (conv_step_kernel's arithmetic),
+// finished by the convolution in-projection's vector GEMV from its own
+// output rows: u = B * x (rows c and 2h + c), the causal taps over the
+// history and u, times C (row h + c); the history rolls into `next`.
+struct ConvStep {
+    const float *kernel = nullptr;   // [hidden, width], oldest tap first
+    const float *history = nullptr;  // [width - 1, hidden]
+    float *next = nullptr;           // [width - 1, hidden]
+    float *out = nullptr;            // [hidden]
+    uint32_t hidden = 0, width = 0;
+};
+
 // packed_linear's admission (backend-cpu/src/packed.rs:96-140 order and
 // messages): fills `call` for the plain product; enqueues nothing.
 mfh_status admit_packed_linear(mfh_ctx *ctx, mfh_buf *output, const mfh_buf *input,
@@ -88,6 +100,13 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
                         const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
                         float *out_b);
 
+// The decode step's convolution block input: the in-projection of `codes`
+// (3 * conv.hidden rows of width k) over add + RMS norm activations with
+// the one-token convolution folded into its epilogue (try_vgemv_conv).
+// MFH_UNSUPPORTED, before anything is enqueued, where it does not apply.
+mfh_status packed_xform_conv(mfh_ctx *ctx, const XForm &xform, uint32_t k,
+                             const mfh_buf *codes, const mfh_buf *scales, const ConvStep &conv);
+
 // Like packed_xform with the Single epilogue, over `count` weight streams of
 // one format and width k in one launch (the LFM2 q/k/v projections).
 mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, uint32_t k,
@@ -102,6 +121,11 @@ void launch_gemv_fma(hipStream_t stream, const PackedCall &call);
 // returns true, or returns false (nothing enqueued) where it does not serve
 // the call.  The matrix-core GEMV tries it first.
 bool try_vgemv(hipStream_t stream, const PackedCall &call);
+
+// The in-projection (3 * hidden rows, add + RMS norm activations, one row)
+// with the convolution folded in; false, with nothing enqueued, where the
+// vector GEMV does not serve the call.
+bool try_vgemv_conv(hipStream_t stream, const PackedCall &call, const ConvStep &conv);
 // Matrix-core decode GEMV for m <= 8 (needs `tiles` and `tiled_scales` on
 // every stream).  `scratch` holds gemv_mfma_scratch_bytes(call) bytes.
 bool gemv_mfma_supported(Format format);

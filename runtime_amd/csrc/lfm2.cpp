@@ -291,13 +291,30 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
         LayerState &st = m->state[index];
         float *block_input_side = right ? x : nullptr;
         if (m->kinds[index] == 0) {
-            if ((s = packed_xform(c, Epilogue::Single, norm_of(lw.operator_norm, block_input_side),
-                                  1, 3 * h, h, lw.conv_in.tensor, lw.conv_in.scales, nullptr,
-                                  nullptr, dev(ws->projection), nullptr)))
+            // The in-projection finishes the one-token convolution in its
+            // epilogue where the vector GEMV serves it (one launch), else
+            // the projection and conv_step_kernel (two).
+            ConvStep conv;
+            conv.kernel = dev(lw.conv_kernel);
+            conv.history = dev(st.history[st.current]);
+            conv.next = dev(st.history[1 - st.current]);
+            conv.out = dev(ws->convolved);
+            conv.hidden = h;
+            conv.width = cfg.conv_width;
+            s = packed_xform_conv(c, norm_of(lw.operator_norm, block_input_side), h,
+                                  lw.conv_in.tensor, lw.conv_in.scales, conv);
+            if (s == MFH_UNSUPPORTED) {
+                if ((s = packed_xform(c, Epilogue::Single,
+                                      norm_of(lw.operator_norm, block_input_side), 1, 3 * h, h,
+                                      lw.conv_in.tensor, lw.conv_in.scales, nullptr, nullptr,
+                                      dev(ws->projection), nullptr)))
+                    return s;
+                launch_conv_step(c->stream, dev(ws->convolved), dev(ws->projection),
+                                 dev(lw.conv_kernel), dev(st.history[st.current]),
+                                 dev(st.history[1 - st.current]), h, cfg.conv_width);
+            } else if (s) {
                 return s;
-            launch_conv_step(c->stream, dev(ws->convolved), dev(ws->projection),
-                             dev(lw.conv_kernel), dev(st.history[st.current]),
-                             dev(st.history[1 - st.current]), h, cfg.conv_width);
+            }
             XForm convolved;
             convolved.a = dev(ws->convolved);
             if ((s = packed_xform(c, Epilogue::Single, convolved, 1, h, h, lw.conv_out.tensor,

@@ -227,6 +227,34 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
 }
 
+mfh_status packed_xform_conv(mfh_ctx *ctx, const XForm &xform, uint32_t k,
+                             const mfh_buf *codes, const mfh_buf *scales, const ConvStep &conv)
+{
+    Packed p;
+    mfh_status s = check_packed(ctx, codes, scales, &p);
+    if (s)
+        return s;
+    if (p.rows != 3 * uint64_t(conv.hidden) || p.inner != k)
+        return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
+    if (xform.kind != XKind::AddRms || !xform.a || !xform.w || !conv.kernel || !conv.history ||
+        !conv.next || !conv.out || conv.width < 1 || ctx->kernel_path != 0)
+        return fail(ctx, MFH_UNSUPPORTED, "fused convolution needs the vector GEMV");
+    PackedCall call;
+    call.format = p.format;
+    call.epilogue = Epilogue::Single;
+    call.m = 1;
+    call.n = p.rows;
+    call.k = k;
+    call.a = stream_of(codes, scales);
+    call.xform = xform;
+    DeviceGuard guard(ctx->device);
+    if (!try_vgemv_conv(ctx->stream, call, conv))
+        return fail(ctx, MFH_UNSUPPORTED, "fused convolution needs the vector GEMV");
+    if (hipGetLastError() != hipSuccess)
+        return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
+    return MFH_OK;
+}
+
 mfh_status packed_xform_segments(mfh_ctx *ctx, const XForm &xform, uint32_t m, uint32_t k,
                                  uint32_t count, const mfh_buf *const *codes,
                                  const mfh_buf *const *scales, const uint32_t *n,

@@ -50,6 +50,14 @@
 // writes the sum row.  It serves the LFM2 decode step's norm-fed NF4 and
 // ternary products (conv in-projections, grouped q/k/v).
 //
+// Convolution variant of the norm variant (the conv in-projection of the
+// decode step): block c computes rows c, h + c and 2h + c (the B, C and x
+// chunks of channel c), so its epilogue holds everything one token of the
+// gated short convolution of channel c needs and finishes it (ConvStep;
+// conv_step_kernel's arithmetic, so the outputs equal the two-launch form bit
+// for bit), rolling the history into the second buffer.  One launch per
+// convolution block instead of two.
+//
 // Decode (crates/kernels-simd/src/lib.rs:31-57,113-130,145-183):
 //   ternary  level = c - 1, c = 2-bit field (code 3 gives +2, as on the CPU):
 //            sum (c - 1) x = sum c x - sum x, with c converted by byte;
@@ -58,6 +66,8 @@
 //   NF4      a 256-entry LDS table of (low nibble, high nibble) level pairs.
 #include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
+
+#include <type_traits>
 
 #include "kernels.hpp"
 
@@ -99,6 +109,10 @@ struct VArgs {
     const uint16_t *seg_scales16[kMaxSegments];
     float *seg_out[kMaxSegments];
     uint32_t seg_n[kMaxSegments];
+    // Convolution variant: the block's rows are c, hidden + c and
+    // 2 hidden + c of its R channels c, and its epilogue finishes their
+    // one-token convolution (ConvStep).
+    ConvStep conv;
 };
 
 // Code words of one row's SL-wide slice: N words of EB bytes each (a slice
@@ -182,13 +196,15 @@ __device__ __forceinline__ float quad_add(float v)
     return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xF, 0xF, false));
 }
 
-template <Format F, int R, int SL, int NORM>
+template <Format F, int R, int SL, int NORM, bool CONV = false>
 __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
 {
     using SC = Slice<F, SL>;
     constexpr int LPG = 128 / SL;  // lanes per 128-group
+    // Rows per block: R, or the three chunks of R channels (CONV).
+    constexpr int RR = CONV ? 3 * R : R;
     __shared__ float2 pairs[F == Format::Nf4 ? 256 : 1];
-    __shared__ float red[kMaxWaves][R];
+    __shared__ float red[kMaxWaves][RR];
     __shared__ float squares_of[NORM ? kMaxWaves : 1];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // The block's weight stream (compile-time segment indices only: a
@@ -288,11 +304,13 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
         for (int j = 0; j < SL; ++j)
             x[j] = (x[j] * reciprocal) * w[j];
     }
-    unsigned codes[R][SC::N];
-    float scale[R];
+    unsigned codes[RR][SC::N];
+    float scale[RR];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const uint32_t row = row0 + r < n ? row0 + r : n - 1;
+    for (int r = 0; r < RR; ++r) {
+        // CONV: chunk r / R (B, C, x) of channel row0 + r % R.
+        const uint32_t want = CONV ? (r / R) * a.conv.hidden + row0 + r % R : row0 + r;
+        const uint32_t row = want < n ? want : n - 1;
         load_slice<SC::N, SC::EB>(codes_of + row * row_bytes + size_t(sl) * SC::bytes, codes[r]);
         const size_t si = size_t(row) * groups + sl / LPG;
         scale[r] = scales16_of ? __half2float(reinterpret_cast<const __half *>(scales16_of)[si])
@@ -307,9 +325,9 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
     if constexpr (F == Format::Nf4)
         __syncthreads();  // the level table
 
-    float val[R];
+    float val[RR];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
+    for (int r = 0; r < RR; ++r) {
         float v = slice_dot<F, SL, SC::N, SC::EB>(codes[r], x, pairs) - xsum;
         // Group sum over its lanes (all end equal), then the group's scale.
         v = quad_add<0xB1>(v);  // quad_perm [1, 0, 3, 2]
@@ -326,12 +344,41 @@ __global__ __launch_bounds__(64 * kMaxWaves) void vgemv_kernel(VArgs a)
     }
     if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < R; ++r)
+        for (int r = 0; r < RR; ++r)
             red[wave][r] = val[r];
     }
     __syncthreads();
     const int waves = blockDim.x >> 6;
-    if (tid < R) {
+    if constexpr (CONV) {
+        // Wave 0: lane r < 3R sums row r (the in-projection value), then
+        // lane c < R holds B, C and x of channel row0 + c and finishes
+        // conv_step_kernel's arithmetic for it.
+        if (wave == 0) {
+            const int r = tid < RR ? tid : 0;
+            float sum = red[0][r];
+            for (int w = 1; w < waves; ++w)
+                sum += red[w][r];
+            const float cgate = __shfl(sum, (tid + R) & 63, 64);
+            const float xval = __shfl(sum, (tid + 2 * R) & 63, 64);
+            const uint32_t channel = row0 + uint32_t(tid);
+            const ConvStep &cv = a.conv;
+            if (tid < R && channel < cv.hidden) {
+                const uint32_t rows = cv.width - 1;
+                const float u = sum * xval;
+                const float *taps = cv.kernel + uint64_t(channel) * cv.width;
+                float total = 0.0f;
+                for (uint32_t tap = 0; tap < rows; ++tap)
+                    total += taps[tap] * cv.history[uint64_t(tap) * cv.hidden + channel];
+                total += taps[rows] * u;
+                for (uint32_t rr = 0; rr + 1 < rows; ++rr)
+                    cv.next[uint64_t(rr) * cv.hidden + channel] =
+                        cv.history[uint64_t(rr + 1) * cv.hidden + channel];
+                if (rows)
+                    cv.next[uint64_t(rows - 1) * cv.hidden + channel] = u;
+                cv.out[channel] = total * cgate;
+            }
+        }
+    } else if (tid < R) {
         float sum = red[0][tid];
         for (int w = 1; w < waves; ++w)
             sum += red[w][tid];
@@ -452,6 +499,48 @@ bool try_norm(hipStream_t stream, const PackedCall &call)
 }
 
 }  // namespace
+
+bool try_vgemv_conv(hipStream_t stream, const PackedCall &call, const ConvStep &conv)
+{
+    const XForm &t = call.xform;
+    const uint32_t min_k = call.format == Format::Ternary ? kTernaryMinK : kNormMinK;
+    if (call.format == Format::Int8 || t.kind != XKind::AddRms || call.separate_prologue ||
+        call.segments || call.epilogue != Epilogue::Single || call.m != 1 || call.k < min_k ||
+        call.k > kMaxK || call.k % 128 || !t.a || !t.w || !aligned16(t.a) ||
+        (t.b && !aligned16(t.b)) || !aligned16(t.w) || (t.side && !aligned16(t.side)) ||
+        conv.hidden == 0 || call.n != 3 * conv.hidden || conv.width < 1 || !call.a.codes ||
+        !call.a.scales)
+        return false;
+    VArgs args{};
+    args.x = t.a;
+    args.right = t.b;
+    args.weight = t.w;
+    args.side = t.side;
+    args.epsilon = t.epsilon;
+    args.k = call.k;
+    args.codes = call.a.codes;
+    args.scales = call.a.scales;
+    args.scales16 = call.a.scales16;
+    args.n = call.n;
+    args.conv = conv;
+    // One channel (three rows) per block: LFM2 decode 1.2B shape 304.4 ->
+    // 293.9 ms per 512 tokens against the projection + conv_step_kernel
+    // launches, 350M 96.3 -> 94.0 ms per 256; two channels per block 300.5 /
+    // 96.2, four (the norm variant's row count) 314.5 / 101.8.
+    const unsigned waves = (args.k + 64 * 8 - 1) / (64 * 8);
+    auto go = [&](auto f_tag) {
+        constexpr Format F = decltype(f_tag)::value;
+        if (args.right)
+            vgemv_kernel<F, 1, 8, 1, true><<<conv.hidden, 64 * waves, 0, stream>>>(args);
+        else
+            vgemv_kernel<F, 1, 8, 2, true><<<conv.hidden, 64 * waves, 0, stream>>>(args);
+    };
+    if (call.format == Format::Ternary)
+        go(std::integral_constant<Format, Format::Ternary>{});
+    else
+        go(std::integral_constant<Format, Format::Nf4>{});
+    return true;
+}
 
 bool try_vgemv(hipStream_t stream, const PackedCall &call)
 {
