@@ -2474,6 +2474,159 @@ __global__ __launch_bounds__(1024) void wide_row_kernel(StreamArgs a)
     }
 }
 
+// Wide-matrix GEMV at two to eight activation rows, written for both
+// integer formats and launched for INT8 (launch_wide_rows): the plan of
+// wide_row_kernel (one wave per 256-k slice across R tiles, the
+// slices' sums added in slice order through LDS) with the register
+// prologue's fragment layout.  Lane 16q + 4b + p loads x[4f + b] at
+// k = 256 part + 64 s + 16q + 4p + 0..3 for the slice's four ksteps s and
+// forms digit p of them (reg_digits), so one MFMA per kstep, fragment and
+// tile serves four rows; each of the slice's two 128-groups keeps its own
+// accumulator.  Output lane block q holds batch 4f + q: the group sums,
+// scales and slice order are wide_row_kernel's, so each row's result is the
+// one-row kernel's bit for bit.  Rows at or beyond m read row 0 and are
+// zeroed.
+template <Format F, bool HALF, int P, int R, int NF>
+__global__ __launch_bounds__(1024) void wide_rows_kernel(StreamArgs a)
+{
+    static_assert(F != Format::Nf4, "integer formats");
+    using ST = typename ScaleT<HALF>::type;
+    using Blk = I8Block<F, 1, 1, NF, HALF>;
+    constexpr int W = 16;
+    constexpr int TS = W / P;                       // tiles per round
+    constexpr int L = WideGeo<F>::loads;
+    constexpr int KPL = WideGeo<F>::ksteps_per_load;
+    constexpr int NL = R * L;                       // lane loads per wave
+    constexpr int AH = NL < kWideAhead ? NL : kWideAhead;
+    constexpr int G = 2 * P;                        // 128-groups per tile
+    constexpr int LB = Geo<F>::lb;                  // ksteps per digit block
+    constexpr int NB = 4 / LB;                      // digit blocks per slice
+    constexpr int MB = 4 * NF;                      // batch rows held
+    __shared__ float partial[TS * R * P * MB * 16];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t part = wave % P, tslot = wave / P;
+    const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
+    auto tile_of = [&](int i) {
+        const uint32_t t = tile0 + uint32_t(TS * i);
+        return t < a.n_tiles ? t : a.n_tiles - 1;
+    };
+
+    // 1. The slice's activations: one float4 per kstep and fragment (K is
+    // 256 P, so every address lies in the row).
+    const uint32_t b = (lane >> 2) & 3;
+    const uint32_t off = 256 * part + 16 * q + 4 * (lane & 3);
+    RegX<LB> rx[NF][NB];
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+        const bool live = 4 * f + b < a.m;
+        const float *xrow = a.x + size_t(live ? 4 * f + b : 0) * a.k + off;
+#pragma unroll
+        for (int bi = 0; bi < NB; ++bi)
+#pragma unroll
+            for (int kk = 0; kk < LB; ++kk) {
+                const v4f v = *reinterpret_cast<const v4f *>(xrow + 64 * (bi * LB + kk));
+                rx[f][bi].v[kk] = live ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            }
+    }
+    // 2. Both group scales of every tile (this lane's row j), then the
+    // first weight loads.
+    ST sc[R][2];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int gs = 0; gs < 2; ++gs)
+            sc[i][gs] = reinterpret_cast<const ST *>(
+                a.scales)[(size_t(tile_of(i)) * G + 2 * part + gs) * 16 + j];
+    __builtin_amdgcn_sched_barrier(0);
+    v4u w[NL];
+    auto issue = [&](auto n_tag) {
+        constexpr int n = decltype(n_tag)::value;
+        const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
+                         (size_t(tile_of(n / L)) * (P * L) + part * L + n % L) * 64 + lane;
+        w[n] = __builtin_nontemporal_load(src);
+    };
+    unroll_groups<AH>(issue);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // 3. Digits, group factors and corrections of the slice.
+    Blk blk[NB];
+#pragma unroll
+    for (int bi = 0; bi < NB; ++bi)
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            reg_digits(rx[f][bi], blk[bi], f);
+
+    // 4. The tiles: products of the slice per group, then the combine.
+    unroll_groups<R>([&](auto i_tag) {
+        constexpr int i = decltype(i_tag)::value;
+        v4i acc[2][NF];
+#pragma unroll
+        for (int gs = 0; gs < 2; ++gs)
+#pragma unroll
+            for (int f = 0; f < NF; ++f)
+                acc[gs][f] = v4i{0, 0, 0, 0};
+        unroll_groups<L>([&](auto l_tag) {
+            constexpr int l = decltype(l_tag)::value;
+            constexpr int n = i * L + l;
+            if constexpr (n + AH < NL)
+                issue(std::integral_constant<int, n + AH>{});
+#pragma unroll
+            for (int ks = 0; ks < KPL; ++ks) {
+                const int s2 = l * KPL + ks;  // kstep within the slice
+                v4i bw;
+                if constexpr (F == Format::Ternary) {
+                    const unsigned word = w[n][ks];
+                    bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
+                             int(word & 0xC0C0C0C0u)};
+                } else {
+                    const v4u wv = w[n];
+                    bw = v4i{int(wv.x), int(wv.y), int(wv.z), int(wv.w)};
+                }
+#pragma unroll
+                for (int f = 0; f < NF; ++f)
+                    acc[s2 / 2][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                        blk[s2 / LB].af[s2 % LB][f], bw, acc[s2 / 2][f], 0, 0, 0);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+#pragma unroll
+        for (int f = 0; f < NF; ++f) {
+            // Each group's product is rounded before the add (no fused
+            // multiply-add), as the one-row kernel's cross-lane sum.
+#pragma clang fp contract(off)
+            float g[2];
+#pragma unroll
+            for (int gs = 0; gs < 2; ++gs) {
+                // Rows 4q + r: digit r of batch 4f + q.
+                const v4i d = acc[gs][f];
+                const int2 cv = blk[gs * 2 / LB].cv[gs % (LB / 2)][f];
+                const float xf = blk[gs * 2 / LB].xf[gs % (LB / 2)][f];
+                // |d.x| < 2^21, so the pairs combine exactly in int32.
+                const int hi = (d.x << 8) + d.y - cv.x;
+                const int lo = (d.z << 8) + d.w - cv.y;
+                const float gsum = float(hi) * 65536.0f + float(lo);
+                g[gs] = gsum * (to_f32<HALF>(sc[i][gs]) * xf);
+            }
+            partial[(((tslot + TS * i) * P + part) * MB + 4 * f + q) * 16 + j] = g[0] + g[1];
+        }
+    });
+
+    // 5. The slices of each (tile, batch row), added in order.
+    __syncthreads();
+    for (uint32_t v = threadIdx.x; v < uint32_t(TS * R * MB * 16); v += blockDim.x) {
+        const uint32_t tl = v / (MB * 16), bb = (v / 16) % MB, r = v % 16;
+        float sum = partial[((tl * P) * MB + bb) * 16 + r];
+#pragma unroll
+        for (int pp = 1; pp < P; ++pp)
+            sum += partial[((tl * P + pp) * MB + bb) * 16 + r];
+        const uint32_t t = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
+        const uint32_t row = t * 16 + r;
+        if (bb < a.m && t < a.n_tiles && row < a.n)
+            a.out[size_t(bb) * a.n + row] = sum;
+    }
+}
+
 // ---------------------------------------------------------------------------
 // Repack canonical codes into tiles, and scales into [tile][group][16].
 // ---------------------------------------------------------------------------
@@ -2893,14 +3046,35 @@ void launch_wide_row(hipStream_t stream, const StreamArgs &args)
     wide_row_kernel<F, HALF, P, R><<<blocks, 1024, 0, stream>>>(args);
 }
 
-// Serves a one-row product of a wide matrix (the LM heads at decode) with
-// wide_row_kernel; false leaves it to the other plans.
+// Tiles per wave of wide_rows_kernel: R = P, so each block's 16 waves cover
+// 16 tiles.  Measured at 65536 rows, INT8, B = 2 / 4 / 8 (us per launch, 1
+// GiB rotation): K = 2048 R = 8 22.1 / 22.0 / 22.9, R = 4 22.6 / 23.0 /
+// 25.3, R = 2 24.1 / 24.7 / 30.3 (the K-split plans 28.4 / 25.6 / 28.7);
+// K = 1024 R = 4 12.3 / 12.5 / 13.3, R = 8 15.1 / 15.2 / 16.1.  Ternary
+// stays on the streaming kernels: its digit prologue (the field
+// telescoping), repeated by every wave of a slice, cost more than it saved
+// (65536 x 2048, B = 2 / 4 / 8: R = 8 8.9 / 9.3 / 14.2 us against 8.1 / 8.9
+// / 14.3).
+template <Format F, bool HALF, int P, int NF>
+void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
+{
+    constexpr int R = P;
+    constexpr int TS = 16 / P;
+    const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
+    wide_rows_kernel<F, HALF, P, R, NF><<<blocks, 1024, 0, stream>>>(args);
+}
+
+// Serves a product of a wide matrix (the LM heads at decode) with
+// wide_row_kernel (one row) or wide_rows_kernel (INT8, two to eight rows);
+// false leaves it to the other plans.
 template <Format F>
 bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 {
+    const uint32_t max_m = F == Format::Int8 ? 8 : 1;
     if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
-        call.epilogue != Epilogue::Single || call.m != 1 || n_tiles < kHeadTiles ||
-        (call.k != 1024 && call.k != 2048) || (F == Format::Ternary && call.k != 1024) ||
+        call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
+        n_tiles < kHeadTiles || (call.k != 1024 && call.k != 2048) ||
+        (F == Format::Ternary && call.m == 1 && call.k != 1024) ||
         reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
         return false;
     StreamArgs args{};
@@ -2913,6 +3087,26 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     args.k = call.k;
     args.n_tiles = n_tiles;
     const bool half = call.a.tiled_half;
+    if constexpr (F == Format::Int8) {
+        if (call.m > 1) {
+            auto rows = [&](auto p_tag, auto nf_tag) {
+                constexpr int P = decltype(p_tag)::value, NF = decltype(nf_tag)::value;
+                if (half)
+                    launch_wide_rows<F, true, P, NF>(stream, args);
+                else
+                    launch_wide_rows<F, false, P, NF>(stream, args);
+            };
+            using One = std::integral_constant<int, 1>;
+            using Two = std::integral_constant<int, 2>;
+            if (call.k == 2048)
+                call.m <= 4 ? rows(std::integral_constant<int, 8>{}, One{})
+                            : rows(std::integral_constant<int, 8>{}, Two{});
+            else
+                call.m <= 4 ? rows(std::integral_constant<int, 4>{}, One{})
+                            : rows(std::integral_constant<int, 4>{}, Two{});
+            return true;
+        }
+    }
     if (call.k == 2048) {
         if (half)
             launch_wide_row<F, true, 8>(stream, args);

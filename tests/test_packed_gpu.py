@@ -188,6 +188,38 @@ def test_wide_matrix_shapes(backend, path, scheme, m, n, k):
     assert_close(got, want, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("scheme", ["ternary", "int8"])
+@pytest.mark.parametrize("k", [1024, 2048])
+def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k):
+    """Past 4096 row tiles with the last tile five rows long: two and five
+    activation rows (dead batch slots in the one- and two-fragment layouts)
+    against the oracle, and for INT8 every row of the batch equal bit for bit
+    to the same row multiplied alone (the multi-row wide kernel keeps the
+    one-row kernel's group and slice order)."""
+    say("wide rows", scheme, path, k)
+    n = 65541
+    codes, scales = make_weights(n, k, scheme, 0x5EED0008 + k)
+    cb, sb = upload_weights(backend, codes, scales)
+    x = convert.normal((5, k), 0xAC70021 + k)
+    alone = []
+    for b in range(5):
+        xb = backend.upload_f32((1, k), x[b:b + 1])
+        out = backend.allocate_f32((1, n))
+        backend.packed_linear(out, xb, cb, sb)
+        alone.append(backend.read(out)[0])
+    for m in (2, 5):
+        xb = backend.upload_f32((m, k), x[:m])
+        out = backend.allocate_f32((m, n))
+        backend.packed_linear(out, xb, cb, sb)
+        got = backend.read(out)
+        want = cached_oracle(("wide rows", scheme, m, n, k), x[:m], codes, scales)
+        assert max_rel_err(got, want) <= 1e-3
+        assert_close(got, want, 1e-4, 1e-4)
+        if path == "auto" and scheme == "int8":
+            for b in range(m):
+                assert np.array_equal(got[b], alone[b]), (m, b)
+
+
 # The prefill GEMM configuration: M in {512, 2048} tokens against 8192 x 2048
 # and 2048 x 8192 weights.  M = 512 is checked on every row; M = 2048 on a
 # seeded subset of rows (all N columns), the oracle being a scalar CPU path.
