@@ -2191,6 +2191,78 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
 // ---------------------------------------------------------------------------
 constexpr int kWideAhead = 3;  // 16-byte lane loads in flight per wave
 
+// The packed one-row operand layout (wide_row_kernel, wide_pair_kernel):
+// lane 16q + 4s + p holds x[64 s + 16 q + 4 p + t], t = 0..3, of a 256-k
+// slice (s: the slice's kstep, which lane bit 3 splits into its two
+// 128-groups).  The group's exponent (|x| < 2^e) reduces over lane bits 0-2
+// and the lane blocks; `bad` marks a group holding a non-finite value.
+__device__ __forceinline__ void packed_group_exponent(const float (&v)[4], int &e, bool &bad)
+{
+    unsigned mb = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
+    mb = max(mb, quad_xor1(mb));
+    mb = max(mb, quad_xor2(mb));
+    mb = max(mb, half_mirror(mb));
+    mb = max_xor16(mb);
+    mb = max_xor32(mb);
+    bad = mb >= 0x7F800000u;
+    e = 0;
+    if (!bad && mb)
+        frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+}
+
+// Integer formats, packed layout: the lane's A fragment for its own kstep
+// (digit p = lane & 3 of the quad's 16 values, as reg_digits forms it) and,
+// for ternary, the group correction split as hi * 2^16 + lo (zero for INT8).
+template <Format F>
+__device__ __forceinline__ v4i packed_digits(const float (&v)[4], int e, bool bad, int2 &cv)
+{
+    const uint32_t p = threadIdx.x & 3;
+    long long corr = 0;
+    unsigned vp[4];
+    int u_prev = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        int val = bad ? 0 : int(rintf(ldexpf(v[t], 30 - e)));
+        if constexpr (F == Format::Ternary) {
+            // Field t of the nested masks (see the operand-field note).
+            const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
+            val = t == 0 ? u : u - u_prev;
+            u_prev = u;
+            corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
+                          : -(static_cast<long long>(u) << 6);
+        }
+        vp[t] = unsigned(val + 0x808080);
+    }
+    unsigned d[4], wd[4];
+    byte_transpose<true>(vp, d);
+    quad_transpose(d, p);
+    if constexpr (F == Format::Ternary) {
+        byte_transpose<false>(d, wd);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            wd[i] = d[i];
+    }
+    const unsigned flip = p ? 0x80808080u : 0u;
+    cv = int2{0, 0};
+    if constexpr (F == Format::Ternary) {
+        corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
+                (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
+        corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
+                (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
+        corr += static_cast<long long>(half_mirror(unsigned(corr))) |
+                (static_cast<long long>(half_mirror(unsigned(corr >> 32))) << 32);
+        corr = sum_xor16(corr);
+        corr = sum_xor32(corr);
+        const long long lo = ((corr + 32768) & 65535) - 32768;
+        cv = int2{int((corr - lo) >> 16), int(lo)};
+    }
+    return v4i{int(wd[0] ^ flip), int(wd[1] ^ flip), int(wd[2] ^ flip), int(wd[3] ^ flip)};
+}
+
 template <Format F>
 struct WideGeo {
     // Lane loads per (tile, slice) and ksteps per lane load.
@@ -2263,21 +2335,9 @@ __global__ __launch_bounds__(1024) void wide_row_kernel(StreamArgs a)
 #pragma unroll
     for (int t = 0; t < 4; ++t)
         v[t] = inb ? xv[t] : 0.0f;
-    unsigned mb = 0;
-#pragma unroll
-    for (int t = 0; t < 4; ++t)
-        mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
-    // Group lanes: integer formats bits 0-2 (digit p, kstep bit 0) and the
-    // lane blocks; NF4 bits 0-2 (half, kstep bits 0-1) and the lane blocks.
-    mb = max(mb, quad_xor1(mb));
-    mb = max(mb, quad_xor2(mb));
-    mb = max(mb, half_mirror(mb));
-    mb = max_xor16(mb);
-    mb = max_xor32(mb);
-    const bool bad = mb >= 0x7F800000u;
-    int e = 0;
-    if (!bad && mb)
-        frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+    int e;
+    bool bad;
+    packed_group_exponent(v, e, bad);
     typedef typename std::conditional<NF4, v8h, v4i>::type AT;
     AT af;
     float factor;
@@ -2301,48 +2361,7 @@ __global__ __launch_bounds__(1024) void wide_row_kernel(StreamArgs a)
         af = __builtin_bit_cast(v8h, d);
     } else {
         factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
-        const uint32_t p = lane & 3;
-        long long corr = 0;
-        unsigned vp[4];
-        int u_prev = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            int val = bad ? 0 : int(rintf(ldexpf(v[t], 30 - e)));
-            if constexpr (F == Format::Ternary) {
-                // Field t of the nested masks (see the operand-field note).
-                const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
-                val = t == 0 ? u : u - u_prev;
-                u_prev = u;
-                corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
-                              : -(static_cast<long long>(u) << 6);
-            }
-            vp[t] = unsigned(val + 0x808080);
-        }
-        unsigned d[4], wd[4];
-        byte_transpose<true>(vp, d);
-        quad_transpose(d, p);
-        if constexpr (F == Format::Ternary) {
-            byte_transpose<false>(d, wd);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 4; ++i)
-                wd[i] = d[i];
-        }
-        const unsigned flip = p ? 0x80808080u : 0u;
-        af = v4i{int(wd[0] ^ flip), int(wd[1] ^ flip), int(wd[2] ^ flip), int(wd[3] ^ flip)};
-        if constexpr (F == Format::Ternary) {
-            corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
-                    (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
-            corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
-                    (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
-            corr += static_cast<long long>(half_mirror(unsigned(corr))) |
-                    (static_cast<long long>(half_mirror(unsigned(corr >> 32))) << 32);
-            corr = sum_xor16(corr);
-            corr = sum_xor32(corr);
-            // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
-            const long long lo = ((corr + 32768) & 65535) - 32768;
-            cv = int2{int((corr - lo) >> 16), int(lo)};
-        }
+        af = packed_digits<F>(v, e, bad, cv);
     }
     // The combine of lane block q' uses group q' / 2 of the slice, whose
     // constants lanes 8 (q' / 2) .. hold.
@@ -2624,6 +2643,170 @@ __global__ __launch_bounds__(1024) void wide_rows_kernel(StreamArgs a)
         const uint32_t row = t * 16 + r;
         if (bb < a.m && t < a.n_tiles && row < a.n)
             a.out[size_t(bb) * a.n + row] = sum;
+    }
+}
+
+// Two-stream wide GEMV at one activation row (the ternary FFN gate/up pair at
+// decode): the packed one-row layout of wide_row_kernel over both weight
+// streams of R tiles per wave, with the Pair or SwiGLU epilogue.  A block's
+// waves are TS tile slots x P slices of 256 k (K = 256 P).  NORM forms the
+// add + RMS norm in the slices: each wave loads its four values of a, b and
+// the norm weight, the first tile slot's waves sum the squares of their
+// slices (wave sums, then slice order through LDS), every wave takes
+// x = (s * reciprocal) * weight, and block 0's first tile slot writes
+// s = a + b to the side output.
+struct WidePairArgs {
+    XForm xform;  // Plain: a = x
+    const uint8_t *tiles[2];
+    const void *scales[2];
+    float *out[2];
+    uint32_t n, k, n_tiles;
+};
+
+template <bool HALF, int P, int TS, int R, bool NORM, Epilogue E>
+__global__ __launch_bounds__(64 * TS * P) void wide_pair_kernel(WidePairArgs a)
+{
+    static_assert(E != Epilogue::Single, "two streams");
+    using ST = typename ScaleT<HALF>::type;
+    constexpr int G = 2 * P;  // 128-groups per tile
+    __shared__ float partial[TS * R * 2 * P * 16];
+    __shared__ float squares_part[P];
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t q = lane >> 4, j = lane & 15;
+    const uint32_t part = wave % P, tslot = wave / P;
+    const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
+    auto tile_of = [&](int i) {
+        const uint32_t t = tile0 + uint32_t(TS * i);
+        return t < a.n_tiles ? t : a.n_tiles - 1;
+    };
+    const XForm &t = a.xform;
+
+    // 1. The slice's activations (and norm operands): one float4 each.
+    const uint32_t kx = 256 * part + 64 * ((lane >> 2) & 3) + 16 * q + 4 * (lane & 3);
+    const v4f av = *reinterpret_cast<const v4f *>(t.a + kx);
+    v4f bv{0.0f, 0.0f, 0.0f, 0.0f}, wv{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (NORM) {
+        if (t.b)
+            bv = *reinterpret_cast<const v4f *>(t.b + kx);
+        wv = *reinterpret_cast<const v4f *>(t.w + kx);
+    }
+    // 2. Group scales (group 2 part + q / 2, row j) and the weights.
+    const uint32_t my_group = 2 * part + (q >> 1);
+    ST sc[2][R];
+    v4u w[2][R];
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+            sc[st][i] = reinterpret_cast<const ST *>(
+                a.scales[st])[(size_t(tile_of(i)) * G + my_group) * 16 + j];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+            w[st][i] = __builtin_nontemporal_load(
+                reinterpret_cast<const v4u *>(a.tiles[st]) +
+                (size_t(tile_of(i)) * P + part) * 64 + lane);
+
+    // 3. The norm, then the operands.
+    float v[4];
+    if constexpr (NORM) {
+        v4f sv = av;
+        if (t.b)
+            sv = av + bv;
+        float squares = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            squares += sv[e] * sv[e];
+        squares = wave_sum_f(squares);
+        if (tslot == 0 && lane == 0)
+            squares_part[part] = squares;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp)
+            total += squares_part[pp];
+        const float reciprocal = rms_reciprocal(total, a.k, t.epsilon);
+        if (blockIdx.x == 0 && tslot == 0 && t.side)
+            *reinterpret_cast<v4f *>(t.side + kx) = sv;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = (sv[e] * reciprocal) * wv[e];
+    } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = av[e];
+    }
+    int e;
+    bool bad;
+    packed_group_exponent(v, e, bad);
+    const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
+    int2 cv;
+    const v4i af = packed_digits<Format::Ternary>(v, e, bad, cv);
+    // Lane block q's combine uses group q / 2, whose constants lanes
+    // 8 (q / 2) .. hold.
+    const int src_lane = 8 * int(q >> 1);
+    const float my_factor = __shfl(factor, src_lane, 64);
+    const int2 my_corr = int2{__shfl(cv.x, src_lane, 64), __shfl(cv.y, src_lane, 64)};
+    const uint32_t own = j >> 2;
+    v4i as[4];
+#pragma unroll
+    for (int s2 = 0; s2 < 4; ++s2)
+        as[s2] = own == uint32_t(s2) ? af : v4i{0, 0, 0, 0};
+
+    // 4. Products of the slice per (tile, stream), then the combine.
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            v4i acc = v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const unsigned word = w[st][i][ks];
+                const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
+                                   int(word & 0xC0C0C0C0u)};
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[ks], bw, acc, 0, 0, 0);
+            }
+            // Rows 4q' + r: digit r of kstep q'; the group's two ksteps
+            // are lane blocks q' and q' ^ 1.
+            int d[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const auto pr = __builtin_amdgcn_permlane16_swap(unsigned(acc[r]),
+                                                                 unsigned(acc[r]), false, false);
+                d[r] = int(pr[0]) + int(pr[1]);
+            }
+            const int hi = (d[0] << 8) + d[1] - my_corr.x;
+            const int lo = (d[2] << 8) + d[3] - my_corr.y;
+            const float gsum = float(hi) * 65536.0f + float(lo);
+            float total = gsum * (to_f32<HALF>(sc[st][i]) * my_factor);
+            total = sum_xor32(total);  // the slice's two groups
+            if (q == 0)
+                partial[(((tslot + TS * i) * 2 + st) * P + part) * 16 + j] = total;
+        }
+
+    // 5. The slices of each tile and stream, added in order; the epilogue.
+    __syncthreads();
+    if (threadIdx.x < uint32_t(TS * R * 16)) {
+        const uint32_t tl = threadIdx.x / 16, r = threadIdx.x % 16;
+        float sum[2];
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+            sum[st] = partial[((tl * 2 + st) * P) * 16 + r];
+#pragma unroll
+            for (int pp = 1; pp < P; ++pp)
+                sum[st] += partial[((tl * 2 + st) * P + pp) * 16 + r];
+        }
+        const uint32_t tt = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
+        const uint32_t row = tt * 16 + r;
+        if (tt < a.n_tiles && row < a.n) {
+            if constexpr (E == Epilogue::Pair) {
+                a.out[0][row] = sum[0];
+                a.out[1][row] = sum[1];
+            } else {
+                a.out[0][row] = silu_mul(sum[0], sum[1]);
+            }
+        }
     }
 }
 
@@ -3121,6 +3304,77 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     return true;
 }
 
+// One tile slot per block (P waves), one tile per wave.  Measured in the
+// LFM2 greedy decode (tok/s, fused step / op by op): 1.2B shape (8192 x
+// 2048 pairs) 2052 / 1443 with TS = 1, 2029 / 1467 with TS = 2, 2050 /
+// 1443 with TS = 4, against 1743 / 1315 on the register-prologue plans;
+// 350M shape (4608 x 1024) 3094 / 1986, 3085 / 1757, 2960 / 1763, against
+// 2741 / 1875.
+template <bool HALF, int P, bool NORM, Epilogue E>
+void launch_wide_pair(hipStream_t stream, const WidePairArgs &args)
+{
+    constexpr int TS = 1, R = 1;
+    const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
+    wide_pair_kernel<HALF, P, TS, R, NORM, E><<<blocks, 64 * TS * P, 0, stream>>>(args);
+}
+
+// Serves a ternary two-stream product at one row (plain activations or the
+// add + RMS norm, Pair or SwiGLU epilogue) with wide_pair_kernel; false
+// leaves it to the other plans.
+bool try_wide_pair(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
+{
+    const XForm &t = call.xform;
+    auto aligned = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    const bool norm = t.kind == XKind::AddRms;
+    if (call.format != Format::Ternary || call.separate_prologue || call.segments ||
+        call.epilogue == Epilogue::Single || call.m != 1 || (call.k != 1024 && call.k != 2048) ||
+        (t.kind != XKind::Plain && !norm) || !call.b.tiles)
+        return false;
+    const float *x = norm ? t.a : call.x;
+    if (!x || !aligned(x) ||
+        (norm && (!t.w || !aligned(t.w) || (t.b && !aligned(t.b)) || (t.side && !aligned(t.side)))))
+        return false;
+    if (call.a.tiled_half != call.b.tiled_half)
+        return false;
+    WidePairArgs args{};
+    args.xform = t;
+    args.xform.a = x;
+    args.tiles[0] = call.a.tiles;
+    args.tiles[1] = call.b.tiles;
+    args.scales[0] = call.a.tiled_scales;
+    args.scales[1] = call.b.tiled_scales;
+    args.out[0] = call.out_a;
+    args.out[1] = call.out_b;
+    args.n = call.n;
+    args.k = call.k;
+    args.n_tiles = n_tiles;
+    auto go = [&](auto half_tag, auto p_tag, auto norm_tag) {
+        constexpr bool H = decltype(half_tag)::value, N = decltype(norm_tag)::value;
+        constexpr int P = decltype(p_tag)::value;
+        if (call.epilogue == Epilogue::Pair)
+            launch_wide_pair<H, P, N, Epilogue::Pair>(stream, args);
+        else
+            launch_wide_pair<H, P, N, Epilogue::SwigluPair>(stream, args);
+    };
+    auto by_norm = [&](auto half_tag, auto p_tag) {
+        if (norm)
+            go(half_tag, p_tag, std::true_type{});
+        else
+            go(half_tag, p_tag, std::false_type{});
+    };
+    auto by_k = [&](auto half_tag) {
+        if (call.k == 2048)
+            by_norm(half_tag, std::integral_constant<int, 8>{});
+        else
+            by_norm(half_tag, std::integral_constant<int, 4>{});
+    };
+    if (call.a.tiled_half)
+        by_k(std::true_type{});
+    else
+        by_k(std::false_type{});
+    return true;
+}
+
 template <Format F>
 void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
 {
@@ -3132,6 +3386,8 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     if (try_wide_row<F>(stream, call, n_tiles))
         return;
     if constexpr (F == Format::Ternary) {
+        if (try_wide_pair(stream, call, n_tiles))
+            return;
         if (try_stream_ternary(stream, call, n_tiles))
             return;
     }

@@ -572,13 +572,14 @@ def test_pair_and_swiglu_variants(backend, path, scheme, m):
 
 @pytest.mark.parametrize("scheme", SCHEMES)
 @pytest.mark.parametrize("m", [1, 2, 4])
-def test_pair_ffn_shape(backend, path, scheme, m):
-    # The LFM2-1.2B FFN gate/up shape: 8192 rows per stream at K = 2048, where
-    # the plain pair takes the 8-wave register-prologue plan.
-    say("pair ffn shape", scheme, path, m)
-    n, k = 8192, 2048
-    ca, sa = make_weights(n, k, scheme, 0x5EED0410)
-    cb, sb = make_weights(n, k, scheme, 0x5EED0411)
+@pytest.mark.parametrize("n,k", [(8192, 2048), (4608, 1024), (4613, 1024)])
+def test_pair_ffn_shape(backend, path, scheme, m, n, k):
+    # The LFM2 FFN gate/up shapes (1.2B: 8192 rows per stream at K = 2048;
+    # 350M: 4608 at K = 1024; and a partial last tile): one ternary row takes
+    # the two-stream wide kernel, more rows the register-prologue plans.
+    say("pair ffn shape", scheme, path, m, n, k)
+    ca, sa = make_weights(n, k, scheme, 0x5EED0410 + n)
+    cb, sb = make_weights(n, k, scheme, 0x5EED0411 + n)
     x = convert.normal((m, k), 0xAC70410 + m)
     ga, gsa = upload_weights(backend, ca, sa)
     gb, gsb = upload_weights(backend, cb, sb)
