@@ -2271,11 +2271,10 @@ struct WideGeo {
     static constexpr int ksteps = loads * ksteps_per_load;  // 4, 8, 4
 };
 
-template <Format F, bool HALF, int P, int R>
-__global__ __launch_bounds__(1024) void wide_row_kernel(StreamArgs a)
+template <Format F, bool HALF, int P, int R, int W = 16>
+__global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 {
     using ST = typename ScaleT<HALF>::type;
-    constexpr int W = 16;
     constexpr int TS = W / P;                      // tiles per round
     constexpr int L = WideGeo<F>::loads;
     constexpr int KPL = WideGeo<F>::ksteps_per_load;
@@ -3220,9 +3219,21 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
 // 18.4-21.8; K = 1024 R = 4 8.9-10.5 against 10.9-12.1.  Ternary K = 1024
 // R = 4 5.6-5.9 against the rows kernel's 5.9-6.2; at K = 2048 the rows
 // kernel (7.5 us) beats R = 8 (8.1-8.6), which keeps it.
+// Below kHeadTiles row tiles (the decode projections) one tile per wave and
+// one block of P waves per tile (W = P, R = 1).  Measured at one row (us per
+// launch, rotation) against the plans they replace: ternary 2048 x 2048
+// 4.10 -> 3.29-3.37, 8192 x 2048 5.84 -> 4.07, 4608 x 1024 4.26 -> 3.37
+// (K-split register prologue); NF4 2048 x 2048 4.97 -> 3.68, 8192 x 2048
+// 7.13 -> 4.88 (f32 vector GEMV); INT8 8192 x 2048 6.09 -> 4.84, 2048 x 2048
+// 3.71 -> 3.59.  LFM2 greedy decode, 1.2B shape 2073 -> 2168 tok/s (op by
+// op 1439 -> 1585), 350M 3053 -> 3047 (op by op 1741 -> 1923).
 template <Format F, bool HALF, int P>
 void launch_wide_row(hipStream_t stream, const StreamArgs &args)
 {
+    if (args.n_tiles < kHeadTiles) {
+        wide_row_kernel<F, HALF, P, 1, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
+        return;
+    }
     constexpr int R = F == Format::Nf4 && P == 8 ? 8 : 4;
     constexpr int TS = 16 / P;
     const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
@@ -3247,17 +3258,19 @@ void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
     wide_rows_kernel<F, HALF, P, R, NF><<<blocks, 1024, 0, stream>>>(args);
 }
 
-// Serves a product of a wide matrix (the LM heads at decode) with
-// wide_row_kernel (one row) or wide_rows_kernel (INT8, two to eight rows);
-// false leaves it to the other plans.
+// Serves a one-row product at K = 1024 or 2048 with wide_row_kernel, and
+// a wide matrix (the LM heads at decode) at two to eight rows with
+// wide_rows_kernel (INT8); false leaves it to the other plans.  The
+// ternary head at K = 2048 keeps the streaming rows kernel.
 template <Format F>
 bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 {
     const uint32_t max_m = F == Format::Int8 ? 8 : 1;
+    const bool head = n_tiles >= kHeadTiles;
     if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
-        n_tiles < kHeadTiles || (call.k != 1024 && call.k != 2048) ||
-        (F == Format::Ternary && call.m == 1 && call.k != 1024) ||
+        (call.m > 1 && !head) || (call.k != 1024 && call.k != 2048) ||
+        (F == Format::Ternary && head && call.k != 1024) ||
         reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
         return false;
     StreamArgs args{};
@@ -3381,9 +3394,9 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
-    if (try_vgemv(stream, call))
-        return;
     if (try_wide_row<F>(stream, call, n_tiles))
+        return;
+    if (try_vgemv(stream, call))
         return;
     if constexpr (F == Format::Ternary) {
         if (try_wide_pair(stream, call, n_tiles))
@@ -3581,9 +3594,9 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t k_pad = pad_to(call.k, 128);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
-    if (try_vgemv(stream, call))
-        return;
     if (try_wide_row<Format::Nf4>(stream, call, n_tiles))
+        return;
+    if (try_vgemv(stream, call))
         return;
     if (try_stream_nf4(stream, call, n_tiles))
         return;

@@ -188,6 +188,21 @@ def test_wide_matrix_shapes(backend, path, scheme, m, n, k):
     assert_close(got, want, 1e-4, 1e-4)
 
 
+@pytest.mark.parametrize("scheme", SCHEMES)
+@pytest.mark.parametrize("n", [1, 17, 130])
+@pytest.mark.parametrize("k", [1024, 2048])
+def test_one_row_few_tiles(backend, path, scheme, n, k):
+    """One activation row against one, two and nine row tiles (one block of
+    K / 256 waves per tile), the last tile partial."""
+    say("one row few tiles", scheme, path, n, k)
+    codes, scales = make_weights(n, k, scheme, 0x5EED0009 + n + k)
+    x = convert.normal((1, k), 0xAC70031 + n + k)
+    got = run_linear(backend, x, codes, scales)
+    want = oracle.packed_linear(x, codes, scales)
+    assert max_rel_err(got, want) <= 1e-3
+    assert_close(got, want, 1e-4, 1e-4)
+
+
 @pytest.mark.parametrize("scheme", ["ternary", "int8"])
 @pytest.mark.parametrize("k", [1024, 2048])
 def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k):
