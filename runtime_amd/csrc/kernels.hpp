@@ -102,7 +102,8 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
 
 // The decode step's convolution block input: the in-projection of `codes`
 // (3 * conv.hidden rows of width k) over add + RMS norm activations with
-// the one-token convolution folded into its epilogue (try_vgemv_conv).
+// the one-token convolution folded into its epilogue (try_wide_conv where
+// it applies, else try_vgemv_conv).
 // MFH_UNSUPPORTED, before anything is enqueued, where it does not apply.
 mfh_status packed_xform_conv(mfh_ctx *ctx, const XForm &xform, uint32_t k,
                              const mfh_buf *codes, const mfh_buf *scales, const ConvStep &conv);
@@ -126,6 +127,12 @@ bool try_vgemv(hipStream_t stream, const PackedCall &call);
 // with the convolution folded in; false, with nothing enqueued, where the
 // vector GEMV does not serve the call.
 bool try_vgemv_conv(hipStream_t stream, const PackedCall &call, const ConvStep &conv);
+// The same on the one-row wide matrix-core kernel (packed_mfma.hip), which
+// reads the repacked tiles: whether it applies (checked before the tiles
+// are prepared), and the launch (false where it does not apply or the
+// tiles are missing).
+bool wide_conv_supported(const PackedCall &call, const ConvStep &conv);
+bool try_wide_conv(hipStream_t stream, const PackedCall &call, const ConvStep &conv);
 // Matrix-core decode GEMV for m <= 8 (needs `tiles` and `tiled_scales` on
 // every stream).  `scratch` holds gemv_mfma_scratch_bytes(call) bytes.
 bool gemv_mfma_supported(Format format);

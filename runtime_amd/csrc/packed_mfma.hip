@@ -2645,80 +2645,113 @@ __global__ __launch_bounds__(1024) void wide_rows_kernel(StreamArgs a)
     }
 }
 
-// Two-stream wide GEMV at one activation row (the ternary FFN gate/up pair at
-// decode): the packed one-row layout of wide_row_kernel over both weight
-// streams of R tiles per wave, with the Pair or SwiGLU epilogue.  A block's
-// waves are TS tile slots x P slices of 256 k (K = 256 P).  NORM forms the
-// add + RMS norm in the slices: each wave loads its four values of a, b and
-// the norm weight, the first tile slot's waves sum the squares of their
-// slices (wave sums, then slice order through LDS), every wave takes
-// x = (s * reciprocal) * weight, and block 0's first tile slot writes
-// s = a + b to the side output.
-struct WidePairArgs {
+// One-row wide GEMV for the decode projections (m = 1): the packed one-row
+// operand layout of wide_row_kernel with one block of P waves per row tile,
+// each wave SPW consecutive 256-k slices (K = 256 P SPW), over S weight
+// streams: one (Single), two (Pair, SwigluPair), or three row regions of
+// one matrix (the convolution in-projection: rows c, h + c and 2h + c of
+// channel c, finished by conv_step_kernel's arithmetic).  The activation
+// transform forms x in the slices: Plain; AddRms (s = a + b, the block sums
+// the squares of its waves in wave order, x = (s * reciprocal) * weight,
+// block 0 writes s to the side output); Swiglu (x = silu(a) * b).  Each
+// (stream, slice) sums its two 128-groups as wide_row_kernel; a wave adds
+// its slices in order, and the block adds the waves in order.
+struct WideArgs {
     XForm xform;  // Plain: a = x
     const uint8_t *tiles[2];
     const void *scales[2];
     float *out[2];
-    uint32_t n, k, n_tiles;
+    uint32_t n, k;
+    uint32_t stream_tiles;  // S = 3: region s starts at tile s * stream_tiles
+    ConvStep conv;          // S = 3
 };
 
-template <bool HALF, int P, int TS, int R, bool NORM, Epilogue E>
-__global__ __launch_bounds__(64 * TS * P) void wide_pair_kernel(WidePairArgs a)
+template <Format F, bool HALF, int P, int SPW, int S, XKind PRO, Epilogue E>
+__global__ __launch_bounds__(64 * P) void wide_one_kernel(WideArgs a)
 {
-    static_assert(E != Epilogue::Single, "two streams");
+    static_assert(S == 1 || S == 2 || S == 3, "one, two or three weight streams");
+    static_assert((S == 2) == (E != Epilogue::Single), "two streams for the pair epilogues");
     using ST = typename ScaleT<HALF>::type;
-    constexpr int G = 2 * P;  // 128-groups per tile
-    __shared__ float partial[TS * R * 2 * P * 16];
+    constexpr bool NF4 = F == Format::Nf4;
+    constexpr int L = WideGeo<F>::loads;             // lane loads per (tile, slice)
+    constexpr int KPL = WideGeo<F>::ksteps_per_load;
+    constexpr int G = 2 * P * SPW;                   // 128-groups per tile
+    __shared__ float partial[S * P * 16];
     __shared__ float squares_part[P];
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __shared__ unsigned lut[NF4 ? 256 * 2 * kStreamLutCopies : 1];
+    __shared__ uint2 entries[NF4 ? 256 : 1];
+    const uint32_t lane = threadIdx.x & 63, part = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t part = wave % P, tslot = wave / P;
-    const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
-    auto tile_of = [&](int i) {
-        const uint32_t t = tile0 + uint32_t(TS * i);
-        return t < a.n_tiles ? t : a.n_tiles - 1;
-    };
     const XForm &t = a.xform;
+    auto tile_of = [&](int st) {
+        return S == 3 ? blockIdx.x + uint32_t(st) * a.stream_tiles : blockIdx.x;
+    };
+    auto tiles_of = [&](int st) { return S == 3 ? a.tiles[0] : a.tiles[st]; };
+    auto scales_of = [&](int st) { return S == 3 ? a.scales[0] : a.scales[st]; };
 
-    // 1. The slice's activations (and norm operands): one float4 each.
-    const uint32_t kx = 256 * part + 64 * ((lane >> 2) & 3) + 16 * q + 4 * (lane & 3);
-    const v4f av = *reinterpret_cast<const v4f *>(t.a + kx);
-    v4f bv{0.0f, 0.0f, 0.0f, 0.0f}, wv{0.0f, 0.0f, 0.0f, 0.0f};
-    if constexpr (NORM) {
-        if (t.b)
-            bv = *reinterpret_cast<const v4f *>(t.b + kx);
-        wv = *reinterpret_cast<const v4f *>(t.w + kx);
+    // 1. The slices' activations (and transform operands): one float4 each.
+    uint32_t kx[SPW];
+    v4f av[SPW], bv[SPW], wv[SPW];
+#pragma unroll
+    for (int sp = 0; sp < SPW; ++sp) {
+        const uint32_t slice = part * SPW + sp;
+        kx[sp] = NF4 ? 256 * slice + 32 * ((lane >> 1) & 7) + 8 * q + 4 * (lane & 1)
+                     : 256 * slice + 64 * ((lane >> 2) & 3) + 16 * q + 4 * (lane & 3);
+        av[sp] = *reinterpret_cast<const v4f *>(t.a + kx[sp]);
+        bv[sp] = wv[sp] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+        if constexpr (PRO == XKind::Swiglu)
+            bv[sp] = *reinterpret_cast<const v4f *>(t.b + kx[sp]);
+        if constexpr (PRO == XKind::AddRms) {
+            if (t.b)
+                bv[sp] = *reinterpret_cast<const v4f *>(t.b + kx[sp]);
+            wv[sp] = *reinterpret_cast<const v4f *>(t.w + kx[sp]);
+        }
     }
-    // 2. Group scales (group 2 part + q / 2, row j) and the weights.
-    const uint32_t my_group = 2 * part + (q >> 1);
-    ST sc[2][R];
-    v4u w[2][R];
+    // 2. Group scales (group 2 slice + q / 2, row j) and every weight load.
+    ST sc[S][SPW];
+    v4u w[S][SPW][L];
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
+    for (int st = 0; st < S; ++st)
 #pragma unroll
-        for (int i = 0; i < R; ++i)
-            sc[st][i] = reinterpret_cast<const ST *>(
-                a.scales[st])[(size_t(tile_of(i)) * G + my_group) * 16 + j];
+        for (int sp = 0; sp < SPW; ++sp)
+            sc[st][sp] = reinterpret_cast<const ST *>(scales_of(st))
+                [(size_t(tile_of(st)) * G + 2 * (part * SPW + sp) + (q >> 1)) * 16 + j];
 #pragma unroll
-    for (int i = 0; i < R; ++i)
+    for (int st = 0; st < S; ++st)
 #pragma unroll
-        for (int st = 0; st < 2; ++st)
-            w[st][i] = __builtin_nontemporal_load(
-                reinterpret_cast<const v4u *>(a.tiles[st]) +
-                (size_t(tile_of(i)) * P + part) * 64 + lane);
+        for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+                w[st][sp][l] = __builtin_nontemporal_load(
+                    reinterpret_cast<const v4u *>(tiles_of(st)) +
+                    (size_t(tile_of(st)) * (P * SPW * L) + (part * SPW + sp) * L + l) * 64 +
+                    lane);
 
-    // 3. The norm, then the operands.
-    float v[4];
-    if constexpr (NORM) {
-        v4f sv = av;
-        if (t.b)
-            sv = av + bv;
+    // 3. NF4: the code-byte table (as wide_row_kernel's).
+    if constexpr (NF4) {
+        if (threadIdx.x < 256)
+            entries[threadIdx.x] = nf4_lut_entry(threadIdx.x);
+        __syncthreads();
+        for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
+            const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
+            reinterpret_cast<v4u *>(lut)[v] = v4u{e.x, e.y, e.x, e.y};
+        }
+    }
+
+    // 4. The transform.
+    float v[SPW][4];
+    if constexpr (PRO == XKind::AddRms) {
+        v4f sv[SPW];
         float squares = 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            squares += sv[e] * sv[e];
+        for (int sp = 0; sp < SPW; ++sp) {
+            sv[sp] = t.b ? av[sp] + bv[sp] : av[sp];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                squares += sv[sp][e] * sv[sp][e];
+        }
         squares = wave_sum_f(squares);
-        if (tslot == 0 && lane == 0)
+        if (lane == 0)
             squares_part[part] = squares;
         __syncthreads();
         float total = 0.0f;
@@ -2726,80 +2759,186 @@ __global__ __launch_bounds__(64 * TS * P) void wide_pair_kernel(WidePairArgs a)
         for (int pp = 0; pp < P; ++pp)
             total += squares_part[pp];
         const float reciprocal = rms_reciprocal(total, a.k, t.epsilon);
-        if (blockIdx.x == 0 && tslot == 0 && t.side)
-            *reinterpret_cast<v4f *>(t.side + kx) = sv;
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            v[e] = (sv[e] * reciprocal) * wv[e];
+        for (int sp = 0; sp < SPW; ++sp) {
+            if (blockIdx.x == 0 && t.side)
+                *reinterpret_cast<v4f *>(t.side + kx[sp]) = sv[sp];
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[sp][e] = (sv[sp][e] * reciprocal) * wv[sp][e];
+        }
     } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-            v[e] = av[e];
+        for (int sp = 0; sp < SPW; ++sp)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[sp][e] = PRO == XKind::Swiglu ? silu_mul(av[sp][e], bv[sp][e]) : av[sp][e];
     }
-    int e;
-    bool bad;
-    packed_group_exponent(v, e, bad);
-    const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
-    int2 cv;
-    const v4i af = packed_digits<Format::Ternary>(v, e, bad, cv);
-    // Lane block q's combine uses group q / 2, whose constants lanes
-    // 8 (q / 2) .. hold.
+
+    // 5. Operands and group constants per slice.  Lane block q's combine
+    // uses group q / 2 of the slice, whose constants lanes 8 (q / 2) .. hold.
+    typedef typename std::conditional<NF4, v8h, v4i>::type AT;
     const int src_lane = 8 * int(q >> 1);
-    const float my_factor = __shfl(factor, src_lane, 64);
-    const int2 my_corr = int2{__shfl(cv.x, src_lane, 64), __shfl(cv.y, src_lane, 64)};
-    const uint32_t own = j >> 2;
-    v4i as[4];
+    v4u dq[SPW];
+    float my_factor[SPW];
+    int2 my_corr[SPW];
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
-        as[s2] = own == uint32_t(s2) ? af : v4i{0, 0, 0, 0};
-
-    // 4. Products of the slice per (tile, stream), then the combine.
+    for (int sp = 0; sp < SPW; ++sp) {
+        int e;
+        bool bad;
+        packed_group_exponent(v[sp], e, bad);
+        float factor;
+        int2 cv = int2{0, 0};
+        if constexpr (NF4) {
+            factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e);
+            const uint32_t h = lane & 1;
+            unsigned mine[2], recv[2];
 #pragma unroll
-    for (int i = 0; i < R; ++i)
-#pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            v4i acc = v4i{0, 0, 0, 0};
-#pragma unroll
-            for (int ks = 0; ks < 4; ++ks) {
-                const unsigned word = w[st][i][ks];
-                const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
-                                   int(word & 0xC0C0C0C0u)};
-                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[ks], bw, acc, 0, 0, 0);
+            for (int pr = 0; pr < 2; ++pr) {
+                const float v0 = bad ? 0.0f : ldexpf(v[sp][2 * pr], -e);
+                const float v1 = bad ? 0.0f : ldexpf(v[sp][2 * pr + 1], -e);
+                const _Float16 h0 = _Float16(v0), h1 = _Float16(v1);
+                const _Float16 l0 = _Float16(v0 - float(h0)), l1 = _Float16(v1 - float(h1));
+                const unsigned hi_pair = pack_halves(h0, h1), lo_pair = pack_halves(l0, l1);
+                mine[pr] = h ? lo_pair : hi_pair;
+                recv[pr] = quad_xor1(h ? hi_pair : lo_pair);  // the partner's half h
             }
-            // Rows 4q' + r: digit r of kstep q'; the group's two ksteps
-            // are lane blocks q' and q' ^ 1.
-            int d[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const auto pr = __builtin_amdgcn_permlane16_swap(unsigned(acc[r]),
-                                                                 unsigned(acc[r]), false, false);
-                d[r] = int(pr[0]) + int(pr[1]);
-            }
-            const int hi = (d[0] << 8) + d[1] - my_corr.x;
-            const int lo = (d[2] << 8) + d[3] - my_corr.y;
-            const float gsum = float(hi) * 65536.0f + float(lo);
-            float total = gsum * (to_f32<HALF>(sc[st][i]) * my_factor);
-            total = sum_xor32(total);  // the slice's two groups
-            if (q == 0)
-                partial[(((tslot + TS * i) * 2 + st) * P + part) * 16 + j] = total;
+            dq[sp] = h ? v4u{recv[0], recv[1], mine[0], mine[1]}
+                       : v4u{mine[0], mine[1], recv[0], recv[1]};
+        } else {
+            factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
+            dq[sp] = __builtin_bit_cast(v4u, packed_digits<F>(v[sp], e, bad, cv));
         }
-
-    // 5. The slices of each tile and stream, added in order; the epilogue.
-    __syncthreads();
-    if (threadIdx.x < uint32_t(TS * R * 16)) {
-        const uint32_t tl = threadIdx.x / 16, r = threadIdx.x % 16;
-        float sum[2];
+        my_factor[sp] = __shfl(factor, src_lane, 64);
+        my_corr[sp] = int2{__shfl(cv.x, src_lane, 64), __shfl(cv.y, src_lane, 64)};
+    }
+    // Operand of kstep s2 (NF4: two per kstep, the lane's activation pair
+    // repeated for its hi and lo slots): the own fragment, zero otherwise.
+    const uint32_t own = NF4 ? j >> 1 : j >> 2;
+    auto operand = [&](int sp, int s2, int o) {
+        const v4u d = dq[sp];
+        const v4u z{0, 0, 0, 0};
+        const v4u pick = NF4 ? (o == 0 ? v4u{d.x, d.x, d.y, d.y} : v4u{d.z, d.z, d.w, d.w}) : d;
+        return __builtin_bit_cast(AT, own == uint32_t(s2) ? pick : z);
+    };
+    if constexpr (NF4)
+        __syncthreads();  // the table
+    const unsigned copy_byte = 8 * (lane % kStreamLutCopies);
+    const char *cells = reinterpret_cast<const char *>(lut);
+    auto nf4_entries = [&](unsigned word, v4u &b0, v4u &b1) {
+        uint2 ent[4];
 #pragma unroll
-        for (int st = 0; st < 2; ++st) {
-            sum[st] = partial[((tl * 2 + st) * P) * 16 + r];
+        for (int b = 0; b < 4; ++b) {
+            const unsigned at =
+                __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + b) << 8));
+            ent[b] = *reinterpret_cast<const uint2 *>(cells + at);
+        }
+        b0 = v4u{ent[0].x, ent[0].y, ent[1].x, ent[1].y};
+        b1 = v4u{ent[2].x, ent[2].y, ent[3].x, ent[3].y};
+    };
+
+    // 6. Products per (stream, slice), the combine, the wave's slice sum.
+#pragma unroll
+    for (int st = 0; st < S; ++st) {
+        float wave_total = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < SPW; ++sp) {
+            typedef typename std::conditional<NF4, v4f, v4i>::type CT;
+            CT acc = CT{};
+            v4u nb0{}, nb1{};
+            if constexpr (NF4)
+                nf4_entries(w[st][sp][0][0], nb0, nb1);
+#pragma unroll
+            for (int l = 0; l < L; ++l)
+#pragma unroll
+                for (int ks = 0; ks < KPL; ++ks) {
+                    const int s2 = l * KPL + ks;  // kstep within the slice
+                    if constexpr (F == Format::Int8) {
+                        const v4u wv2 = w[st][sp][l];
+                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
+                            operand(sp, s2, 0),
+                            v4i{int(wv2.x), int(wv2.y), int(wv2.z), int(wv2.w)}, acc, 0, 0, 0);
+                    } else if constexpr (F == Format::Ternary) {
+                        const unsigned word = w[st][sp][l][ks];
+                        const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu),
+                                           int(word & 0xF0F0F0F0u), int(word & 0xC0C0C0C0u)};
+                        acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(operand(sp, s2, 0), bw, acc,
+                                                                    0, 0, 0);
+                    } else {
+                        const v4u b0 = nb0, b1 = nb1;
+                        if (ks + 1 < KPL)
+                            nf4_entries(w[st][sp][l][ks + 1], nb0, nb1);
+                        else if (l + 1 < L)
+                            nf4_entries(w[st][sp][l + 1][0], nb0, nb1);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            operand(sp, s2, 0), __builtin_bit_cast(v8h, b0), acc, 0, 0, 0);
+                        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+                            operand(sp, s2, 1), __builtin_bit_cast(v8h, b1), acc, 0, 0, 0);
+                    }
+                }
+            float gsum;
+            if constexpr (NF4) {
+                // Rows 4q' + r: kstep 2q' + r / 2, half r % 2; the group's
+                // other two ksteps are lane block q' ^ 1.
+                gsum = sum_xor16((acc.x + acc.y) + (acc.z + acc.w));
+            } else {
+                // Rows 4q' + r: digit r of kstep q'; the group's two ksteps
+                // are lane blocks q' and q' ^ 1.
+                int d[4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const auto pr = __builtin_amdgcn_permlane16_swap(
+                        unsigned(acc[r]), unsigned(acc[r]), false, false);
+                    d[r] = int(pr[0]) + int(pr[1]);
+                }
+                const int hi = (d[0] << 8) + d[1] - my_corr[sp].x;
+                const int lo = (d[2] << 8) + d[3] - my_corr[sp].y;
+                gsum = float(hi) * 65536.0f + float(lo);
+            }
+            float total = gsum * (to_f32<HALF>(sc[st][sp]) * my_factor[sp]);
+            total = sum_xor32(total);  // the slice's two groups
+            wave_total = sp == 0 ? total : wave_total + total;
+        }
+        if (q == 0)
+            partial[(st * P + part) * 16 + j] = wave_total;
+    }
+
+    // 7. The waves of each stream, added in order; the epilogue.
+    __syncthreads();
+    if (threadIdx.x < 16) {
+        const uint32_t r = threadIdx.x;
+        float sum[S];
+#pragma unroll
+        for (int st = 0; st < S; ++st) {
+            sum[st] = partial[(st * P) * 16 + r];
 #pragma unroll
             for (int pp = 1; pp < P; ++pp)
-                sum[st] += partial[((tl * 2 + st) * P + pp) * 16 + r];
+                sum[st] += partial[(st * P + pp) * 16 + r];
         }
-        const uint32_t tt = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
-        const uint32_t row = tt * 16 + r;
-        if (tt < a.n_tiles && row < a.n) {
-            if constexpr (E == Epilogue::Pair) {
+        const uint32_t row = blockIdx.x * 16 + r;
+        if constexpr (S == 3) {
+            // Channel `row`: B, C and x of the in-projection, then the
+            // one-token convolution (conv_step_kernel's arithmetic).
+            const ConvStep &cv = a.conv;
+            if (row < cv.hidden) {
+                const uint32_t rows = cv.width - 1;
+                const float u = sum[0] * sum[2];
+                const float *taps = cv.kernel + uint64_t(row) * cv.width;
+                float total = 0.0f;
+                for (uint32_t tap = 0; tap < rows; ++tap)
+                    total += taps[tap] * cv.history[uint64_t(tap) * cv.hidden + row];
+                total += taps[rows] * u;
+                for (uint32_t rr = 0; rr + 1 < rows; ++rr)
+                    cv.next[uint64_t(rr) * cv.hidden + row] =
+                        cv.history[uint64_t(rr + 1) * cv.hidden + row];
+                if (rows)
+                    cv.next[uint64_t(rows - 1) * cv.hidden + row] = u;
+                cv.out[row] = total * sum[1];
+            }
+        } else if (row < a.n) {
+            if constexpr (E == Epilogue::Single) {
+                a.out[0][row] = sum[0];
+            } else if constexpr (E == Epilogue::Pair) {
                 a.out[0][row] = sum[0];
                 a.out[1][row] = sum[1];
             } else {
@@ -3317,76 +3456,205 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     return true;
 }
 
-// One tile slot per block (P waves), one tile per wave.  Measured in the
-// LFM2 greedy decode (tok/s, fused step / op by op): 1.2B shape (8192 x
-// 2048 pairs) 2052 / 1443 with TS = 1, 2029 / 1467 with TS = 2, 2050 /
-// 1443 with TS = 4, against 1743 / 1315 on the register-prologue plans;
-// 350M shape (4608 x 1024) 3094 / 1986, 3085 / 1757, 2960 / 1763, against
-// 2741 / 1875.
-template <bool HALF, int P, bool NORM, Epilogue E>
-void launch_wide_pair(hipStream_t stream, const WidePairArgs &args)
+template <Format F, bool HALF, int P, int SPW, int S, XKind PRO, Epilogue E>
+void launch_wide_one(hipStream_t stream, const WideArgs &args, uint32_t blocks)
 {
-    constexpr int TS = 1, R = 1;
-    const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
-    wide_pair_kernel<HALF, P, TS, R, NORM, E><<<blocks, 64 * TS * P, 0, stream>>>(args);
+    wide_one_kernel<F, HALF, P, SPW, S, PRO, E><<<blocks, 64 * P, 0, stream>>>(args);
 }
 
-// Serves a ternary two-stream product at one row (plain activations or the
-// add + RMS norm, Pair or SwiGLU epilogue) with wide_pair_kernel; false
-// leaves it to the other plans.
-bool try_wide_pair(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
+// Kernel shape of a one-row wide product: (P waves, SPW slices) for K, or
+// false.
+bool wide_one_shape(uint32_t k, int &p, int &spw)
+{
+    switch (k) {
+    case 1024: p = 4; spw = 1; return true;
+    case 2048: p = 8; spw = 1; return true;
+    case 4608: p = 9; spw = 2; return true;
+    case 8192: p = 16; spw = 2; return true;
+    default: return false;
+    }
+}
+
+// Dispatch over (HALF, K shape) for one (S, PRO, E) combination.
+template <Format F, int S, XKind PRO, Epilogue E>
+void wide_one_go(hipStream_t stream, const WideArgs &args, uint32_t blocks, bool half, int p)
+{
+    auto go = [&](auto half_tag) {
+        constexpr bool H = decltype(half_tag)::value;
+        if constexpr (S == 1 && E == Epilogue::Single && PRO != XKind::AddRms) {
+            // Plain and SwiGLU singles: the long contractions (down
+            // projections); K = 1024 and 2048 plain rows take wide_row_kernel.
+            if constexpr (PRO == XKind::Swiglu) {
+                if (p == 9)
+                    return launch_wide_one<F, H, 9, 2, S, PRO, E>(stream, args, blocks);
+            }
+            if (p == 16)
+                return launch_wide_one<F, H, 16, 2, S, PRO, E>(stream, args, blocks);
+        }
+        if constexpr (PRO != XKind::Swiglu || S == 1) {
+            if (p == 4)
+                return launch_wide_one<F, H, 4, 1, S, PRO, E>(stream, args, blocks);
+            if (p == 8)
+                return launch_wide_one<F, H, 8, 1, S, PRO, E>(stream, args, blocks);
+        }
+    };
+    if (half)
+        go(std::true_type{});
+    else
+        go(std::false_type{});
+}
+
+// Whether the one-row wide kernel serves this call (ternary and NF4, m = 1,
+// K one of wide_one_shape's, 16-byte aligned operands).
+bool wide_one_ok(const PackedCall &call, int &p, int &spw)
 {
     const XForm &t = call.xform;
     auto aligned = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
-    const bool norm = t.kind == XKind::AddRms;
-    if (call.format != Format::Ternary || call.separate_prologue || call.segments ||
-        call.epilogue == Epilogue::Single || call.m != 1 || (call.k != 1024 && call.k != 2048) ||
-        (t.kind != XKind::Plain && !norm) || !call.b.tiles)
+    if (call.format == Format::Int8 || call.separate_prologue || call.segments || call.m != 1 ||
+        !wide_one_shape(call.k, p, spw) || !call.a.tiles)
         return false;
-    const float *x = norm ? t.a : call.x;
-    if (!x || !aligned(x) ||
-        (norm && (!t.w || !aligned(t.w) || (t.b && !aligned(t.b)) || (t.side && !aligned(t.side)))))
+    const bool single = call.epilogue == Epilogue::Single;
+    if (!single && (!call.b.tiles || call.a.tiled_half != call.b.tiled_half))
         return false;
-    if (call.a.tiled_half != call.b.tiled_half)
+    // Two slices per wave serve the long single contractions: SwiGLU rows,
+    // and plain rows at K = 8192 (at K = 4608, 64 blocks of nine waves for
+    // the 350M-shape down projection measured slower than the f32 vector
+    // GEMV: decode 3194 against 3102 tok/s).
+    if (spw == 2 && !(single && (t.kind == XKind::Swiglu ||
+                                 (t.kind == XKind::Plain && call.k == 8192))))
         return false;
-    WidePairArgs args{};
-    args.xform = t;
-    args.xform.a = x;
-    args.tiles[0] = call.a.tiles;
-    args.tiles[1] = call.b.tiles;
-    args.scales[0] = call.a.tiled_scales;
-    args.scales[1] = call.b.tiled_scales;
-    args.out[0] = call.out_a;
-    args.out[1] = call.out_b;
-    args.n = call.n;
-    args.k = call.k;
-    args.n_tiles = n_tiles;
-    auto go = [&](auto half_tag, auto p_tag, auto norm_tag) {
-        constexpr bool H = decltype(half_tag)::value, N = decltype(norm_tag)::value;
-        constexpr int P = decltype(p_tag)::value;
-        if (call.epilogue == Epilogue::Pair)
-            launch_wide_pair<H, P, N, Epilogue::Pair>(stream, args);
-        else
-            launch_wide_pair<H, P, N, Epilogue::SwigluPair>(stream, args);
-    };
-    auto by_norm = [&](auto half_tag, auto p_tag) {
-        if (norm)
-            go(half_tag, p_tag, std::true_type{});
-        else
-            go(half_tag, p_tag, std::false_type{});
-    };
-    auto by_k = [&](auto half_tag) {
-        if (call.k == 2048)
-            by_norm(half_tag, std::integral_constant<int, 8>{});
-        else
-            by_norm(half_tag, std::integral_constant<int, 4>{});
-    };
-    if (call.a.tiled_half)
-        by_k(std::true_type{});
-    else
-        by_k(std::false_type{});
+    // Plain single rows at K = 1024 and 2048 are wide_row_kernel's (and the
+    // ternary head's streaming rows kernel's).
+    if (single && t.kind == XKind::Plain && spw == 1)
+        return false;
+    if (t.kind == XKind::Swiglu && !single)
+        return false;
+    const float *x = t.kind == XKind::Plain ? call.x : t.a;
+    if (!x || !aligned(x))
+        return false;
+    if (t.kind == XKind::Swiglu && (!t.b || !aligned(t.b)))
+        return false;
+    if (t.kind == XKind::AddRms &&
+        (!t.w || !aligned(t.w) || (t.b && !aligned(t.b)) || (t.side && !aligned(t.side))))
+        return false;
     return true;
 }
+
+// Serves a one-row product (single, pair or SwiGLU pair; plain, add + RMS
+// norm or SwiGLU activations) with wide_one_kernel; false leaves it to the
+// other plans.  Measured in the LFM2 greedy decode (tok/s, fused step / op
+// by op; 1.2B shape, then 350M) against the plans each use replaces: all of
+// them 2302 / 1710, 3102 / 2030; the pairs on the register-prologue
+// plans 2008 / 1571, 2730 / 2008; SwiGLU rows as a prologue kernel plus
+// the K-split GEMV (op by op) 1620, 1814; the K = 8192 down projection on
+// the f32 vector GEMV 2245 / 1710; the norm-fed singles (grouped q/k/v) on
+// the vector GEMV's norm variant 2300 / 1711, 3104 / 2056 (the same).
+template <Format F>
+bool try_wide_one(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
+{
+    int p, spw;
+    if constexpr (F == Format::Int8) {
+        return false;
+    } else {
+        if (!wide_one_ok(call, p, spw))
+            return false;
+        const XKind kind = call.xform.kind;
+        WideArgs args{};
+        args.xform = call.xform;
+        if (kind == XKind::Plain)
+            args.xform.a = call.x;
+        args.tiles[0] = call.a.tiles;
+        args.tiles[1] = call.b.tiles;
+        args.scales[0] = call.a.tiled_scales;
+        args.scales[1] = call.b.tiled_scales;
+        args.out[0] = call.out_a;
+        args.out[1] = call.out_b;
+        args.n = call.n;
+        args.k = call.k;
+        const bool half = call.a.tiled_half;
+        switch (call.epilogue) {
+        case Epilogue::Single:
+            if (kind == XKind::AddRms)
+                wide_one_go<F, 1, XKind::AddRms, Epilogue::Single>(stream, args, n_tiles, half, p);
+            else if (kind == XKind::Swiglu)
+                wide_one_go<F, 1, XKind::Swiglu, Epilogue::Single>(stream, args, n_tiles, half, p);
+            else
+                wide_one_go<F, 1, XKind::Plain, Epilogue::Single>(stream, args, n_tiles, half, p);
+            break;
+        case Epilogue::Pair:
+            if (kind == XKind::AddRms)
+                wide_one_go<F, 2, XKind::AddRms, Epilogue::Pair>(stream, args, n_tiles, half, p);
+            else
+                wide_one_go<F, 2, XKind::Plain, Epilogue::Pair>(stream, args, n_tiles, half, p);
+            break;
+        case Epilogue::SwigluPair:
+            if (kind == XKind::AddRms)
+                wide_one_go<F, 2, XKind::AddRms, Epilogue::SwigluPair>(stream, args, n_tiles, half,
+                                                                        p);
+            else
+                wide_one_go<F, 2, XKind::Plain, Epilogue::SwigluPair>(stream, args, n_tiles, half,
+                                                                       p);
+            break;
+        }
+        return true;
+    }
+}
+
+}  // namespace
+
+// The convolution in-projection at one row (three row regions of one
+// matrix: B, C, x) with the add + RMS norm, finished by the one-token
+// convolution in the epilogue; ternary and NF4, hidden a multiple of 16.
+// LFM2 greedy decode against the vector GEMV's convolution variant: 1.2B
+// shape 2253 -> 2302 tok/s, 350M 2974 -> 3102.
+bool wide_conv_supported(const PackedCall &call, const ConvStep &conv)
+{
+    int p, spw;
+    const XForm &t = call.xform;
+    auto aligned = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    return call.format != Format::Int8 && call.m == 1 && t.kind == XKind::AddRms &&
+           wide_one_shape(call.k, p, spw) && spw == 1 && conv.hidden % 16 == 0 &&
+           call.n == 3 * conv.hidden && conv.width >= 1 && t.a && aligned(t.a) && t.w &&
+           aligned(t.w) && (!t.b || aligned(t.b)) && (!t.side || aligned(t.side));
+}
+
+bool try_wide_conv(hipStream_t stream, const PackedCall &call, const ConvStep &conv)
+{
+    if (!wide_conv_supported(call, conv) || !call.a.tiles)
+        return false;
+    int p, spw;
+    wide_one_shape(call.k, p, spw);
+    WideArgs args{};
+    args.xform = call.xform;
+    args.tiles[0] = call.a.tiles;
+    args.scales[0] = call.a.tiled_scales;
+    args.n = call.n;
+    args.k = call.k;
+    args.stream_tiles = conv.hidden / 16;
+    args.conv = conv;
+    const uint32_t blocks = conv.hidden / 16;
+    auto go = [&](auto f_tag, auto half_tag) {
+        constexpr Format F = decltype(f_tag)::value;
+        constexpr bool H = decltype(half_tag)::value;
+        if (p == 4)
+            launch_wide_one<F, H, 4, 1, 3, XKind::AddRms, Epilogue::Single>(stream, args, blocks);
+        else
+            launch_wide_one<F, H, 8, 1, 3, XKind::AddRms, Epilogue::Single>(stream, args, blocks);
+    };
+    auto by_half = [&](auto f_tag) {
+        if (call.a.tiled_half)
+            go(f_tag, std::true_type{});
+        else
+            go(f_tag, std::false_type{});
+    };
+    if (call.format == Format::Ternary)
+        by_half(std::integral_constant<Format, Format::Ternary>{});
+    else
+        by_half(std::integral_constant<Format, Format::Nf4>{});
+    return true;
+}
+
+namespace {
 
 template <Format F>
 void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
@@ -3396,11 +3664,11 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t n_tiles = call_tiles(call);
     if (try_wide_row<F>(stream, call, n_tiles))
         return;
+    if (try_wide_one<F>(stream, call, n_tiles))
+        return;
     if (try_vgemv(stream, call))
         return;
     if constexpr (F == Format::Ternary) {
-        if (try_wide_pair(stream, call, n_tiles))
-            return;
         if (try_stream_ternary(stream, call, n_tiles))
             return;
     }
@@ -3595,6 +3863,8 @@ void gemv_nf4(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
     if (try_wide_row<Format::Nf4>(stream, call, n_tiles))
+        return;
+    if (try_wide_one<Format::Nf4>(stream, call, n_tiles))
         return;
     if (try_vgemv(stream, call))
         return;

@@ -238,7 +238,7 @@ mfh_status packed_xform_conv(mfh_ctx *ctx, const XForm &xform, uint32_t k,
         return fail(ctx, MFH_INVALID_SHAPE, "packed linear input width differs from weight width");
     if (xform.kind != XKind::AddRms || !xform.a || !xform.w || !conv.kernel || !conv.history ||
         !conv.next || !conv.out || conv.width < 1 || ctx->kernel_path != 0)
-        return fail(ctx, MFH_UNSUPPORTED, "fused convolution needs the vector GEMV");
+        return fail(ctx, MFH_UNSUPPORTED, "fused convolution needs the one-row decode kernels");
     PackedCall call;
     call.format = p.format;
     call.epilogue = Epilogue::Single;
@@ -248,8 +248,13 @@ mfh_status packed_xform_conv(mfh_ctx *ctx, const XForm &xform, uint32_t k,
     call.a = stream_of(codes, scales);
     call.xform = xform;
     DeviceGuard guard(ctx->device);
-    if (!try_vgemv_conv(ctx->stream, call, conv))
-        return fail(ctx, MFH_UNSUPPORTED, "fused convolution needs the vector GEMV");
+    if (wide_conv_supported(call, conv)) {
+        if ((s = prepare_tiles(ctx, codes, scales, p, &call.a)))
+            return s;
+        try_wide_conv(ctx->stream, call, conv);
+    } else if (!try_vgemv_conv(ctx->stream, call, conv)) {
+        return fail(ctx, MFH_UNSUPPORTED, "fused convolution needs the one-row decode kernels");
+    }
     if (hipGetLastError() != hipSuccess)
         return fail(ctx, MFH_BACKEND_FAILURE, "packed kernel launch failed");
     return MFH_OK;

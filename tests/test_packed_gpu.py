@@ -407,6 +407,8 @@ def test_wide_k_non_finite_row(backend, path, scheme):
     x[1, 4000] = np.nan
     got = run_linear(backend, x, codes, scales)
     assert not np.isfinite(got[1]).any()
+    # The bad row alone (the one-row kernels).
+    assert not np.isfinite(run_linear(backend, x[1:], codes, scales)).any()
 
 
 @pytest.mark.parametrize("scheme", SCHEMES)
