@@ -2492,8 +2492,8 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
     }
 }
 
-// Wide-matrix GEMV at two to eight activation rows, written for both
-// integer formats and launched for INT8 (launch_wide_rows): the plan of
+// Wide-matrix GEMV at two to eight activation rows, integer formats
+// (launch_wide_rows: INT8, and ternary below the head size): the plan of
 // wide_row_kernel (one wave per 256-k slice across R tiles, the
 // slices' sums added in slice order through LDS) with the register
 // prologue's fragment layout.  Lane 16q + 4b + p loads x[4f + b] at
@@ -2504,13 +2504,12 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 // scales and slice order are wide_row_kernel's, so each row's result is the
 // one-row kernel's bit for bit.  Rows at or beyond m read row 0 and are
 // zeroed.
-template <Format F, bool HALF, int P, int R, int NF>
-__global__ __launch_bounds__(1024) void wide_rows_kernel(StreamArgs a)
+template <Format F, bool HALF, int P, int R, int NF, int W = 16>
+__global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
 {
     static_assert(F != Format::Nf4, "integer formats");
     using ST = typename ScaleT<HALF>::type;
     using Blk = I8Block<F, 1, 1, NF, HALF>;
-    constexpr int W = 16;
     constexpr int TS = W / P;                       // tiles per round
     constexpr int L = WideGeo<F>::loads;
     constexpr int KPL = WideGeo<F>::ksteps_per_load;
@@ -3379,11 +3378,11 @@ void launch_wide_row(hipStream_t stream, const StreamArgs &args)
     wide_row_kernel<F, HALF, P, R><<<blocks, 1024, 0, stream>>>(args);
 }
 
-// Tiles per wave of wide_rows_kernel: R = P, so each block's 16 waves cover
-// 16 tiles.  Measured at 65536 rows, INT8, B = 2 / 4 / 8 (us per launch, 1
-// GiB rotation): K = 2048 R = 8 22.1 / 22.0 / 22.9, R = 4 22.6 / 23.0 /
-// 25.3, R = 2 24.1 / 24.7 / 30.3 (the K-split plans 28.4 / 25.6 / 28.7);
-// K = 1024 R = 4 12.3 / 12.5 / 13.3, R = 8 15.1 / 15.2 / 16.1.  Ternary
+// At the head size, tiles per wave R = P, so each block's 16 waves cover 16
+// tiles.  Measured at 65536 rows, INT8, B = 2 / 4 / 8 (us per launch, 1 GiB
+// rotation): K = 2048 R = 8 22.1 / 22.0 / 22.9, R = 4 22.6 / 23.0 / 25.3,
+// R = 2 24.1 / 24.7 / 30.3 (the K-split plans 28.4 / 25.6 / 28.7); K = 1024
+// R = 4 12.3 / 12.5 / 13.3, R = 8 15.1 / 15.2 / 16.1.  The ternary head
 // stays on the streaming kernels: its digit prologue (the field
 // telescoping), repeated by every wave of a slice, cost more than it saved
 // (65536 x 2048, B = 2 / 4 / 8: R = 8 8.9 / 9.3 / 14.2 us against 8.1 / 8.9
@@ -3391,24 +3390,36 @@ void launch_wide_row(hipStream_t stream, const StreamArgs &args)
 template <Format F, bool HALF, int P, int NF>
 void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
 {
+    // Below the head size one block of P waves per tile, as wide_row_kernel.
+    // Measured at B = 2 / 4 / 8 (us per launch) against the K-split
+    // register-prologue plans: ternary 2048 x 2048 4.15 / 4.18 / 6.13 ->
+    // 3.82 / 3.83 / 5.34, 8192 x 2048 5.79 / 5.76 / 9.00 -> 5.33 / 5.38 /
+    // 8.31, 4608 x 1024 4.24 / 4.25 / 6.12 -> 3.78 / 3.75 / 5.39; INT8
+    // 2048 x 2048 3.74 / 3.87 / 5.82 -> 3.69 / 3.71 / 4.86, 8192 x 2048 6.07
+    // / 6.22 / 8.16 -> 5.05 / 5.14 / 7.12 (1024 x 1024: 3.25 / 3.22 / 3.94 ->
+    // 3.51 / 3.46 / 3.70).
+    if (args.n_tiles < kHeadTiles) {
+        wide_rows_kernel<F, HALF, P, 1, NF, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
+        return;
+    }
     constexpr int R = P;
     constexpr int TS = 16 / P;
     const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
     wide_rows_kernel<F, HALF, P, R, NF><<<blocks, 1024, 0, stream>>>(args);
 }
 
-// Serves a one-row product at K = 1024 or 2048 with wide_row_kernel, and
-// a wide matrix (the LM heads at decode) at two to eight rows with
-// wide_rows_kernel (INT8); false leaves it to the other plans.  The
-// ternary head at K = 2048 keeps the streaming rows kernel.
+// Serves products at K = 1024 or 2048: one row with wide_row_kernel, two
+// to eight rows with wide_rows_kernel (INT8, and ternary below the head
+// size); false leaves it to the other plans.  The ternary head keeps the
+// streaming kernels at K = 2048 and from two rows.
 template <Format F>
 bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 {
-    const uint32_t max_m = F == Format::Int8 ? 8 : 1;
     const bool head = n_tiles >= kHeadTiles;
+    const uint32_t max_m = F == Format::Int8 || (F == Format::Ternary && !head) ? 8 : 1;
     if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
-        (call.m > 1 && !head) || (call.k != 1024 && call.k != 2048) ||
+        (call.k != 1024 && call.k != 2048) ||
         (F == Format::Ternary && head && call.k != 1024) ||
         reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
         return false;
@@ -3422,7 +3433,7 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     args.k = call.k;
     args.n_tiles = n_tiles;
     const bool half = call.a.tiled_half;
-    if constexpr (F == Format::Int8) {
+    if constexpr (F != Format::Nf4) {
         if (call.m > 1) {
             auto rows = [&](auto p_tag, auto nf_tag) {
                 constexpr int P = decltype(p_tag)::value, NF = decltype(nf_tag)::value;
