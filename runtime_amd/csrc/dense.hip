@@ -164,27 +164,6 @@ __global__ __launch_bounds__(kBlock) void gather_columns_kernel(float *__restric
 constexpr int kArgmaxBlock = 1024;
 constexpr uint32_t kArgmaxRange = 2048;
 
-struct Candidate {
-    float value;
-    uint32_t index;  // UINT32_MAX: no admitted value
-    int poisoned;
-};
-
-// Whether candidate (ov, oi) replaces (best, index).
-__device__ __forceinline__ bool takes(float ov, uint32_t oi, float best, uint32_t index)
-{
-    return oi != UINT32_MAX && (index == UINT32_MAX || ov > best || (ov == best && oi < index));
-}
-
-__device__ __forceinline__ void merge(Candidate &c, float ov, uint32_t oi, int op)
-{
-    c.poisoned |= op;
-    if (takes(ov, oi, c.value, c.index)) {
-        c.value = ov;
-        c.index = oi;
-    }
-}
-
 // Block-wide reduction; the result is valid in thread 0.
 __device__ Candidate reduce_candidates(Candidate c)
 {
@@ -1487,6 +1466,17 @@ void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t row
     }
     argmax_kernel<<<grid_for(rows, 1), kArgmaxBlock, 0, stream>>>(out, copy, in, rows, width,
                                                                   mask);
+}
+
+void launch_argmax_candidates(hipStream_t stream, float *out, float *copy,
+                              const Candidate *candidates, uint32_t count)
+{
+    // One wave up to 64 candidates (512, the 1.2B-shape head's, measured the
+    // same with either kernel).
+    if (count <= 64)
+        argmax_final_wave_kernel<<<1, 64, 0, stream>>>(out, copy, candidates, count);
+    else
+        argmax_final_kernel<<<1, kArgmaxBlock, 0, stream>>>(out, copy, candidates, count);
 }
 
 void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,

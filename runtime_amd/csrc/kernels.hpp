@@ -43,6 +43,31 @@ struct XForm {
 
 constexpr uint32_t kMaxSegments = 3;
 
+// Greedy selection's (value, index) candidate: index UINT32_MAX admits no
+// value; `poisoned` marks a non-finite value seen.  Candidates merge keeping
+// the largest value, the lowest index among equal values and any poison,
+// so the order of the merges does not change the result.
+struct Candidate {
+    float value;
+    uint32_t index;
+    int poisoned;
+};
+
+// Whether candidate (ov, oi) replaces (best, index).
+__device__ __forceinline__ bool takes(float ov, uint32_t oi, float best, uint32_t index)
+{
+    return oi != UINT32_MAX && (index == UINT32_MAX || ov > best || (ov == best && oi < index));
+}
+
+__device__ __forceinline__ void merge(Candidate &c, float ov, uint32_t oi, int op)
+{
+    c.poisoned |= op;
+    if (takes(ov, oi, c.value, c.index)) {
+        c.value = ov;
+        c.index = oi;
+    }
+}
+
 struct PackedCall {
     Format format = Format::Ternary;
     Epilogue epilogue = Epilogue::Single;
@@ -68,6 +93,12 @@ struct PackedCall {
     PackedStream seg[kMaxSegments];
     float *seg_out[kMaxSegments] = {};
     uint32_t seg_n[kMaxSegments] = {};
+    // One-row products: where the launch's plan can (the one-row wide
+    // kernel), each block also writes the greedy-selection candidate of its
+    // outputs to argmax[block] and the launch stores the block count in
+    // *argmax_count (left unchanged otherwise; the caller zeroes it).
+    Candidate *argmax = nullptr;
+    uint32_t *argmax_count = nullptr;
 };
 
 // One token of the gated short convolution (conv_step_kernel's arithmetic),
@@ -94,11 +125,17 @@ bool prepared_stream(const mfh_buf *codes, const mfh_buf *scales, Format format,
 // A matrix-core GEMV (m <= 2) whose activation prologue
 // applies `xform`, over admitted weights of n rows and width k (the LFM2
 // decode step).  Fails with MFH_UNSUPPORTED where that kernel does not serve
-// the call, before anything is enqueued.
+// the call, before anything is enqueued.  `argmax` / `argmax_count`: see
+// PackedCall.
 mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uint32_t m,
                         uint32_t n, uint32_t k, const mfh_buf *codes_a, const mfh_buf *scales_a,
                         const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
-                        float *out_b);
+                        float *out_b, Candidate *argmax = nullptr,
+                        uint32_t *argmax_count = nullptr);
+// Whether a one-row product of n x k weights in format f at the head size
+// takes the add + RMS norm and the argmax candidates in its one launch
+// (the one-row wide kernel).
+bool head_fold_supported(Format f, uint32_t n, uint32_t k);
 
 // The decode step's convolution block input: the in-projection of `codes`
 // (3 * conv.hidden rows of width k) over add + RMS norm activations with
@@ -206,6 +243,10 @@ size_t argmax_scratch_bytes(uint32_t rows, uint32_t width);
 // `copy`, when non-null, receives the selectors too.
 void launch_argmax(hipStream_t stream, float *out, const float *in, uint32_t rows, uint32_t width,
                    const uint64_t *mask, void *scratch, float *copy = nullptr);
+// The selector of one row from `count` candidates a product's blocks wrote
+// (PackedCall::argmax): the same result as launch_argmax over that row.
+void launch_argmax_candidates(hipStream_t stream, float *out, float *copy,
+                              const Candidate *candidates, uint32_t count);
 // op 0: left + right, op 1: left * right.
 void launch_binary(hipStream_t stream, int op, float *out, const float *left, const float *right,
                    size_t count);

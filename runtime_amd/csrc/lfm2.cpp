@@ -90,6 +90,12 @@ struct mfl_model {
     uint64_t length = 0;
     std::map<uint64_t, std::unique_ptr<Workspace>> workspaces;
     Owned logits, sampled;
+    // Greedy-selection candidates the fused step's LM head wrote beside the
+    // logits (one per head block, Candidate layout), valid while
+    // candidate_count != 0 and the prefix is still candidate_length long.
+    Owned candidates;
+    uint32_t candidate_count = 0;
+    uint64_t candidate_length = 0;
     Owned rotation;  // [max_tokens, head_dim] rotation coefficients by position
     // Weights uploaded by mfl_load_safetensors (the model owns them).
     std::vector<std::unique_ptr<Owned>> loaded;
@@ -165,6 +171,13 @@ mfh_status weight_linear(mfh_ctx *c, mfh_buf *out, const mfh_buf *in, const Weig
 // The pair/fused conditions compare the stored quantization of two roles
 // (role_quant, weights.rs:588): packed streams of one shape share a format
 // exactly when their code widths agree.
+// The format of a packed weight of inner width k, from its code width.
+Format packed_format_of(const Weight &w, uint32_t k)
+{
+    const uint64_t cols = w.tensor->dims[1];
+    return cols == k ? Format::Int8 : 2 * cols == k ? Format::Nf4 : Format::Ternary;
+}
+
 bool same_packed_format(const Weight &a, const Weight &b)
 {
     return a.packed() && b.packed() && a.tensor->dims[1] == b.tensor->dims[1] &&
@@ -248,13 +261,14 @@ bool fused_decode_ready(const mfl_model *m)
     return true;
 }
 
-// One decode token with the elementwise steps folded into the products'
-// activation prologues (see XForm) where that measured faster: per
-// convolution block the in projection (residual add + operator norm) and the
-// gate/up pair (residual add + FFN norm, with SwiGLU in its epilogue); the
-// one-token convolution and the final norm are kernels of their own ahead of
-// plain products.  Attention blocks run q/k/v as one launch (v lands in its
-// cache row) and qk_norm_rope + the key append + attention as two.  Same
+// One decode token with the elementwise steps folded into the products
+// (see XForm) where that measured faster: per convolution block the in
+// projection forms the residual add + operator norm and finishes the
+// one-token convolution in its epilogue, and the gate/up pair forms the
+// residual add + FFN norm with SwiGLU in its epilogue; the LM head forms the
+// final add + norm and writes the greedy-selection candidates of its blocks
+// beside the logits.  Attention blocks run q/k/v as one launch (v lands in
+// its cache row) and qk_norm_rope + the key append + attention as two.  Same
 // operations and order as append() on one row; only the f32 reduction trees
 // of the norms and the softmax differ.
 mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_logits)
@@ -420,7 +434,24 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
         left = residual;
         right = down;
     }
-    if (produce_logits) {
+    if (produce_logits && head_fold_supported(packed_format_of(m->embedding, h), cfg.vocab, h)) {
+        // The final add + norm formed in the LM head's slices, and each head
+        // block's greedy-selection candidate beside the logits (one launch
+        // for what was a row-norm kernel, the head and argmax's range pass).
+        XForm head;
+        head.kind = XKind::AddRms;
+        head.a = left;
+        head.b = right;
+        head.w = dev(m->embedding_norm);
+        head.epsilon = cfg.norm_epsilon;
+        uint32_t count = 0;
+        if ((s = packed_xform(c, Epilogue::Single, head, 1, cfg.vocab, h, m->embedding.tensor,
+                              m->embedding.scales, nullptr, nullptr, dev(m->logits), nullptr,
+                              reinterpret_cast<Candidate *>(dev(m->candidates)), &count)))
+            return s;
+        m->candidate_count = count;
+        m->candidate_length = m->length + 1;
+    } else if (produce_logits) {
         // The final add + norm as a row kernel of its own (the sum goes to a
         // scratch row), then a plain product.
         launch_row_rms(c->stream, dev(ws->u[0]), right ? dev(ws->u[1]) : nullptr, left, right,
@@ -443,6 +474,7 @@ mfh_status append(mfl_model *m, const uint32_t *tokens, size_t count, const mfh_
 {
     mfh_ctx *c = m->ctx;
     const mfl_config &cfg = m->config;
+    m->candidate_count = 0;
     uint64_t rows = count;
     if (device_ids) {
         mfh_status s = check_f32(c, device_ids);
@@ -625,6 +657,12 @@ mfh_status mfl_create(mfh_ctx *ctx, const mfl_config *config, mfl_model **out)
     }
     if (!s)
         s = alloc(ctx, m->logits, 1, c.vocab, MFH_CLASS_CACHE, true);
+    if (!s) {
+        // At most one candidate per 16 logits (sizeof(Candidate) = 3 floats).
+        static_assert(sizeof(Candidate) == 3 * sizeof(float), "Candidate layout");
+        s = alloc(ctx, m->candidates, (uint64_t(c.vocab) + 63) / 64 * 4, 3, MFH_CLASS_SCRATCH,
+                  false);
+    }
     if (!s && (s = alloc(ctx, m->rotation, c.max_tokens, c.head_dim, MFH_CLASS_CACHE, false)) ==
                   MFH_OK) {
         DeviceGuard guard(ctx->device);
@@ -745,17 +783,26 @@ mfh_status mfl_generate(mfl_model *m, uint32_t steps, mfh_buf *ids_out)
     const uint32_t vocab = m->config.vocab;
     for (uint32_t i = 0; i < steps; ++i) {
         {
-            // mfl_sample, with the selector also written to ids_out[i].
+            // mfl_sample, with the selector also written to ids_out[i]: from
+            // the LM head's candidates where the fused step left them for
+            // these logits, else over the logits.
             DeviceGuard guard(c->device);
-            void *partials = nullptr;
-            if (const size_t bytes = argmax_scratch_bytes(1, vocab)) {
-                partials = work_scratch(c, bytes);
-                if (!partials)
-                    return allocation_failed(c);
+            float *ids = static_cast<float *>(ids_out->dev) + i;
+            if (m->candidate_count && m->candidate_length == m->length) {
+                launch_argmax_candidates(c->stream, static_cast<float *>(m->sampled.buf->dev), ids,
+                                         reinterpret_cast<const Candidate *>(dev(m->candidates)),
+                                         m->candidate_count);
+            } else {
+                void *partials = nullptr;
+                if (const size_t bytes = argmax_scratch_bytes(1, vocab)) {
+                    partials = work_scratch(c, bytes);
+                    if (!partials)
+                        return allocation_failed(c);
+                }
+                launch_argmax(c->stream, static_cast<float *>(m->sampled.buf->dev),
+                              static_cast<const float *>(m->logits.buf->dev), 1, vocab, nullptr,
+                              partials, ids);
             }
-            launch_argmax(c->stream, static_cast<float *>(m->sampled.buf->dev),
-                          static_cast<const float *>(m->logits.buf->dev), 1, vocab, nullptr,
-                          partials, static_cast<float *>(ids_out->dev) + i);
         }
         if ((s = append(m, nullptr, 0, m->sampled.buf, true)))
             return s;
@@ -869,6 +916,7 @@ mfh_status mfl_restore(mfl_model *m, const mfl_prefix *p)
     copy_rows(c, m->logits.buf, p->logits.buf, m->config.vocab);
     copy_rows(c, m->sampled.buf, p->sampled.buf, 1);
     m->length = p->length;
+    m->candidate_count = 0;
     if (hipGetLastError() != hipSuccess)
         return fail(c, MFH_BACKEND_FAILURE, "prefix copy launch failed");
     return MFH_OK;

@@ -1235,6 +1235,12 @@ struct StreamArgs {
     const void *scales;
     float *out;
     uint32_t m, n, k, n_tiles;
+    // wide_row_kernel only.  NORM: x is the add + RMS norm of x + b (b may
+    // be null) with weight w.  argmax (may be null): one greedy-selection
+    // candidate per block.
+    const float *b = nullptr, *w = nullptr;
+    float epsilon = 0.0f;
+    Candidate *argmax = nullptr;
 };
 
 // One (batch slot, group) record of the prologue: the correction pair and
@@ -2190,6 +2196,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
 // groups differs.
 // ---------------------------------------------------------------------------
 constexpr int kWideAhead = 3;  // 16-byte lane loads in flight per wave
+// The same in the norm variant, whose block barrier holds back the loads
+// issued after it: 1.2B-shape decode 2298 tok/s with 3, 2307 with 6, 2285
+// with all (16).
+constexpr int kWideAheadNorm = 6;
 
 // The packed one-row operand layout (wide_row_kernel, wide_pair_kernel):
 // lane 16q + 4s + p holds x[64 s + 16 q + 4 p + t], t = 0..3, of a 256-k
@@ -2271,7 +2281,7 @@ struct WideGeo {
     static constexpr int ksteps = loads * ksteps_per_load;  // 4, 8, 4
 };
 
-template <Format F, bool HALF, int P, int R, int W = 16>
+template <Format F, bool HALF, int P, int R, int W = 16, bool NORM = false, bool ARGMAX = false>
 __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 {
     using ST = typename ScaleT<HALF>::type;
@@ -2280,7 +2290,8 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
     constexpr int KPL = WideGeo<F>::ksteps_per_load;
     constexpr int KSU = WideGeo<F>::ksteps;
     constexpr int NL = R * L;                       // lane loads per wave
-    constexpr int AH = NL < kWideAhead ? NL : kWideAhead;
+    constexpr int AHW = NORM ? kWideAheadNorm : kWideAhead;
+    constexpr int AH = NL < AHW ? NL : AHW;
     constexpr int G = 2 * P;                        // 128-groups per tile
     constexpr bool NF4 = F == Format::Nf4;
     __shared__ float partial[TS * R * P * 16];
@@ -2300,6 +2311,12 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
                             : 256 * part + 64 * ((lane >> 2) & 3) + 16 * q + 4 * (lane & 3);
     const bool inb = kx < a.k;
     const v4f xv = *reinterpret_cast<const v4f *>(a.x + (inb ? kx : 0));
+    v4f bv{0.0f, 0.0f, 0.0f, 0.0f}, wv{0.0f, 0.0f, 0.0f, 0.0f};
+    if constexpr (NORM) {
+        if (a.b)
+            bv = *reinterpret_cast<const v4f *>(a.b + (inb ? kx : 0));
+        wv = *reinterpret_cast<const v4f *>(a.w + (inb ? kx : 0));
+    }
     // 2. Every tile's group scale for this lane's combine (group 2p + q'/2,
     // row j), then the first weight loads.
     const uint32_t my_group = 2 * part + (q >> 1);
@@ -2329,11 +2346,34 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
         }
     }
 
-    // 4. The slice's operands and group constants.
+    // 4. The slice's operands and group constants.  NORM: every tile slot's
+    // waves hold all of K, and each slot sums its slices' squares (wave
+    // sums, then slice order).
     float v[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t)
         v[t] = inb ? xv[t] : 0.0f;
+    if constexpr (NORM) {
+        __shared__ float squares_part[W];
+        float sv[4], squares = 0.0f;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            sv[t] = a.b ? v[t] + (inb ? bv[t] : 0.0f) : v[t];
+            squares += sv[t] * sv[t];
+        }
+        squares = wave_sum_f(squares);
+        if (lane == 0)
+            squares_part[wave] = squares;
+        __syncthreads();
+        float total = 0.0f;
+#pragma unroll
+        for (int pp = 0; pp < P; ++pp)
+            total += squares_part[tslot * P + pp];
+        const float reciprocal = rms_reciprocal(total, a.k, a.epsilon);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+            v[t] = inb ? (sv[t] * reciprocal) * wv[t] : 0.0f;
+    }
     int e;
     bool bad;
     packed_group_exponent(v, e, bad);
@@ -2477,18 +2517,50 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
             partial[((tslot + TS * i) * P + part) * 16 + j] = total;
     });
 
-    // 6. The slices of each tile, added in order.
+    // 6. The slices of each tile, added in order; ARGMAX (with `argmax` set),
+    // the block's greedy-selection candidate (non-finite outputs poison it).
     __syncthreads();
+    float sum = 0.0f;
+    uint32_t stored = UINT32_MAX;  // the output row this thread wrote
     if (threadIdx.x < uint32_t(TS * R * 16)) {
         const uint32_t tl = threadIdx.x / 16, r = threadIdx.x % 16;
-        float sum = partial[(tl * P) * 16 + r];
+        sum = partial[(tl * P) * 16 + r];
 #pragma unroll
         for (int pp = 1; pp < P; ++pp)
             sum += partial[(tl * P + pp) * 16 + r];
         const uint32_t t = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
         const uint32_t row = t * 16 + r;
-        if (t < a.n_tiles && row < a.n)
+        if (t < a.n_tiles && row < a.n) {
             a.out[row] = sum;
+            stored = row;
+        }
+    }
+    if (ARGMAX && a.argmax) {  // uniform
+        Candidate cand{-__builtin_inff(), UINT32_MAX, 0};
+        if (stored != UINT32_MAX) {
+            if (isfinite(sum)) {
+                cand.value = sum;
+                cand.index = stored;
+            } else {
+                cand.poisoned = 1;
+            }
+        }
+        constexpr int CW = (TS * R * 16 + 63) / 64;  // waves holding candidates
+        __shared__ Candidate wave_cand[CW];
+        if (wave < uint32_t(CW)) {
+#pragma unroll
+            for (int offset = 32; offset > 0; offset >>= 1)
+                merge(cand, __shfl_xor(cand.value, offset, 64),
+                      __shfl_xor(cand.index, offset, 64), __shfl_xor(cand.poisoned, offset, 64));
+            if (lane == 0)
+                wave_cand[wave] = cand;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            for (int w2 = 1; w2 < CW; ++w2)
+                merge(cand, wave_cand[w2].value, wave_cand[w2].index, wave_cand[w2].poisoned);
+            a.argmax[blockIdx.x] = cand;
+        }
     }
 }
 
@@ -3365,17 +3437,29 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
 // 7.13 -> 4.88 (f32 vector GEMV); INT8 8192 x 2048 6.09 -> 4.84, 2048 x 2048
 // 3.71 -> 3.59.  LFM2 greedy decode, 1.2B shape 2073 -> 2168 tok/s (op by
 // op 1439 -> 1585), 350M 3053 -> 3047 (op by op 1741 -> 1923).
+// Returns the number of argmax candidates written (one per block), 0 where
+// the launched kernel writes none.
 template <Format F, bool HALF, int P>
-void launch_wide_row(hipStream_t stream, const StreamArgs &args)
+unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm)
 {
     if (args.n_tiles < kHeadTiles) {
         wide_row_kernel<F, HALF, P, 1, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
-        return;
+        return 0;
     }
     constexpr int R = F == Format::Nf4 && P == 8 ? 8 : 4;
     constexpr int TS = 16 / P;
     const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
+    // The norm comes with the argmax candidates (the LM head of the fused
+    // decode step); NF4 heads keep the separate norm and selection (folded,
+    // the 128-VGPR NF4 head spilled).
+    if constexpr (F != Format::Nf4) {
+        if (norm) {
+            wide_row_kernel<F, HALF, P, R, 16, true, true><<<blocks, 1024, 0, stream>>>(args);
+            return blocks;
+        }
+    }
     wide_row_kernel<F, HALF, P, R><<<blocks, 1024, 0, stream>>>(args);
+    return args.argmax ? 0u : blocks;
 }
 
 // At the head size, tiles per wave R = P, so each block's 16 waves cover 16
@@ -3417,14 +3501,29 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 {
     const bool head = n_tiles >= kHeadTiles;
     const uint32_t max_m = F == Format::Int8 || (F == Format::Ternary && !head) ? 8 : 1;
-    if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
+    const XForm &t = call.xform;
+    auto aligned = [](const void *ptr) { return reinterpret_cast<uintptr_t>(ptr) % 16 == 0; };
+    // The add + RMS norm: one row at the head size (the LM head after the
+    // last block), no side output.
+    const bool norm = t.kind == XKind::AddRms;
+    if (norm && (F == Format::Nf4 || !head || call.m != 1 || t.side || !t.w || !aligned(t.w) ||
+                 (t.b && !aligned(t.b))))
+        return false;
+    const float *x = norm ? t.a : call.x;
+    if (call.separate_prologue || (t.kind != XKind::Plain && !norm) || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
         (call.k != 1024 && call.k != 2048) ||
-        (F == Format::Ternary && head && call.k != 1024) ||
-        reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
+        (F == Format::Ternary && head && call.k != 1024) || !x || !aligned(x))
         return false;
     StreamArgs args{};
-    args.x = call.x;
+    args.x = x;
+    if (norm) {
+        args.b = t.b;
+        args.w = t.w;
+        args.epsilon = t.epsilon;
+    }
+    if (call.m == 1)
+        args.argmax = call.argmax;
     args.tiles = call.a.tiles;
     args.scales = call.a.tiled_scales;
     args.out = call.out_a;
@@ -3453,17 +3552,15 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
             return true;
         }
     }
-    if (call.k == 2048) {
-        if (half)
-            launch_wide_row<F, true, 8>(stream, args);
-        else
-            launch_wide_row<F, false, 8>(stream, args);
-    } else {
-        if (half)
-            launch_wide_row<F, true, 4>(stream, args);
-        else
-            launch_wide_row<F, false, 4>(stream, args);
-    }
+    unsigned blocks;
+    if (call.k == 2048)
+        blocks = half ? launch_wide_row<F, true, 8>(stream, args, norm)
+                      : launch_wide_row<F, false, 8>(stream, args, norm);
+    else
+        blocks = half ? launch_wide_row<F, true, 4>(stream, args, norm)
+                      : launch_wide_row<F, false, 4>(stream, args, norm);
+    if (blocks && args.argmax && call.argmax_count)
+        *call.argmax_count = blocks;
     return true;
 }
 
@@ -3618,6 +3715,13 @@ bool try_wide_one(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 // convolution in the epilogue; ternary and NF4, hidden a multiple of 16.
 // LFM2 greedy decode against the vector GEMV's convolution variant: 1.2B
 // shape 2253 -> 2302 tok/s, 350M 2974 -> 3102.
+bool head_fold_supported(Format f, uint32_t n, uint32_t k)
+{
+    const uint32_t n_tiles = pad_to(n, 64) / 16;
+    return f != Format::Nf4 && n_tiles >= kHeadTiles &&
+           (k == 1024 || (k == 2048 && f == Format::Int8));
+}
+
 bool wide_conv_supported(const PackedCall &call, const ConvStep &conv)
 {
     int p, spw;

@@ -181,7 +181,7 @@ mfh_status run_packed(mfh_ctx *ctx, PackedCall call, const mfh_buf *codes_a,
 mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uint32_t m,
                         uint32_t n, uint32_t k, const mfh_buf *codes_a, const mfh_buf *scales_a,
                         const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
-                        float *out_b)
+                        float *out_b, Candidate *argmax, uint32_t *argmax_count)
 {
     Packed p;
     mfh_status s = check_packed(ctx, codes_a, scales_a, &p);
@@ -219,6 +219,8 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     call.out_a = out_a;
     call.out_b = out_b;
     call.xform = xform;
+    call.argmax = argmax;
+    call.argmax_count = argmax_count;
     if (xform.kind == XKind::Plain)
         call.x = xform.a;  // the GEMV reads a Plain source from call.x
     if (!use_mfma_gemv(ctx, call) || m == 0 || m > 2)
