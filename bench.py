@@ -247,13 +247,17 @@ MFMA_PASSES = {"ternary": 2, "int8": 2, "nf4": 3}
 MFMA_PASSES_SINGLE = {"ternary": 1, "int8": 1, "nf4": 2}
 
 
-def prefill_gemm(backend, reps: int = 5, cpu: bool = True) -> dict:
+def prefill_gemm(backend, reps: int = 20, warm: int = 10, cpu: bool = True) -> dict:
     """Packed GEMM at M in {512, 2048} x {8192x2048, 2048x8192} x 3 formats
     on the matrix-core kernel (exact hi + lo activations, the default, and
     the opt-in single-half activations) and on the FP32-FMA kernel (seeded
-    N(0, 0.02) weights, N(0, 1) activations).  Reports algorithmic TFLOP/s
-    (2*M*N*K), its fraction of the dense f16 MFMA peak, and the fraction
-    counting the MFMA products actually issued (hi/lo passes)."""
+    N(0, 0.02) weights, N(0, 1) activations).  Each case runs `warm`
+    back-to-back launches, then times `reps` more (HIP events): the first
+    few launches after a change of kernel run up to 15 % slower than the
+    sustained rate of a prefill pass, which is a long run of such launches.
+    Reports algorithmic TFLOP/s (2*M*N*K), its fraction of the dense f16
+    MFMA peak, and the fraction counting the MFMA products actually issued
+    (hi/lo passes)."""
     from runtime_amd import convert, hiptime
     from runtime_amd.backend import WEIGHT
 
@@ -272,8 +276,8 @@ def prefill_gemm(backend, reps: int = 5, cpu: bool = True) -> dict:
                 for label, path, mode in (("mfma", 0, 0), ("mfma_single", 0, 1), ("fma", 1, 0)):
                     previous = backend.set_kernel_path(path)
                     previous_mode = backend.set_gemm_activations(mode)
-                    backend.packed_linear(out, xb, cb, sb)
-                    backend.synchronize()
+                    for _ in range(warm):
+                        backend.packed_linear(out, xb, cb, sb)
                     e0, e1 = hiptime.Event(), hiptime.Event()
                     e0.record(stream)
                     for _ in range(reps):

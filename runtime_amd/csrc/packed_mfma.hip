@@ -2196,6 +2196,10 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
 // groups differs.
 // ---------------------------------------------------------------------------
 constexpr int kWideAhead = 3;  // 16-byte lane loads in flight per wave
+// NF4 in wide_row_kernel: ksteps between a kstep's table reads and its
+// products (a ring of that many B-operand pairs in registers).
+constexpr int kNf4TableAhead = 1;
+constexpr int kWideAheadNf4 = 3;
 // The same in the norm variant, whose block barrier holds back the loads
 // issued after it: 1.2B-shape decode 2298 tok/s with 3, 2307 with 6, 2285
 // with all (16).
@@ -2290,7 +2294,7 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
     constexpr int KPL = WideGeo<F>::ksteps_per_load;
     constexpr int KSU = WideGeo<F>::ksteps;
     constexpr int NL = R * L;                       // lane loads per wave
-    constexpr int AHW = NORM ? kWideAheadNorm : kWideAhead;
+    constexpr int AHW = NORM ? kWideAheadNorm : F == Format::Nf4 ? kWideAheadNf4 : kWideAhead;
     constexpr int AH = NL < AHW ? NL : AHW;
     constexpr int G = 2 * P;                        // 128-groups per tile
     constexpr bool NF4 = F == Format::Nf4;
@@ -2317,20 +2321,24 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
             bv = *reinterpret_cast<const v4f *>(a.b + (inb ? kx : 0));
         wv = *reinterpret_cast<const v4f *>(a.w + (inb ? kx : 0));
     }
-    // 2. Every tile's group scale for this lane's combine (group 2p + q'/2,
-    // row j), then the first weight loads.
+    // 2. The group scales of this lane's combine (group 2p + q'/2, row j):
+    // tile i's is loaded one tile ahead (the first two here).  Then the first
+    // weight loads.  Byte offsets from the tile base are 32-bit
+    // (try_wide_row keeps the codes below 4 GiB).
     const uint32_t my_group = 2 * part + (q >> 1);
+    auto scale_of = [&](int i) {
+        return reinterpret_cast<const ST *>(a.scales)[(tile_of(i) * G + my_group) * 16 + j];
+    };
     ST sc[R];
-#pragma unroll
-    for (int i = 0; i < R; ++i)
-        sc[i] = reinterpret_cast<const ST *>(a.scales)[(size_t(tile_of(i)) * G + my_group) * 16 + j];
+    sc[0] = scale_of(0);
+    if constexpr (R > 1)
+        sc[1] = scale_of(1);
     __builtin_amdgcn_sched_barrier(0);
     v4u w[NL];
     auto issue = [&](auto n_tag) {
         constexpr int n = decltype(n_tag)::value;
-        const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
-                         (size_t(tile_of(n / L)) * (P * L) + part * L + n % L) * 64 + lane;
-        w[n] = __builtin_nontemporal_load(src);
+        const uint32_t off = ((tile_of(n / L) * (P * L) + part * L + n % L) * 64 + lane) * 16;
+        w[n] = __builtin_nontemporal_load(reinterpret_cast<const v4u *>(a.tiles + off));
     };
     unroll_groups<AH>(issue);
     __builtin_amdgcn_sched_barrier(0);
@@ -2447,23 +2455,35 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
         b0 = v4u{ent[0].x, ent[0].y, ent[1].x, ent[1].y};
         b1 = v4u{ent[2].x, ent[2].y, ent[3].x, ent[3].y};
     };
-    v4u nb0{}, nb1{};
-    if constexpr (NF4)
-        nf4_entries(w[0][0], nb0, nb1);
+    // NF4: the table entries of kstep t are read TA ksteps ahead of its
+    // products, into ring slot t % TA (the code words of those ksteps are
+    // in loads already issued: TA <= KPL and AH >= 2).
+    constexpr int NKS = NL * KPL;  // ksteps per wave
+    constexpr int TA = NF4 ? (kNf4TableAhead < NKS ? kNf4TableAhead : NKS) : 1;
+    static_assert(!NF4 || (TA <= KPL && AH >= 2), "NF4 table reads run ahead of the loads");
+    v4u pb0[TA], pb1[TA];
+    if constexpr (NF4) {
+        unroll_groups<TA>([&](auto d_tag) {
+            constexpr int d = decltype(d_tag)::value;
+            nf4_entries(w[d / KPL][d % KPL], pb0[d], pb1[d]);
+        });
+    }
 
     // 5. The tiles: products of the slice, then the combine.
     typedef typename std::conditional<NF4, v4f, v4i>::type CT;
     unroll_groups<R>([&](auto i_tag) {
         constexpr int i = decltype(i_tag)::value;
+        if constexpr (i + 2 < R)
+            sc[i + 2] = scale_of(i + 2);
         CT acc = CT{};
         unroll_groups<L>([&](auto l_tag) {
             constexpr int l = decltype(l_tag)::value;
             constexpr int n = i * L + l;
             if constexpr (n + AH < NL)
                 issue(std::integral_constant<int, n + AH>{});
-#pragma unroll
-            for (int ks = 0; ks < KPL; ++ks) {
-                const int s2 = l * KPL + ks;  // kstep within the slice
+            unroll_groups<KPL>([&](auto ks_tag) {
+                constexpr int ks = decltype(ks_tag)::value;
+                constexpr int s2 = l * KPL + ks;  // kstep within the slice
                 if constexpr (F == Format::Int8) {
                     const v4u wv = w[n];
                     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(
@@ -2474,21 +2494,18 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
                                        int(word & 0xF0F0F0F0u), int(word & 0xC0C0C0C0u)};
                     acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(as[s2][0], bw, acc, 0, 0, 0);
                 } else {
-                    // The table entries of this kstep were read ahead (with
-                    // the previous kstep's products); read the next one's
-                    // now, while these products run.
-                    const v4u b0 = nb0, b1 = nb1;
-                    if (ks + 1 < KPL) {
-                        nf4_entries(w[n][ks + 1], nb0, nb1);
-                    } else if constexpr (n + 1 < NL) {
-                        nf4_entries(w[n + 1][0], nb0, nb1);
-                    }
+                    // This kstep's entries were read TA ksteps ago; read
+                    // kstep t + TA's into the freed slot before the products.
+                    constexpr int t = n * KPL + ks, slot = t % TA;
+                    const v4u b0 = pb0[slot], b1 = pb1[slot];
+                    if constexpr (t + TA < NKS)
+                        nf4_entries(w[(t + TA) / KPL][(t + TA) % KPL], pb0[slot], pb1[slot]);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                         operand(s2, 0), __builtin_bit_cast(v8h, b0), acc, 0, 0, 0);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(
                         operand(s2, OPS - 1), __builtin_bit_cast(v8h, b1), acc, 0, 0, 0);
                 }
-            }
+            });
             __builtin_amdgcn_sched_barrier(0);
         });
         float gsum;
@@ -3514,6 +3531,10 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
         (call.k != 1024 && call.k != 2048) ||
         (F == Format::Ternary && head && call.k != 1024) || !x || !aligned(x))
+        return false;
+    // wide_row_kernel addresses the repacked codes with 32-bit byte offsets.
+    if (uint64_t(n_tiles) * 16 * call.k * (F == Format::Int8 ? 8 : F == Format::Nf4 ? 4 : 2) / 8 >=
+        (uint64_t(1) << 32))
         return false;
     StreamArgs args{};
     args.x = x;
