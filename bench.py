@@ -35,7 +35,11 @@ workload's context from a few sampled steps).
 `read_ceiling` is the control for the heads: a plain read of each head's
 algorithmic bytes, timed the same way over 15 launch shapes
 (runtime_amd/libminifield_probe.so); `roofline_by_format` gives each head's
-fraction of it.
+fraction of it.  `head_clocks` times each head in bursts of back-to-back
+launches and reads the shader clock after each burst (the same probe
+library), which shows how far a head's own load lowers the device clock.
+`unit_rates` gives the LDS read and MFMA rates the heads' table lookups and
+products draw on (same library).
 """
 from __future__ import annotations
 
@@ -169,6 +173,81 @@ def read_ceiling(launches: int = 100) -> dict:
     return out
 
 
+def unit_rates() -> dict:
+    """LDS read rates (bytes per ns per CU) at the NF4 level table's access
+    pattern and at other widths, the same reads mixed with f16 MFMAs as an
+    NF4 kstep issues them, and the f16 / int8 MFMA rates (ns per MFMA per
+    SIMD): mfp_unit_rates of runtime_amd/libminifield_probe.so."""
+    import ctypes
+    import pathlib
+
+    lib = ctypes.CDLL(str(pathlib.Path(__file__).resolve().parent / "runtime_amd" /
+                          "libminifield_probe.so"))
+    fn = lib.mfp_unit_rates
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.POINTER(ctypes.c_double)]
+    out = (ctypes.c_double * 6)()
+    if fn(out) != 0:
+        raise RuntimeError("unit-rate probe failed")
+    return {"lds_read_B_per_ns_per_cu": {"b64_nf4_table_pattern": round(out[0], 1),
+                                         "b32": round(out[1], 1), "b128": round(out[2], 1),
+                                         "b64_with_one_f16_mfma_per_two_reads": round(out[3], 1)},
+            "mfma_ns_per_simd": {"f16_16x16x32": round(out[4], 3),
+                                 "i8_16x16x64": round(out[5], 3)}}
+
+
+def shader_clock_fn():
+    """mfp_shader_clock of the probe library: the shader clock (MHz) one
+    probe wave sees when it runs after the work already queued on a stream."""
+    import ctypes
+    import pathlib
+
+    lib = ctypes.CDLL(str(pathlib.Path(__file__).resolve().parent / "runtime_amd" /
+                          "libminifield_probe.so"))
+    fn = lib.mfp_shader_clock
+    fn.restype = ctypes.c_int
+    fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_double)]
+
+    def clock(stream: int) -> float:
+        mhz = ctypes.c_double()
+        if fn(ctypes.c_void_p(stream), ctypes.byref(mhz)) != 0:
+            raise RuntimeError("shader clock probe failed")
+        return round(mhz.value, 0)
+
+    return clock
+
+
+def head_clocks(backend, stream, weights, dev_x, dev_out, bursts: int = 4,
+                reps: int = 100) -> dict:
+    """Each 65536x2048 head at B=1 over a 1 GiB rotation: `bursts` bursts of
+    `reps` back-to-back launches (HIP events), and the shader clock read by
+    one probe wave queued right after each burst (and once before the
+    first).  Shows how far each head's own load lowers the device clock
+    during sustained streaming."""
+    clock = shader_clock_fn()
+    out = {}
+    for fmt in FORMATS:
+        copies = rotation(backend, *weights[(fmt, 65536, 2048)])
+        x, y = dev_x[(1, 2048)], dev_out[(1, 65536)]
+        rot = [0]
+
+        def run(_r, copies=copies):
+            c, s = copies[rot[0] % len(copies)]
+            rot[0] += 1
+            backend.packed_linear(y, x, c, s)
+
+        for _ in range(len(copies)):
+            run(0)
+        entry = {"mhz_before": clock(stream), "us_by_burst": [], "mhz_after_burst": []}
+        for _ in range(bursts):
+            entry["us_by_burst"].append(round(time_launches(backend, stream, run, reps,
+                                                            lambda: None), 2))
+            entry["mhz_after_burst"].append(clock(stream))
+        out[fmt] = entry
+        del copies
+    return out
+
+
 def measure_traffic() -> dict:
     """HBM bytes per dominant launch from two rocprofv3 --pmc runs
     (FETCH_SIZE, then WRITE_SIZE, in KiB per dispatch) of `--profile
@@ -247,17 +326,21 @@ MFMA_PASSES = {"ternary": 2, "int8": 2, "nf4": 3}
 MFMA_PASSES_SINGLE = {"ternary": 1, "int8": 1, "nf4": 2}
 
 
-def prefill_gemm(backend, reps: int = 20, warm: int = 10, cpu: bool = True) -> dict:
+def prefill_gemm(backend, reps: int = 20, warm: int = 10, sustain_ms: float = 30.0,
+                 cpu: bool = True) -> dict:
     """Packed GEMM at M in {512, 2048} x {8192x2048, 2048x8192} x 3 formats
     on the matrix-core kernel (exact hi + lo activations, the default, and
     the opt-in single-half activations) and on the FP32-FMA kernel (seeded
     N(0, 0.02) weights, N(0, 1) activations).  Each case runs `warm`
-    back-to-back launches, then times `reps` more (HIP events): the first
-    few launches after a change of kernel run up to 15 % slower than the
-    sustained rate of a prefill pass, which is a long run of such launches.
-    Reports algorithmic TFLOP/s (2*M*N*K), its fraction of the dense f16
-    MFMA peak, and the fraction counting the MFMA products actually issued
-    (hi/lo passes)."""
+    back-to-back launches and times `reps` more (HIP events): `*_cold_us`.
+    It then keeps launching for about `sustain_ms` of device time and times
+    `reps` more: `*_us`, the sustained rate.  The same kernel on the same
+    operands runs up to 15-20 % faster after some 20 ms of back-to-back
+    launches (the shader clock reads 2.4 GHz throughout), so a short timing
+    window reports the start of a run rather than its rate.  Reports
+    algorithmic TFLOP/s (2*M*N*K) of the sustained rate, its fraction of the
+    dense f16 MFMA peak, and the fraction counting the MFMA products
+    actually issued (hi/lo passes)."""
     from runtime_amd import convert, hiptime
     from runtime_amd.backend import WEIGHT
 
@@ -276,17 +359,24 @@ def prefill_gemm(backend, reps: int = 20, warm: int = 10, cpu: bool = True) -> d
                 for label, path, mode in (("mfma", 0, 0), ("mfma_single", 0, 1), ("fma", 1, 0)):
                     previous = backend.set_kernel_path(path)
                     previous_mode = backend.set_gemm_activations(mode)
+                    def timed() -> float:
+                        e0, e1 = hiptime.Event(), hiptime.Event()
+                        e0.record(stream)
+                        for _ in range(reps):
+                            backend.packed_linear(out, xb, cb, sb)
+                        e1.record(stream)
+                        e1.synchronize()
+                        return e1.elapsed_ms(e0) / reps * 1e3
+
                     for _ in range(warm):
                         backend.packed_linear(out, xb, cb, sb)
-                    e0, e1 = hiptime.Event(), hiptime.Event()
-                    e0.record(stream)
-                    for _ in range(reps):
+                    cold = timed()
+                    for _ in range(int(np.ceil(sustain_ms * 1e3 / cold))):
                         backend.packed_linear(out, xb, cb, sb)
-                    e1.record(stream)
-                    e1.synchronize()
+                    us = timed()
                     backend.set_kernel_path(previous)
                     backend.set_gemm_activations(previous_mode)
-                    us = e1.elapsed_ms(e0) / reps * 1e3
+                    row[label + "_cold_us"] = round(cold, 1)
                     row[label + "_us"] = round(us, 1)
                     row[label + "_TFLOPs"] = round(2 * m * n * k / (us / 1e6) / 1e12, 1)
                 row["mfma_util"] = round(row["mfma_TFLOPs"] / F16_MFMA_PEAK_TFLOPS, 4)
@@ -778,6 +868,9 @@ def main() -> int:
             del copies
     log("streaming-read ceiling")
     ceiling = read_ceiling()
+    log("head clocks")
+    clocks = head_clocks(backend, stream, weights, dev_x, dev_out)
+    rates = unit_rates()
     heads = {}
     for fmt_i in FORMATS:
         entry = detail[f"{fmt_i}:65536x2048:B1"]
@@ -826,6 +919,8 @@ def main() -> int:
         },
         "roofline_by_format": heads,
         "read_ceiling": ceiling,
+        "head_clocks": clocks,
+        "unit_rates": rates,
         "detail": detail,
         "detail_method": {"reps": args.reps, "rotating_copies": rotations,
                           "prime_launches": prime_count},

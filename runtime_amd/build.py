@@ -2,7 +2,7 @@
 
 Compiles every source under runtime_amd/csrc with hipcc for gfx950 into
 runtime_amd/_build/*.o (in parallel) and links runtime_amd/libminifield_hip.so;
-then builds the streaming-read probe (csrc/probe) as
+then builds the measurement probes (csrc/probe) as
 runtime_amd/libminifield_probe.so.
 Run as `python -m runtime_amd.build` or through __graft_entry__.build().
 """
@@ -19,8 +19,9 @@ PACKAGE = pathlib.Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 BUILD = PACKAGE / "_build"
 LIBRARY = PACKAGE / "libminifield_hip.so"
-# The streaming-read ceiling probe (a measurement tool, not the backend).
-PROBE_SRC = CSRC / "probe" / "read_ceiling.hip"
+# The measurement probes (streaming-read ceiling, shader clock, LDS and MFMA
+# unit rates): a library of their own, not the backend.
+PROBE_SRCS = [CSRC / "probe" / "read_ceiling.hip", CSRC / "probe" / "unit_rates.hip"]
 PROBE_LIBRARY = PACKAGE / "libminifield_probe.so"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
@@ -76,10 +77,10 @@ def build(jobs: int | None = None, verbose: bool = False) -> pathlib.Path:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, LIBRARY)
     tmp = PROBE_LIBRARY.with_suffix(".so.tmp")
-    cmd = [HIPCC, *COMMON, "-shared", "-o", str(tmp), str(PROBE_SRC)]
+    cmd = [HIPCC, *COMMON, "-shared", "-o", str(tmp), *[str(p) for p in PROBE_SRCS]]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {PROBE_SRC.name}:\n{proc.stdout}\n{proc.stderr}")
+        raise RuntimeError(f"hipcc failed for the probe library:\n{proc.stdout}\n{proc.stderr}")
     os.replace(tmp, PROBE_LIBRARY)
     return LIBRARY
 

@@ -63,9 +63,48 @@ void launch_any(int kb_per_wave, const v4u *src, size_t chunks, int wpb, unsigne
     }
 }
 
+// One wave reads the core-clock cycle counter (s_memtime) and the
+// constant-rate counter (s_memrealtime) around `spins` further cycle-counter
+// reads: the shader clock the device is running at when it executes.
+__global__ void clock_kernel(unsigned long long *out, int spins)
+{
+    const unsigned long long c0 = __builtin_readcyclecounter();
+    const unsigned long long r0 = __builtin_amdgcn_s_memrealtime();
+    unsigned long long c = c0;
+    for (int i = 0; i < spins; ++i)
+        c = __builtin_readcyclecounter();
+    const unsigned long long r1 = __builtin_amdgcn_s_memrealtime();
+    if (threadIdx.x == 0) {
+        out[0] = c - c0;
+        out[1] = r1 - r0;
+    }
+}
+
 }  // namespace
 
 extern "C" {
+
+// The shader clock (MHz) of the current device, measured by one wave queued
+// on `stream` (a hipStream_t, so it runs right after the work queued before
+// it); waits for the stream.  Returns 0, or -1 on a HIP error.
+int mfp_shader_clock(void *stream, double *mhz)
+{
+    static unsigned long long *counters = nullptr;
+    static int wall_khz = 0;
+    if (!counters && (hipMalloc(&counters, 16) != hipSuccess ||
+                      hipDeviceGetAttribute(&wall_khz, hipDeviceAttributeWallClockRate, 0) !=
+                          hipSuccess || wall_khz <= 0))
+        return -1;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    clock_kernel<<<1, 64, 0, s>>>(counters, 20000);
+    unsigned long long host[2] = {0, 0};
+    if (hipGetLastError() != hipSuccess ||
+        hipMemcpyAsync(host, counters, 16, hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess || host[1] == 0)
+        return -1;
+    *mhz = double(host[0]) * (wall_khz / 1e3) / double(host[1]);
+    return 0;
+}
 
 // Average microseconds per launch of a plain read of `bytes` (a multiple of
 // 1024) over `launches` back-to-back launches rotating over copies totalling
