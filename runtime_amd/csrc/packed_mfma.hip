@@ -2195,11 +2195,18 @@ __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArg
 // exact as in the other kernels; only the order of the f32 additions over
 // groups differs.
 // ---------------------------------------------------------------------------
-constexpr int kWideAhead = 3;  // 16-byte lane loads in flight per wave
+// 16-byte lane loads in flight per wave.  Two measured faster than three
+// once the kernels' register use fell to 56-62 VGPRs (INT8 65536x2048 B=1
+// 22.1-22.3 -> 21.5-21.7 us, 65536x1024 12.0-12.2 -> 11.6-11.7, 8192x2048
+// 4.85-4.92 -> 4.65-4.73; four and five in between), with LFM2 decode and
+// the ternary products unchanged.
+constexpr int kWideAhead = 2;
 // NF4 in wide_row_kernel: ksteps between a kstep's table reads and its
 // products (a ring of that many B-operand pairs in registers).
 constexpr int kNf4TableAhead = 1;
-constexpr int kWideAheadNf4 = 3;
+// The NF4 head: two measured slightly faster than three (mean of eight
+// 100-launch bursts 15.2 against 15.7 us; four to six slower).
+constexpr int kWideAheadNf4 = 2;
 // The same in the norm variant, whose block barrier holds back the loads
 // issued after it: 1.2B-shape decode 2298 tok/s with 3, 2307 with 6, 2285
 // with all (16).
