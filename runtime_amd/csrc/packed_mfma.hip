@@ -94,14 +94,6 @@ __device__ __forceinline__ float wave_max(float v)
     return v;
 }
 
-__device__ __forceinline__ int wave_sum_i(int v)
-{
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1)
-        v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 __device__ __forceinline__ float silu_mul(float gate, float up)
 {
     float sigmoid = 1.0f / (1.0f + expf(-gate));
