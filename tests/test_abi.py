@@ -70,10 +70,12 @@ def test_library_is_built_for_gfx950():
 
 def test_read_ceiling_probe_loads_and_rejects_bad_sizes():
     """The measurement probe (runtime_amd/libminifield_probe.so) exports its
-    one entry point and refuses arguments it cannot time before touching the
+    entry points and refuses arguments it cannot time before touching the
     device."""
     import ctypes
     probe = ctypes.CDLL(str(ROOT / "runtime_amd" / "libminifield_probe.so"))
+    for name in ("mfp_read_ceiling", "mfp_shader_clock", "mfp_unit_rates"):
+        assert hasattr(probe, name), name
     fn = probe.mfp_read_ceiling
     fn.restype = ctypes.c_int
     fn.argtypes = [ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_int),
