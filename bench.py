@@ -617,10 +617,13 @@ def profile_only(backend, args) -> int:
         sb = backend.upload_f32_classified(scales.shape, scales, WEIGHT)
         xb = backend.upload_f32((m, k), convert.normal((m, k), 0xAC70101 + m))
         out = backend.allocate_f32((m, n))
-        for _ in range(6):
+        # About 30 ms of back-to-back calls: the last ones run at the
+        # sustained rate (the first after idle run 12-20 % slower).
+        calls = 200
+        for _ in range(calls):
             backend.packed_linear(out, xb, cb, sb)
         backend.synchronize()
-        log(f"gemm {args.gemm_format} M={m} {n}x{k} x 6 ({args.profile})")
+        log(f"gemm {args.gemm_format} M={m} {n}x{k} x {calls} ({args.profile})")
         return 0
     if args.profile == "read-ceiling":
         log(json.dumps(read_ceiling()))
