@@ -1669,12 +1669,18 @@ void launch_rotation_table(hipStream_t stream, float *table, uint64_t positions,
             table, positions, head_dim, theta);
 }
 
-void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p)
+void launch_gqa_combine(hipStream_t stream, const DecodeAttention &p)
+{
+    gqa_combine_kernel<<<p.query_heads, kBlock, (size_t(p.splits) + kBlock) * sizeof(float),
+                         stream>>>(p.out, p.partial, p.head_dim, p.splits);
+}
+
+void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p, bool combine)
 {
     gqa_decode_kernel<<<p.key_value_heads * p.splits, kBlock,
                         gqa_split_lds(p.group, p.head_dim), stream>>>(p);
-    gqa_combine_kernel<<<p.query_heads, kBlock, (size_t(p.splits) + kBlock) * sizeof(float),
-                         stream>>>(p.out, p.partial, p.head_dim, p.splits);
+    if (combine)
+        launch_gqa_combine(stream, p);
 }
 
 void launch_short_conv(hipStream_t stream, float *out, const float *projection,

@@ -31,15 +31,23 @@ enum class XKind : uint32_t {
     Plain = 0,   // x = a
     AddRms = 1,  // s = a + b (b may be null); x = (s * rsqrt(mean(s^2) + eps)) * w
     Swiglu = 2,  // x = silu(a) * b
+    // x = one decode token's attention output merged from its key ranges:
+    // a holds launch_gqa_decode's (m, l, acc[head_dim]) records, `ranges`
+    // per head (gqa_combine_kernel's formula, summed in range order).
+    GqaMerge = 3,
 };
 struct XForm {
     XKind kind = XKind::Plain;
-    const float *a = nullptr;  // Plain x; AddRms left; Swiglu gate
+    const float *a = nullptr;  // Plain x; AddRms left; Swiglu gate; GqaMerge records
     const float *b = nullptr;  // AddRms right; Swiglu up
     const float *w = nullptr;  // AddRms norm weight [k]
     float *side = nullptr;     // AddRms: s [m, k] (may be null)
     float epsilon = 0.0f;
+    uint32_t ranges = 0, head_dim = 0;  // GqaMerge
 };
+// Most key ranges per head a GqaMerge prologue reads (each lane merges its
+// head's records itself; more ranges keep the separate combine launch).
+constexpr uint32_t kGqaMergeMaxRanges = 8;
 
 constexpr uint32_t kMaxSegments = 3;
 
@@ -132,6 +140,9 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
                         const mfh_buf *codes_b, const mfh_buf *scales_b, float *out_a,
                         float *out_b, Candidate *argmax = nullptr,
                         uint32_t *argmax_count = nullptr);
+// Whether the one-row wide kernel serves `call` with its GqaMerge prologue
+// (the only kernel that reads that transform).
+bool gqa_merge_supported(const PackedCall &call);
 // Whether a one-row product of n x k weights in format f at the head size
 // takes the add + RMS norm and the argmax candidates in its one launch
 // (the one-row wide kernel).
@@ -311,7 +322,11 @@ void launch_rotation_table(hipStream_t stream, float *table, uint64_t positions,
                            uint32_t head_dim, float theta);
 uint32_t gqa_decode_splits(const DecodeAttention &p);
 size_t gqa_decode_scratch_bytes(const DecodeAttention &p);
-void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p);
+// `combine` false: the key ranges' records only, for a GqaMerge prologue
+// (launch_gqa_combine merges them into p.out later if that prologue does
+// not serve the projection).
+void launch_gqa_decode(hipStream_t stream, const DecodeAttention &p, bool combine = true);
+void launch_gqa_combine(hipStream_t stream, const DecodeAttention &p);
 void launch_short_conv(hipStream_t stream, float *out, const float *projection,
                        const float *kernel, float *history, uint64_t tokens, uint32_t hidden,
                        uint32_t width);

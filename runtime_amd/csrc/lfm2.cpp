@@ -381,11 +381,20 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
             da.epsilon = cfg.block_norm_epsilon;
             da.scale = 1.0f / std::sqrt(float(cfg.head_dim));
             da.splits = gqa_decode_splits(da);
+            // With few key ranges the output projection merges them in its
+            // prologue (no combine launch); else the combine kernel does.
+            XForm merged;
+            merged.kind = XKind::GqaMerge;
+            merged.ranges = da.splits;
+            merged.head_dim = cfg.head_dim;
+            bool merge = false;
             if (da.splits) {
                 da.partial = static_cast<float *>(work_scratch(c, gqa_decode_scratch_bytes(da)));
                 if (!da.partial)
                     return allocation_failed(c);
-                launch_gqa_decode(c->stream, da);
+                merged.a = da.partial;
+                merge = da.splits <= kGqaMergeMaxRanges;
+                launch_gqa_decode(c->stream, da, !merge);
             } else {
                 Positions positions;
                 positions.base = position;
@@ -411,11 +420,25 @@ mfh_status decode_step(mfl_model *m, const mfh_buf *device_ids, bool produce_log
                            dev(st.key), dev(st.value), g, partials);
             }
             st.length += 1;
-            XForm plain;
-            plain.a = dev(ws->attention);
-            if ((s = packed_xform(c, Epilogue::Single, plain, 1, h, h, lw.output.tensor,
-                                  lw.output.scales, nullptr, nullptr, op, nullptr)))
-                return s;
+            if (merge) {
+                s = packed_xform(c, Epilogue::Single, merged, 1, h, h, lw.output.tensor,
+                                 lw.output.scales, nullptr, nullptr, op, nullptr);
+                if (s == MFH_UNSUPPORTED) {
+                    // Not the one-row wide kernel's shape: combine, then the
+                    // plain projection below.
+                    launch_gqa_combine(c->stream, da);
+                    merge = false;
+                } else if (s) {
+                    return s;
+                }
+            }
+            if (!merge) {
+                XForm plain;
+                plain.a = dev(ws->attention);
+                if ((s = packed_xform(c, Epilogue::Single, plain, 1, h, h, lw.output.tensor,
+                                      lw.output.scales, nullptr, nullptr, op, nullptr)))
+                    return s;
+            }
         }
         // FFN: residual = block input + op, normed into the gate/up pair,
         // whose epilogue forms silu(gate) * up (the value packed_swiglu_linear

@@ -1233,6 +1233,9 @@ struct StreamArgs {
     const float *b = nullptr, *w = nullptr;
     float epsilon = 0.0f;
     Candidate *argmax = nullptr;
+    // wide_row_kernel at one tile per block, MERGE: x is merged from the
+    // decode attention's key-range records (XKind::GqaMerge) at a.x.
+    uint32_t ranges = 0, head_dim = 0;
 };
 
 // One (batch slot, group) record of the prologue: the correction pair and
@@ -2284,9 +2287,60 @@ struct WideGeo {
     static constexpr int ksteps = loads * ksteps_per_load;  // 4, 8, 4
 };
 
-template <Format F, bool HALF, int P, int R, int W = 16, bool NORM = false, bool ARGMAX = false>
+// One decode token's attention output at k .. k + 3 (one head, head_dim a
+// multiple of 4) merged from its key ranges' (m, l, acc) records by
+// gqa_combine_kernel's formula: weights e^(m_s - M) over the non-empty
+// ranges (l != 0), M their largest m, divided by the weighted sum of l.  The
+// sums run serially in range order (the combine kernel's run as block
+// reductions, so the two round differently in the last bits); a NaN in any
+// record reaches the output.  Every record is loaded before any is used
+// (one memory round trip).
+__device__ __forceinline__ void gqa_merge4(const float *records, uint32_t ranges,
+                                           uint32_t head_dim, uint32_t k, float (&v)[4])
+{
+    constexpr int S = int(kGqaMergeMaxRanges);
+    const uint32_t head = k / head_dim, dim = k % head_dim;
+    const uint32_t stride = head_dim + 2;
+    const float *rec = records + size_t(head) * ranges * stride;
+    float m[S], l[S];
+    float2 lo[S], hi[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const bool live = uint32_t(s) < ranges;
+        const float *r = rec + (live ? s : 0) * stride;
+        m[s] = r[0];
+        l[s] = live ? r[1] : 0.0f;
+        // acc[dim .. dim + 3]: 8-byte aligned (stride and dim are even).
+        lo[s] = *reinterpret_cast<const float2 *>(r + 2 + dim);
+        hi[s] = *reinterpret_cast<const float2 *>(r + 4 + dim);
+    }
+    float maximum = -__builtin_inff();
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+        if (l[s] != 0.0f)
+            maximum = fmaxf(maximum, m[s]);
+    float denominator = 0.0f, acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        if (l[s] == 0.0f)
+            continue;  // an empty (or absent) range: weight 0, acc 0
+        const float w = expf(m[s] - maximum);
+        denominator += l[s] * w;
+        acc[0] += lo[s].x * w;
+        acc[1] += lo[s].y * w;
+        acc[2] += hi[s].x * w;
+        acc[3] += hi[s].y * w;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+        v[t] = acc[t] / denominator;
+}
+
+template <Format F, bool HALF, int P, int R, int W = 16, bool NORM = false, bool ARGMAX = false,
+          bool MERGE = false>
 __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 {
+    static_assert(!MERGE || (R == 1 && !NORM), "the merge prologue: one tile per block");
     using ST = typename ScaleT<HALF>::type;
     constexpr int TS = W / P;                      // tiles per round
     constexpr int L = WideGeo<F>::loads;
@@ -2313,7 +2367,14 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
     const uint32_t kx = NF4 ? 256 * part + 32 * ((lane >> 1) & 7) + 8 * q + 4 * (lane & 1)
                             : 256 * part + 64 * ((lane >> 2) & 3) + 16 * q + 4 * (lane & 3);
     const bool inb = kx < a.k;
-    const v4f xv = *reinterpret_cast<const v4f *>(a.x + (inb ? kx : 0));
+    v4f xv;
+    if constexpr (MERGE) {
+        float mv[4];
+        gqa_merge4(a.x, a.ranges, a.head_dim, inb ? kx : 0, mv);
+        xv = v4f{mv[0], mv[1], mv[2], mv[3]};
+    } else {
+        xv = *reinterpret_cast<const v4f *>(a.x + (inb ? kx : 0));
+    }
     v4f bv{0.0f, 0.0f, 0.0f, 0.0f}, wv{0.0f, 0.0f, 0.0f, 0.0f};
     if constexpr (NORM) {
         if (a.b)
@@ -3456,10 +3517,14 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
 // Returns the number of argmax candidates written (one per block), 0 where
 // the launched kernel writes none.
 template <Format F, bool HALF, int P>
-unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm)
+unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, bool merge)
 {
     if (args.n_tiles < kHeadTiles) {
-        wide_row_kernel<F, HALF, P, 1, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
+        if (merge)
+            wide_row_kernel<F, HALF, P, 1, P, false, false, true><<<args.n_tiles, 64 * P, 0,
+                                                                   stream>>>(args);
+        else
+            wide_row_kernel<F, HALF, P, 1, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
         return 0;
     }
     constexpr int R = F == Format::Nf4 && P == 8 ? 8 : 4;
@@ -3525,8 +3590,14 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     if (norm && (F == Format::Nf4 || !head || call.m != 1 || t.side || !t.w || !aligned(t.w) ||
                  (t.b && !aligned(t.b))))
         return false;
-    const float *x = norm ? t.a : call.x;
-    if (call.separate_prologue || (t.kind != XKind::Plain && !norm) || call.segments ||
+    // The attention merge: one row below the head size (an attention output
+    // projection), at most kGqaMergeMaxRanges ranges of whole heads.
+    const bool merge = t.kind == XKind::GqaMerge;
+    if (merge && (head || call.m != 1 || t.ranges == 0 || t.ranges > kGqaMergeMaxRanges ||
+                  t.head_dim == 0 || t.head_dim % 4 || call.k % t.head_dim))
+        return false;
+    const float *x = norm || merge ? t.a : call.x;
+    if (call.separate_prologue || (t.kind != XKind::Plain && !norm && !merge) || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
         (call.k != 1024 && call.k != 2048) ||
         (F == Format::Ternary && head && call.k != 1024) || !x || !aligned(x))
@@ -3541,6 +3612,10 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
         args.b = t.b;
         args.w = t.w;
         args.epsilon = t.epsilon;
+    }
+    if (merge) {
+        args.ranges = t.ranges;
+        args.head_dim = t.head_dim;
     }
     if (call.m == 1)
         args.argmax = call.argmax;
@@ -3574,11 +3649,11 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     }
     unsigned blocks;
     if (call.k == 2048)
-        blocks = half ? launch_wide_row<F, true, 8>(stream, args, norm)
-                      : launch_wide_row<F, false, 8>(stream, args, norm);
+        blocks = half ? launch_wide_row<F, true, 8>(stream, args, norm, merge)
+                      : launch_wide_row<F, false, 8>(stream, args, norm, merge);
     else
-        blocks = half ? launch_wide_row<F, true, 4>(stream, args, norm)
-                      : launch_wide_row<F, false, 4>(stream, args, norm);
+        blocks = half ? launch_wide_row<F, true, 4>(stream, args, norm, merge)
+                      : launch_wide_row<F, false, 4>(stream, args, norm, merge);
     if (blocks && args.argmax && call.argmax_count)
         *call.argmax_count = blocks;
     return true;
@@ -4101,8 +4176,33 @@ size_t gemv_mfma_scratch_bytes(const PackedCall &call)
            size_t(8) * (k_pad / 128) * 4 * sizeof(int);
 }
 
+bool gqa_merge_supported(const PackedCall &call)
+{
+    const uint32_t n_tiles = pad_to(call.n, 64) / 16;
+    const XForm &t = call.xform;
+    const uint64_t code_bytes = uint64_t(n_tiles) * 16 * call.k *
+                                (call.format == Format::Int8 ? 8 : call.format == Format::Nf4 ? 4 : 2) / 8;
+    return t.kind == XKind::GqaMerge && t.a && call.m == 1 && !call.separate_prologue &&
+           !call.segments && call.epilogue == Epilogue::Single && n_tiles < kHeadTiles &&
+           (call.k == 1024 || call.k == 2048) && code_bytes < (uint64_t(1) << 32) &&
+           reinterpret_cast<uintptr_t>(t.a) % 16 == 0 && t.ranges > 0 &&
+           t.ranges <= kGqaMergeMaxRanges && t.head_dim > 0 && t.head_dim % 4 == 0 &&
+           call.k % t.head_dim == 0;
+}
+
 void launch_gemv_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
 {
+    if (call.xform.kind == XKind::GqaMerge) {
+        // Only the one-row wide kernel reads the merge transform; callers
+        // check gqa_merge_supported first.
+        const uint32_t n_tiles = pad_to(call.n, 64) / 16;
+        switch (call.format) {
+        case Format::Ternary: (void)try_wide_row<Format::Ternary>(stream, call, n_tiles); break;
+        case Format::Int8: (void)try_wide_row<Format::Int8>(stream, call, n_tiles); break;
+        case Format::Nf4: (void)try_wide_row<Format::Nf4>(stream, call, n_tiles); break;
+        }
+        return;
+    }
     switch (call.format) {
     case Format::Ternary: gemv_i8_format<Format::Ternary>(stream, call, scratch); break;
     case Format::Int8: gemv_i8_format<Format::Int8>(stream, call, scratch); break;

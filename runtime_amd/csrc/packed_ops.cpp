@@ -204,6 +204,7 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     case XKind::Plain: break;
     case XKind::AddRms: operands = operands && xform.w; break;
     case XKind::Swiglu: operands = operands && xform.b; break;
+    case XKind::GqaMerge: break;
     }
     if (!operands)
         return fail(ctx, MFH_INVALID_ARGUMENT, "fused decode product is missing an operand");
@@ -223,7 +224,16 @@ mfh_status packed_xform(mfh_ctx *ctx, Epilogue epilogue, const XForm &xform, uin
     call.argmax_count = argmax_count;
     if (xform.kind == XKind::Plain)
         call.x = xform.a;  // the GEMV reads a Plain source from call.x
-    if (!use_mfma_gemv(ctx, call) || m == 0 || m > 2)
+    const bool mfma = use_mfma_gemv(ctx, call) && m >= 1 && m <= 2;
+    if (xform.kind == XKind::GqaMerge) {
+        // A merge the one-row wide kernel cannot serve is the caller's
+        // ordinary case (it combines the ranges and projects plainly), so
+        // it leaves no error message.
+        call.separate_prologue = ctx->kernel_path == 2;
+        if (!mfma || !gqa_merge_supported(call))
+            return MFH_UNSUPPORTED;
+    }
+    if (!mfma)
         return fail(ctx, MFH_UNSUPPORTED, "fused decode product needs the matrix-core GEMV");
     DeviceGuard guard(ctx->device);
     return run_packed(ctx, call, codes_a, scales_a, codes_b, scales_b);
