@@ -1261,9 +1261,13 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
     typedef typename std::conditional<HALF, uint2, v4u>::type SV;
     constexpr int SLANES = G * 16 * (HALF ? 2 : 4) / int(sizeof(SV));
     // Fragments [kstep][fragment][lane] (the MFMA A operand of every lane),
-    // records [slot][group], each wave's scale block.
+    // records [slot][group] with one spare record per slot (a slot stride of
+    // G + 1 records puts the four lane blocks' reads of one group in
+    // different banks; at G records they fell in the same ones: 65536 x
+    // 2048 at B = 8 13.1-14.1 -> 11.9-12.8 us with the records read one
+    // group ahead), each wave's scale block.
     __shared__ v4i frag[KS * NF * 64];
-    __shared__ StreamRecord rec[4 * NF * G];
+    __shared__ StreamRecord rec[4 * NF * (G + 1)];
     __shared__ SV scale_lds[W * SLANES];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
@@ -1320,7 +1324,7 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
             if (j == 0) {
 #pragma unroll
                 for (int gg = 0; gg < 2; ++gg)
-                    rec[(4 * F + q) * G + 2 * pu + gg] =
+                    rec[(4 * F + q) * (G + 1) + 2 * pu + gg] =
                         StreamRecord{blk.cv[gg][F], blk.xf[gg][F], 0.0f};
             }
         };
@@ -1350,13 +1354,23 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
     for (int f = 0; f < NF; ++f)
         accf[f] = 0.0f;
     v4i cur[2][NF], next[2][NF];
+    // Each group's records are read with its fragments, one group ahead.
+    StreamRecord rcur[NF], rnext[NF];
+    auto read_records = [&](int g, StreamRecord (&rv)[NF]) {
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            rv[f] = rec[(4 * f + q) * (G + 1) + g];
+    };
     read_group(0, cur);
+    read_records(0, rcur);
 #pragma unroll
     for (int g = 0; g < G; ++g) {
         if (g % 2 == 0 && g / 2 + AHEAD < KL)
             w[g / 2 + AHEAD] = __builtin_nontemporal_load(&wp[(g / 2 + AHEAD) * 64]);
-        if (g + 1 < G)
+        if (g + 1 < G) {
             read_group(g + 1, next);
+            read_records(g + 1, rnext);
+        }
         v4i acci[NF];
 #pragma unroll
         for (int f = 0; f < NF; ++f)
@@ -1374,7 +1388,7 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
         const float scale = to_f32<HALF>(scl[g * 16]);
 #pragma unroll
         for (int f = 0; f < NF; ++f) {
-            const StreamRecord r = rec[(4 * f + q) * G + g];
+            const StreamRecord r = rcur[f];
             const v4i d = acci[f];
             // |d.x| < 2^21, so the pairs combine exactly in int32.
             const int hi = (d.x << 8) + d.y - r.corr.x;
@@ -1390,6 +1404,9 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_kernel(StreamArgs a)
 #pragma unroll
             for (int f = 0; f < NF; ++f)
                 cur[kk][f] = next[kk][f];
+#pragma unroll
+        for (int f = 0; f < NF; ++f)
+            rcur[f] = rnext[f];
         __builtin_amdgcn_sched_barrier(0);
     }
     const uint32_t row = tile_id * 16 + j;
@@ -2652,14 +2669,18 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 // accumulator.  Output lane block q holds batch 4f + q: the group sums,
 // scales and slice order are wide_row_kernel's, so each row's result is the
 // one-row kernel's bit for bit.  Rows at or beyond m read row 0 and are
-// zeroed.
-template <Format F, bool HALF, int P, int R, int NF, int W = 16>
+// zeroed.  FS = 2 splits a slice's two fragments over two waves (each forms
+// and multiplies one, both loading the slice's weights), halving the
+// digit prologue on each wave's path.
+template <Format F, bool HALF, int P, int R, int NF, int W = 16, int FS = 1>
 __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
 {
     static_assert(F != Format::Nf4, "integer formats");
+    static_assert(NF % FS == 0, "whole fragments per wave");
     using ST = typename ScaleT<HALF>::type;
-    using Blk = I8Block<F, 1, 1, NF, HALF>;
-    constexpr int TS = W / P;                       // tiles per round
+    constexpr int NFL = NF / FS;                    // fragments this wave forms
+    using Blk = I8Block<F, 1, 1, NFL, HALF>;
+    constexpr int TS = W / (P * FS);                // tiles per round
     constexpr int L = WideGeo<F>::loads;
     constexpr int KPL = WideGeo<F>::ksteps_per_load;
     constexpr int NL = R * L;                       // lane loads per wave
@@ -2671,7 +2692,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     __shared__ float partial[TS * R * P * MB * 16];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t part = wave % P, tslot = wave / P;
+    const uint32_t part = wave % P, fbase = NFL * ((wave / P) % FS), tslot = wave / (P * FS);
     const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
     auto tile_of = [&](int i) {
         const uint32_t t = tile0 + uint32_t(TS * i);
@@ -2682,11 +2703,12 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     // 256 P, so every address lies in the row).
     const uint32_t b = (lane >> 2) & 3;
     const uint32_t off = 256 * part + 16 * q + 4 * (lane & 3);
-    RegX<LB> rx[NF][NB];
+    RegX<LB> rx[NFL][NB];
 #pragma unroll
-    for (int f = 0; f < NF; ++f) {
-        const bool live = 4 * f + b < a.m;
-        const float *xrow = a.x + size_t(live ? 4 * f + b : 0) * a.k + off;
+    for (int f = 0; f < NFL; ++f) {
+        const uint32_t row = 4 * (fbase + f) + b;
+        const bool live = row < a.m;
+        const float *xrow = a.x + size_t(live ? row : 0) * a.k + off;
 #pragma unroll
         for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
@@ -2720,17 +2742,17 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
 #pragma unroll
     for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-        for (int f = 0; f < NF; ++f)
+        for (int f = 0; f < NFL; ++f)
             reg_digits(rx[f][bi], blk[bi], f);
 
     // 4. The tiles: products of the slice per group, then the combine.
     unroll_groups<R>([&](auto i_tag) {
         constexpr int i = decltype(i_tag)::value;
-        v4i acc[2][NF];
+        v4i acc[2][NFL];
 #pragma unroll
         for (int gs = 0; gs < 2; ++gs)
 #pragma unroll
-            for (int f = 0; f < NF; ++f)
+            for (int f = 0; f < NFL; ++f)
                 acc[gs][f] = v4i{0, 0, 0, 0};
         unroll_groups<L>([&](auto l_tag) {
             constexpr int l = decltype(l_tag)::value;
@@ -2750,14 +2772,14 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                     bw = v4i{int(wv.x), int(wv.y), int(wv.z), int(wv.w)};
                 }
 #pragma unroll
-                for (int f = 0; f < NF; ++f)
+                for (int f = 0; f < NFL; ++f)
                     acc[s2 / 2][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                         blk[s2 / LB].af[s2 % LB][f], bw, acc[s2 / 2][f], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         });
 #pragma unroll
-        for (int f = 0; f < NF; ++f) {
+        for (int f = 0; f < NFL; ++f) {
             // Each group's product is rounded before the add (no fused
             // multiply-add), as the one-row kernel's cross-lane sum.
 #pragma clang fp contract(off)
@@ -2774,7 +2796,8 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                 const float gsum = float(hi) * 65536.0f + float(lo);
                 g[gs] = gsum * (to_f32<HALF>(sc[i][gs]) * xf);
             }
-            partial[(((tslot + TS * i) * P + part) * MB + 4 * f + q) * 16 + j] = g[0] + g[1];
+            partial[(((tslot + TS * i) * P + part) * MB + 4 * (fbase + f) + q) * 16 + j] =
+                g[0] + g[1];
         }
     });
 
@@ -3552,6 +3575,15 @@ unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, 
 // telescoping), repeated by every wave of a slice, cost more than it saved
 // (65536 x 2048, B = 2 / 4 / 8: R = 8 8.9 / 9.3 / 14.2 us against 8.1 / 8.9
 // / 14.3).
+// Below the head size, five to eight rows: each slice's two fragments on
+// two waves (wide_rows_kernel FS = 2) when the one-wave launch holds at most
+// two waves per SIMD (tiles x slices <= 2048).  Measured at B = 8 (us per
+// launch, A/B on one device): INT8 1024 x 1024 3.9 -> 3.4-3.7, ternary 4608
+// x 1024 5.4-5.5 -> 5.2-5.3, ternary 2048 x 2048 5.5 -> 5.4, INT8 2048 x
+// 2048 5.0-5.2 -> 5.0-5.1 (B = 5 5.0 -> 4.7); at four waves per SIMD the
+// duplicated weight loads cost more (INT8 8192 x 2048 7.1 -> 7.5).
+constexpr uint32_t kWideRowsSplitWaves = 2048;
+
 template <Format F, bool HALF, int P, int NF>
 void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
 {
@@ -3564,6 +3596,13 @@ void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
     // / 6.22 / 8.16 -> 5.05 / 5.14 / 7.12 (1024 x 1024: 3.25 / 3.22 / 3.94 ->
     // 3.51 / 3.46 / 3.70).
     if (args.n_tiles < kHeadTiles) {
+        if constexpr (NF == 2) {
+            if (args.n_tiles * uint32_t(P) <= kWideRowsSplitWaves) {
+                wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 2>
+                    <<<args.n_tiles, 128 * P, 0, stream>>>(args);
+                return;
+            }
+        }
         wide_rows_kernel<F, HALF, P, 1, NF, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
         return;
     }

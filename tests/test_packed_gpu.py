@@ -205,24 +205,26 @@ def test_one_row_few_tiles(backend, path, scheme, n, k):
 
 @pytest.mark.parametrize("scheme", ["ternary", "int8"])
 @pytest.mark.parametrize("k", [1024, 2048])
-def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k):
-    """Past 4096 row tiles with the last tile five rows long: two and five
-    activation rows (dead batch slots in the one- and two-fragment layouts)
-    against the oracle, and for INT8 every row of the batch equal bit for bit
-    to the same row multiplied alone (the multi-row wide kernel keeps the
-    one-row kernel's group and slice order)."""
-    say("wide rows", scheme, path, k)
-    n = 65541
+@pytest.mark.parametrize("n", [65541, 2053])
+def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k, n):
+    """Past 4096 row tiles (n = 65541) and at 129 row tiles (n = 2053, where
+    five to eight rows split each slice's two fragments over two waves), the
+    last tile five rows long: two, five and eight activation rows (dead batch
+    slots in the one- and two-fragment layouts) against the oracle, and for
+    INT8 every row of the batch equal bit for bit to the same row multiplied
+    alone (the multi-row wide kernel keeps the one-row kernel's group and
+    slice order)."""
+    say("wide rows", scheme, path, k, n)
     codes, scales = make_weights(n, k, scheme, 0x5EED0008 + k)
     cb, sb = upload_weights(backend, codes, scales)
-    x = convert.normal((5, k), 0xAC70021 + k)
+    x = convert.normal((8, k), 0xAC70021 + k)
     alone = []
-    for b in range(5):
+    for b in range(8):
         xb = backend.upload_f32((1, k), x[b:b + 1])
         out = backend.allocate_f32((1, n))
         backend.packed_linear(out, xb, cb, sb)
         alone.append(backend.read(out)[0])
-    for m in (2, 5):
+    for m in (2, 5, 8):
         xb = backend.upload_f32((m, k), x[:m])
         out = backend.allocate_f32((m, n))
         backend.packed_linear(out, xb, cb, sb)
