@@ -2671,38 +2671,45 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 // one-row kernel's bit for bit.  Rows at or beyond m read row 0 and are
 // zeroed.  FS = 2 splits a slice's two fragments over two waves (each forms
 // and multiplies one, both loading the slice's weights), halving the
-// digit prologue on each wave's path.
-template <Format F, bool HALF, int P, int R, int NF, int W = 16, int FS = 1>
+// digit prologue on each wave's path.  HS = 2 (INT8) splits each slice into
+// two 128-k pieces, one group each, on two waves (half the weight loads and
+// digits per wave, none duplicated); the block adds the two pieces of a
+// slice before adding the slices in order, the one-row kernel's sum.
+template <Format F, bool HALF, int P, int R, int NF, int W = 16, int FS = 1, int HS = 1>
 __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
 {
     static_assert(F != Format::Nf4, "integer formats");
     static_assert(NF % FS == 0, "whole fragments per wave");
+    static_assert(HS == 1 || (HS == 2 && F == Format::Int8), "128-k pieces: INT8");
     using ST = typename ScaleT<HALF>::type;
     constexpr int NFL = NF / FS;                    // fragments this wave forms
     using Blk = I8Block<F, 1, 1, NFL, HALF>;
-    constexpr int TS = W / (P * FS);                // tiles per round
-    constexpr int L = WideGeo<F>::loads;
+    constexpr int PW = P * HS;                      // slice pieces per tile
+    constexpr int TS = W / (PW * FS);               // tiles per round
+    constexpr int LS = WideGeo<F>::loads;           // lane loads per (tile, slice)
+    constexpr int L = LS / HS;                      // ... per (tile, piece)
     constexpr int KPL = WideGeo<F>::ksteps_per_load;
     constexpr int NL = R * L;                       // lane loads per wave
     constexpr int AH = NL < kWideAhead ? NL : kWideAhead;
     constexpr int G = 2 * P;                        // 128-groups per tile
+    constexpr int GW = 2 / HS;                      // 128-groups per piece
     constexpr int LB = Geo<F>::lb;                  // ksteps per digit block
-    constexpr int NB = 4 / LB;                      // digit blocks per slice
+    constexpr int NB = 4 / LB / HS;                 // digit blocks per piece
     constexpr int MB = 4 * NF;                      // batch rows held
-    __shared__ float partial[TS * R * P * MB * 16];
+    __shared__ float partial[TS * R * PW * MB * 16];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t part = wave % P, fbase = NFL * ((wave / P) % FS), tslot = wave / (P * FS);
+    const uint32_t part = wave % PW, fbase = NFL * ((wave / PW) % FS), tslot = wave / (PW * FS);
     const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
     auto tile_of = [&](int i) {
         const uint32_t t = tile0 + uint32_t(TS * i);
         return t < a.n_tiles ? t : a.n_tiles - 1;
     };
 
-    // 1. The slice's activations: one float4 per kstep and fragment (K is
+    // 1. The piece's activations: one float4 per kstep and fragment (K is
     // 256 P, so every address lies in the row).
     const uint32_t b = (lane >> 2) & 3;
-    const uint32_t off = 256 * part + 16 * q + 4 * (lane & 3);
+    const uint32_t off = (256 / HS) * part + 16 * q + 4 * (lane & 3);
     RegX<LB> rx[NFL][NB];
 #pragma unroll
     for (int f = 0; f < NFL; ++f) {
@@ -2717,27 +2724,27 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                 rx[f][bi].v[kk] = live ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
             }
     }
-    // 2. Both group scales of every tile (this lane's row j), then the
-    // first weight loads.
-    ST sc[R][2];
+    // 2. The piece's group scales of every tile (this lane's row j), then
+    // the first weight loads.
+    ST sc[R][GW];
 #pragma unroll
     for (int i = 0; i < R; ++i)
 #pragma unroll
-        for (int gs = 0; gs < 2; ++gs)
+        for (int gs = 0; gs < GW; ++gs)
             sc[i][gs] = reinterpret_cast<const ST *>(
-                a.scales)[(size_t(tile_of(i)) * G + 2 * part + gs) * 16 + j];
+                a.scales)[(size_t(tile_of(i)) * G + GW * part + gs) * 16 + j];
     __builtin_amdgcn_sched_barrier(0);
     v4u w[NL];
     auto issue = [&](auto n_tag) {
         constexpr int n = decltype(n_tag)::value;
         const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
-                         (size_t(tile_of(n / L)) * (P * L) + part * L + n % L) * 64 + lane;
+                         (size_t(tile_of(n / L)) * (P * LS) + part * L + n % L) * 64 + lane;
         w[n] = __builtin_nontemporal_load(src);
     };
     unroll_groups<AH>(issue);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. Digits, group factors and corrections of the slice.
+    // 3. Digits, group factors and corrections of the piece.
     Blk blk[NB];
 #pragma unroll
     for (int bi = 0; bi < NB; ++bi)
@@ -2745,12 +2752,12 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
         for (int f = 0; f < NFL; ++f)
             reg_digits(rx[f][bi], blk[bi], f);
 
-    // 4. The tiles: products of the slice per group, then the combine.
+    // 4. The tiles: products of the piece per group, then the combine.
     unroll_groups<R>([&](auto i_tag) {
         constexpr int i = decltype(i_tag)::value;
-        v4i acc[2][NFL];
+        v4i acc[GW][NFL];
 #pragma unroll
-        for (int gs = 0; gs < 2; ++gs)
+        for (int gs = 0; gs < GW; ++gs)
 #pragma unroll
             for (int f = 0; f < NFL; ++f)
                 acc[gs][f] = v4i{0, 0, 0, 0};
@@ -2783,9 +2790,9 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
             // Each group's product is rounded before the add (no fused
             // multiply-add), as the one-row kernel's cross-lane sum.
 #pragma clang fp contract(off)
-            float g[2];
+            float g[GW];
 #pragma unroll
-            for (int gs = 0; gs < 2; ++gs) {
+            for (int gs = 0; gs < GW; ++gs) {
                 // Rows 4q + r: digit r of batch 4f + q.
                 const v4i d = acc[gs][f];
                 const int2 cv = blk[gs * 2 / LB].cv[gs % (LB / 2)][f];
@@ -2796,19 +2803,24 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                 const float gsum = float(hi) * 65536.0f + float(lo);
                 g[gs] = gsum * (to_f32<HALF>(sc[i][gs]) * xf);
             }
-            partial[(((tslot + TS * i) * P + part) * MB + 4 * (fbase + f) + q) * 16 + j] =
-                g[0] + g[1];
+            partial[(((tslot + TS * i) * PW + part) * MB + 4 * (fbase + f) + q) * 16 + j] =
+                GW == 2 ? g[0] + g[GW - 1] : g[0];
         }
     });
 
-    // 5. The slices of each (tile, batch row), added in order.
+    // 5. The slices of each (tile, batch row), added in order (each slice
+    // the sum of its pieces).
     __syncthreads();
     for (uint32_t v = threadIdx.x; v < uint32_t(TS * R * MB * 16); v += blockDim.x) {
         const uint32_t tl = v / (MB * 16), bb = (v / 16) % MB, r = v % 16;
-        float sum = partial[((tl * P) * MB + bb) * 16 + r];
+        auto slice = [&](int pp) {
+            const float *at = partial + ((tl * PW + HS * pp) * MB + bb) * 16 + r;
+            return HS == 2 ? at[0] + at[MB * 16] : at[0];
+        };
+        float sum = slice(0);
 #pragma unroll
         for (int pp = 1; pp < P; ++pp)
-            sum += partial[((tl * P + pp) * MB + bb) * 16 + r];
+            sum += slice(pp);
         const uint32_t t = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
         const uint32_t row = t * 16 + r;
         if (bb < a.m && t < a.n_tiles && row < a.n)
@@ -3575,9 +3587,10 @@ unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, 
 // telescoping), repeated by every wave of a slice, cost more than it saved
 // (65536 x 2048, B = 2 / 4 / 8: R = 8 8.9 / 9.3 / 14.2 us against 8.1 / 8.9
 // / 14.3).
-// Below the head size, five to eight rows: each slice's two fragments on
-// two waves (wide_rows_kernel FS = 2) when the one-wave launch holds at most
-// two waves per SIMD (tiles x slices <= 2048).  Measured at B = 8 (us per
+// Below the head size, ternary at five to eight rows: each slice's two
+// fragments on two waves (wide_rows_kernel FS = 2) when the one-wave launch
+// holds at most two waves per SIMD (tiles x slices <= 2048).  (INT8 takes
+// the 128-k pieces instead.)  Measured at B = 8 (us per
 // launch, A/B on one device): INT8 1024 x 1024 3.9 -> 3.4-3.7, ternary 4608
 // x 1024 5.4-5.5 -> 5.2-5.3, ternary 2048 x 2048 5.5 -> 5.4, INT8 2048 x
 // 2048 5.0-5.2 -> 5.0-5.1 (B = 5 5.0 -> 4.7); at four waves per SIMD the
@@ -3596,6 +3609,17 @@ void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
     // / 6.22 / 8.16 -> 5.05 / 5.14 / 7.12 (1024 x 1024: 3.25 / 3.22 / 3.94 ->
     // 3.51 / 3.46 / 3.70).
     if (args.n_tiles < kHeadTiles) {
+        if constexpr (F == Format::Int8) {
+            // Two waves per slice, one 128-k piece each.  Measured at B = 2
+            // / 4 / 8 (us per launch, A/B on one device): 2048 x 2048 3.84
+            // / 3.96 / 4.84 -> 3.62 / 3.53 / 4.31, 4608 x 1024 - / 3.78 /
+            // 4.41 -> - / 3.48 / 4.15, 8192 x 2048 5.1 / 5.1 / 7.27 -> 5.1
+            // / 5.1 / 6.64, 1024 x 1024 the same; B = 5 at 2048 x 2048
+            // 4.81 -> 4.27-4.48.
+            wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 1, 2>
+                <<<args.n_tiles, 128 * P, 0, stream>>>(args);
+            return;
+        }
         if constexpr (NF == 2) {
             if (args.n_tiles * uint32_t(P) <= kWideRowsSplitWaves) {
                 wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 2>
