@@ -33,7 +33,8 @@
 // tiles' byte order) or k = 32h + 8q + 0..7 (NF4: its 32-wide kstep).
 //
 // Tiling.  A 256-lane block (4 waves) computes a 128 (m) x 128 (n) output
-// tile, split over S weight streams of 128 / S columns each.  The waves lie
+// tile (64 x 128 where 128-row tiles would need a K split; its waves lie
+// along n), split over S weight streams of 128 / S columns each.  The waves lie
 // along n: each owns all 128 rows x 32 columns (8 x 2 MFMA tiles), so every
 // weight tile is decoded by one wave of the block; exact ternary keeps 2 x 2
 // waves of 64 x 64 (4 x 4 MFMA tiles), which reuse each activation fragment
@@ -238,17 +239,18 @@ __device__ __forceinline__ v8h decode_ternary(unsigned w, int h)
     return out;
 }
 
-template <Format F, int S, Epilogue E, bool HALF, bool LO>
+template <Format F, int S, Epilogue E, bool HALF, bool LO, int BM>
 __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
 {
+    static_assert(BM == kBM || BM == kBM / 2, "128- or 64-row block tiles");
     constexpr int P = F == Format::Nf4 ? 2 : 1;  // weight level planes
     constexpr int PA = LO ? 2 : 1;               // activation planes (hi, lo)
     // Waves along n (M = 2048 x 8192 x 2048 against 2 x 2: NF4 exact 218 ->
     // 206 us, INT8 exact 172 -> 165, single-half 3-9 % faster; exact ternary
-    // 158 -> 159-160, so it keeps 2 x 2).
-    constexpr int WN = LO && F == Format::Ternary ? 2 : 4;
+    // 158 -> 159-160, so it keeps 2 x 2 at 128 rows).
+    constexpr int WN = LO && F == Format::Ternary && BM == kBM ? 2 : 4;
     constexpr int WM = 4 / WN;
-    constexpr int TI = kBM / 16 / WM;            // 16-row MFMA tiles per wave
+    constexpr int TI = BM / 16 / WM;             // 16-row MFMA tiles per wave
     constexpr int TJ = kBN / 16 / WN;            // 16-column MFMA tiles per wave
     constexpr int TJS = TJ / S;                  // column tiles per stream per wave
     constexpr int BNS = kBN / S;                 // block columns per stream
@@ -258,7 +260,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     // as fast or faster without it (INT8 exact 168.6 against 165.3 us, NF4
     // single-half 150.7 against 144.1).
     constexpr bool PRIO = LO && F == Format::Ternary;
-    __shared__ _Float16 As[2][PA][kBM][kRow];  // [stage][hi, lo][row][k]
+    __shared__ _Float16 As[2][PA][BM][kRow];   // [stage][hi, lo][row][k]
     __shared__ uint2 lut[F == Format::Nf4 ? 256 : 1];
 
     if constexpr (F == Format::Nf4) {
@@ -280,7 +282,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     if (blocks % 8 == 0)
         block = (blockIdx.x % 8) * (blocks / 8) + blockIdx.x / 8;
     const uint32_t chunk = block / g.tiles, tile = block % g.tiles;
-    const uint32_t m0 = (tile / g.tiles_n) * kBM, n0 = (tile % g.tiles_n) * BNS;
+    const uint32_t m0 = (tile / g.tiles_n) * BM, n0 = (tile % g.tiles_n) * BNS;
     const int tid = threadIdx.x, lane = tid & 63;
     // Wave-uniform, so the tile addresses live in scalar registers.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -289,28 +291,30 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     const uint32_t chunk_stages = g.k / kBK / g.chunks;
     const uint32_t s_begin = chunk * chunk_stages, s_end = s_begin + chunk_stages;
 
-    // A staging: thread -> (row, 32-wide k half) of both activation halves.
-    // Rows past m load row 0 (their outputs are never stored), so every
-    // load is unconditional and nothing waits to clear a destination.
-    const uint32_t a_row = tid >> 1, a_k = (tid & 1) * 32;
+    // A staging: thread -> (row, k run of kBK / TPR) of both activation
+    // halves.  Rows past m load row 0 (their outputs are never stored), so
+    // every load is unconditional and nothing waits to clear a destination.
+    constexpr int TPR = kThreads / BM;            // threads per staged row
+    constexpr int AV = kBK / TPR / 8;             // 8-half vectors per thread
+    const uint32_t a_row = tid / TPR, a_k = (tid % TPR) * (kBK / TPR);
     const bool a_live = m0 + a_row < g.m;
     const _Float16 *a_src[2] = {g.xh + size_t(a_live ? m0 + a_row : 0) * g.k + a_k,
                                 g.xl + size_t(a_live ? m0 + a_row : 0) * g.k + a_k};
     struct ARaw {
-        v8h v[PA][4];
+        v8h v[PA][AV];
     };
     auto fetch_a = [&](uint32_t s, ARaw &r) {
 #pragma unroll
         for (int p = 0; p < PA; ++p)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < AV; ++u)
                 r.v[p][u] = *reinterpret_cast<const v8h *>(a_src[p] + s * kBK + 8 * u);
     };
     auto store_a = [&](int buf, const ARaw &r) {
 #pragma unroll
         for (int p = 0; p < PA; ++p)
 #pragma unroll
-            for (int u = 0; u < 4; ++u)
+            for (int u = 0; u < AV; ++u)
                 *reinterpret_cast<v8h *>(&As[buf][p][a_row][a_k + 8 * u]) = r.v[p][u];
     };
 
@@ -415,7 +419,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
                 __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int i = 0; i < TI; ++i) {
-                const int row = wm * (kBM / WM) + i * 16 + li;
+                const int row = wm * (BM / WM) + i * 16 + li;
                 const v8h ah = *reinterpret_cast<const v8h *>(&As[buf][0][row][koff]);
                 const v8h al = *reinterpret_cast<const v8h *>(&As[buf][PA - 1][row][koff]);
 #pragma unroll
@@ -477,14 +481,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm_mfma_kernel(GemmArgs g)
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t mm = m0 + wm * (kBM / WM) + i * 16 + lq * 4 + r;
+            const uint32_t mm = m0 + wm * (BM / WM) + i * 16 + lq * 4 + r;
             rowf[i][r] = g.factor[mm < g.m ? mm : 0];
         }
 #pragma unroll
     for (int i = 0; i < TI; ++i)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const uint32_t mm = m0 + wm * (kBM / WM) + i * 16 + lq * 4 + r;
+            const uint32_t mm = m0 + wm * (BM / WM) + i * 16 + lq * 4 + r;
             if (mm >= g.m)
                 continue;
 #pragma unroll
@@ -544,18 +548,27 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(float *__restrict__ 
     }
 }
 
-template <Format F, int S, Epilogue E>
-void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half, bool lo)
+template <Format F, int S, Epilogue E, int BM>
+void launch_rows(hipStream_t stream, const GemmArgs &args, bool half, bool lo)
 {
     const unsigned grid = args.tiles * args.chunks;
     if (half && lo)
-        gemm_mfma_kernel<F, S, E, true, true><<<grid, kThreads, 0, stream>>>(args);
+        gemm_mfma_kernel<F, S, E, true, true, BM><<<grid, kThreads, 0, stream>>>(args);
     else if (lo)
-        gemm_mfma_kernel<F, S, E, false, true><<<grid, kThreads, 0, stream>>>(args);
+        gemm_mfma_kernel<F, S, E, false, true, BM><<<grid, kThreads, 0, stream>>>(args);
     else if (half)
-        gemm_mfma_kernel<F, S, E, true, false><<<grid, kThreads, 0, stream>>>(args);
+        gemm_mfma_kernel<F, S, E, true, false, BM><<<grid, kThreads, 0, stream>>>(args);
     else
-        gemm_mfma_kernel<F, S, E, false, false><<<grid, kThreads, 0, stream>>>(args);
+        gemm_mfma_kernel<F, S, E, false, false, BM><<<grid, kThreads, 0, stream>>>(args);
+}
+
+template <Format F, int S, Epilogue E>
+void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half, bool lo, uint32_t bm)
+{
+    if (bm == kBM)
+        launch_rows<F, S, E, kBM>(stream, args, half, lo);
+    else
+        launch_rows<F, S, E, kBM / 2>(stream, args, half, lo);
     if (args.chunks > 1) {
         const size_t plane = size_t(args.m) * args.n;
         const unsigned rgrid = unsigned(std::min<size_t>((plane + 255) / 256, 65536));
@@ -565,16 +578,17 @@ void launch_epilogue(hipStream_t stream, const GemmArgs &args, bool half, bool l
 }
 
 template <Format F>
-void launch_format(hipStream_t stream, const PackedCall &call, const GemmArgs &args, bool half)
+void launch_format(hipStream_t stream, const PackedCall &call, const GemmArgs &args, bool half,
+                   uint32_t bm)
 {
     const bool lo = !call.single_half;
     switch (call.epilogue) {
     case Epilogue::Single:
-        return launch_epilogue<F, 1, Epilogue::Single>(stream, args, half, lo);
+        return launch_epilogue<F, 1, Epilogue::Single>(stream, args, half, lo, bm);
     case Epilogue::Pair:
-        return launch_epilogue<F, 2, Epilogue::Pair>(stream, args, half, lo);
+        return launch_epilogue<F, 2, Epilogue::Pair>(stream, args, half, lo, bm);
     case Epilogue::SwigluPair:
-        return launch_epilogue<F, 2, Epilogue::SwigluPair>(stream, args, half, lo);
+        return launch_epilogue<F, 2, Epilogue::SwigluPair>(stream, args, half, lo, bm);
     }
 }
 
@@ -594,11 +608,25 @@ uint32_t split_chunks(uint32_t tiles, uint32_t groups)
     return chunks;
 }
 
-uint32_t tiles_of(const PackedCall &call, uint32_t *tiles_n)
+uint32_t tiles_of(const PackedCall &call, uint32_t *tiles_n, uint32_t bm)
 {
     const int S = call.epilogue == Epilogue::Single ? 1 : 2;
     *tiles_n = (call.n + kBN / S - 1) / (kBN / S);
-    return *tiles_n * ((call.m + kBM - 1) / kBM);
+    return *tiles_n * ((call.m + bm - 1) / bm);
+}
+
+// Rows per block tile: 64 where 128-row tiles would not fill the grid
+// without a K split (fewer than kHalfRowsBelow tiles), so the product
+// needs fewer K chunks (none at M = 512 x 8192) and their reduction.
+// Measured (us per call, A/B on one device): M = 512 x 8192 x 2048 ternary
+// 58.4 -> 50.0, INT8 61.3 -> 50.0-50.9, NF4 70-73 -> 62.6-63.5; M = 128
+// 35.6 -> 30.1; M = 256 41.8 -> 39.0; M = 512 x 2048 x 8192 (still split)
+// 2-7 % faster.
+constexpr uint32_t kHalfRowsBelow = 512;
+uint32_t block_rows(const PackedCall &call)
+{
+    uint32_t tiles_n;
+    return tiles_of(call, &tiles_n, kBM) < kHalfRowsBelow ? kBM / 2 : kBM;
 }
 
 }  // namespace
@@ -606,7 +634,8 @@ uint32_t tiles_of(const PackedCall &call, uint32_t *tiles_n)
 size_t gemm_mfma_scratch_bytes(const PackedCall &call)
 {
     uint32_t tiles_n;
-    const uint32_t chunks = split_chunks(tiles_of(call, &tiles_n), call.k / 128);
+    const uint32_t chunks =
+        split_chunks(tiles_of(call, &tiles_n, block_rows(call)), call.k / 128);
     const int S = call.epilogue == Epilogue::Single ? 1 : 2;
     const size_t partial = chunks > 1 ? size_t(chunks) * S * call.m * call.n * sizeof(float) : 0;
     return size_t(call.m) * call.k * 2 * sizeof(_Float16) + size_t(call.m) * sizeof(float) +
@@ -644,15 +673,16 @@ void launch_gemm_mfma(hipStream_t stream, const PackedCall &call, void *scratch)
     args.n_tiles = (call.n + 63) / 64 * 4;
     args.tile_vecs = k_pad / chunk_k * 64;
     args.groups_pad = k_pad / 128;
-    args.tiles = tiles_of(call, &args.tiles_n);
+    const uint32_t bm = block_rows(call);
+    args.tiles = tiles_of(call, &args.tiles_n, bm);
     args.chunks = split_chunks(args.tiles, groups);
     args.partial = factor + call.m;
     const int streams = call.epilogue == Epilogue::Single ? 1 : 2;
     const bool half = call.a.tiled_half && (streams == 1 || call.b.tiled_half);
     switch (call.format) {
-    case Format::Ternary: launch_format<Format::Ternary>(stream, call, args, half); break;
-    case Format::Nf4: launch_format<Format::Nf4>(stream, call, args, half); break;
-    case Format::Int8: launch_format<Format::Int8>(stream, call, args, half); break;
+    case Format::Ternary: launch_format<Format::Ternary>(stream, call, args, half, bm); break;
+    case Format::Nf4: launch_format<Format::Nf4>(stream, call, args, half, bm); break;
+    case Format::Int8: launch_format<Format::Int8>(stream, call, args, half, bm); break;
     }
 }
 
