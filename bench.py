@@ -610,7 +610,7 @@ def profile_only(backend, args) -> int:
     if args.profile in ("gemm", "gemm-single"):
         # gemm-single: the opt-in single-half activations.
         backend.set_gemm_activations(1 if args.profile == "gemm-single" else 0)
-        n, k, m = 8192, 2048, 2048
+        n, k, m = 8192, 2048, args.gemm_m
         codes, scales16 = convert.packed_weights(n, k, args.gemm_format, 0x5EED0101)
         scales = convert.f16_to_f32(scales16)
         cb = backend.upload_u8_classified(codes.shape, codes, WEIGHT)
@@ -728,9 +728,11 @@ def main() -> int:
                                           "product"],
                     help="run only the dominant operation (or the 65536x2048 head of "
                          "another format, a 256 MiB device copy, the counter calibration, "
-                         "the streaming-read ceiling of the three heads' bytes, an LFM2 decode, the M=2048 x 8192x2048 prefill GEMM, "
+                         "the streaming-read ceiling of the three heads' bytes, an LFM2 decode, the M=2048 (or --gemm-m) x 8192x2048 prefill GEMM, "
                          "gemm-single with single-half activations, or the --product "
                          "decode GEMV) for rocprofv3, and print no JSON line")
+    ap.add_argument("--gemm-m", type=int, choices=[512, 2048], default=2048,
+                    help="activation rows of --profile gemm / gemm-single")
     ap.add_argument("--gemm-format", choices=["ternary", "int8", "nf4"], default="ternary",
                     help="weight format of --profile gemm / gemm-single")
     ap.add_argument("--product", default="ternary,2048,8192,1",
