@@ -1214,6 +1214,11 @@ constexpr int kStreamWaves = 16;
 // 8.8 / 8.1 / 8.2 with one to four; NF4 (one load = 128 k) 28.4 us with all
 // sixteen, 24.4 with eight, 21.5 / 20.0 / 21.5 / 21.9 with one to four.
 constexpr int kStreamTernaryAhead = 3;
+// The same for a wave of the one- or two-row kernel that has no prologue
+// pass (it waits at the barrier while the others form the digits): 65536 x
+// 2048, one row, 7.34-7.43 us with three, 7.21-7.28 with five or six,
+// 7.70-7.82 with eight (interleaved runs on one device).
+constexpr int kStreamTernaryIdleAhead = 6;
 constexpr int kStreamNf4Ahead = 2;
 // Widest grids only: below this many tiles the K-split plans keep more
 // waves busy.
@@ -1544,146 +1549,157 @@ __global__ __launch_bounds__(64 * W) void stream_ternary_rows_kernel(StreamArgs 
         xv[pi] = *reinterpret_cast<const v4f *>(a.x + size_t(pb) * a.k + (kx < a.k ? kx : 0));
     }
     __builtin_amdgcn_sched_barrier(0);
-    // 3. The first weight loads of the tile.
-    v4u w[KL];
-    const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * KL * 64 + lane;
-    constexpr int AHEAD = KL < kStreamTernaryAhead ? KL : kStreamTernaryAhead;
+    // Steps 3-5 with AHEAD_W weight loads in flight: a wave with a prologue
+    // pass keeps kStreamTernaryAhead, a wave without one (it only waits at
+    // the barrier) kStreamTernaryIdleAhead.  The choice is wave-uniform and
+    // every wave reaches the one barrier of either copy.
+    auto rest = [&](auto ahead_tag) {
+        constexpr int AHEAD_W = decltype(ahead_tag)::value;
+        // 3. The first weight loads of the tile.
+        v4u w[KL];
+        const v4u *wp = reinterpret_cast<const v4u *>(a.tiles) + size_t(tile) * KL * 64 + lane;
+        constexpr int AHEAD = KL < AHEAD_W ? KL : AHEAD_W;
 #pragma unroll
-    for (int l = 0; l < AHEAD; ++l)
-        w[l] = __builtin_nontemporal_load(&wp[l * 64]);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // 4. The prologue passes (the register prologue's arithmetic, per slot),
-    // then the scale block, into LDS.
-#pragma unroll
-    for (int pi = 0; pi < PER; ++pi) {
-        const uint32_t pass = wave + W * pi;
-        if (pass >= uint32_t(PASSES))
-            continue;
-        const uint32_t ps = pass * PASS_KS + (MB == 1 ? slot : slot & 1);
-        const bool inb = 64 * ps + 16 * q + 4 * p < a.k;
-        float v[4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            v[t] = inb ? xv[pi][t] : 0.0f;
-        unsigned mb = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-            mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
-        mb = max(mb, quad_xor1(mb));
-        mb = max(mb, quad_xor2(mb));
-        mb = max(mb, half_mirror(mb));
-        mb = max_xor16(mb);
-        mb = max_xor32(mb);
-        const bool bad = mb >= 0x7F800000u;
-        int e = 0;
-        if (!bad && mb)
-            frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
-        const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
-        long long corr = 0;
-        unsigned vp[4];
-        int u_prev = 0;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            int val = bad ? 0 : int(rintf(ldexpf(v[t], 30 - e)));
-            // Field t of the nested masks (see the operand-field note).
-            const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
-            val = t == 0 ? u : u - u_prev;
-            u_prev = u;
-            corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
-                          : -(static_cast<long long>(u) << 6);
-            vp[t] = unsigned(val + 0x808080);
-        }
-        unsigned d[4], wd[4];
-        byte_transpose<true>(vp, d);
-        quad_transpose(d, p);
-        byte_transpose<false>(d, wd);
-        const unsigned flip = p ? 0x80808080u : 0u;
-        frag[(ps * 4 + q) * RB + 4 * pb + p] =
-            v4i{int(wd[0] ^ flip), int(wd[1] ^ flip), int(wd[2] ^ flip), int(wd[3] ^ flip)};
-        corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
-                (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
-        corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
-                (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
-        corr += static_cast<long long>(half_mirror(unsigned(corr))) |
-                (static_cast<long long>(half_mirror(unsigned(corr >> 32))) << 32);
-        corr = sum_xor16(corr);
-        corr = sum_xor32(corr);
-        // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
-        const long long lo = ((corr + 32768) & 65535) - 32768;
-        const int hi = int((corr - lo) >> 16);
-        if (lane < 16 && p == 0 && (slot & 1) == 0)
-            rec[pb * G + ps / 2] = StreamRecord{int2{hi, int(lo)}, factor, 0.0f};
-    }
-    for (uint32_t i = threadIdx.x; i < uint32_t(KS * 4 * RB); i += 64 * W)
-        zeros[i] = v4i{0, 0, 0, 0};
-    if (lane < uint32_t(SLANES))
-        scale_lds[wave * SLANES + lane] = sv;
-    __syncthreads();
-
-    // 5. The tile's products.  Lane (q, i) supplies A row i: row block
-    // i / RB takes the groups g with g % IL == i / RB.
-    const uint32_t phase = j / RB;
-    const ST *scl = reinterpret_cast<const ST *>(scale_lds + wave * SLANES) + j;
-    // Per phase, the lane's fragment base: its own compact rows for its row
-    // block's phase, the zero region (same offsets) for the others.  Every
-    // read is then one unconditional 16-byte LDS load.
-    const v4i *abase[IL];
-#pragma unroll
-    for (int ph = 0; ph < IL; ++ph)
-        abase[ph] = (phase == uint32_t(ph) ? frag : zeros) + q * RB + j % RB;
-    v4i cur[2], next[2];
-    auto read_group = [&](auto g_tag, v4i (&av)[2]) {
-        constexpr int g = decltype(g_tag)::value;
-        av[0] = abase[g % IL][(2 * g) * 4 * RB];
-        av[1] = abase[g % IL][(2 * g + 1) * 4 * RB];
-    };
-    // Lane block q' of each accumulation holds group base + q' / MB, batch
-    // row q' % MB.
-    const uint32_t my_group = q / MB, my_batch = q % MB;
-    float accf = 0.0f;
-    v4i acci = v4i{0, 0, 0, 0};
-    read_group(std::integral_constant<int, 0>{}, cur);
-    unroll_groups<G>([&](auto g_tag) {
-        constexpr int g = decltype(g_tag)::value;
-        if constexpr (g % 2 == 0 && g / 2 + AHEAD < KL)
-            w[g / 2 + AHEAD] = __builtin_nontemporal_load(&wp[(g / 2 + AHEAD) * 64]);
-        if constexpr (g + 1 < G)
-            read_group(std::integral_constant<int, g + 1>{}, next);
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-            const int s = 2 * g + kk;
-            const unsigned word = w[s / 4][s % 4];
-            const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
-                               int(word & 0xC0C0C0C0u)};
-            acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[kk], bw, acci, 0, 0, 0);
-        }
-        cur[0] = next[0];
-        cur[1] = next[1];
-        if constexpr (g % IL == IL - 1) {
-            const uint32_t gg = uint32_t(g - (IL - 1)) + my_group;
-            const StreamRecord r = rec[my_batch * G + gg];
-            const float scale = to_f32<HALF>(scl[gg * 16]);
-            // |d.x| < 2^21, so the pairs combine exactly in int32.
-            const int hi = (acci.x << 8) + acci.y - r.corr.x;
-            const int lo = (acci.z << 8) + acci.w - r.corr.y;
-            const float gsum = float(hi) * 65536.0f + float(lo);
-            accf += gsum * (scale * r.xf);
-            // Keep the accumulation here: otherwise it sinks into the
-            // guarded store below and every group's MFMA results stay live.
-            asm volatile("" : "+v"(accf));
-            acci = v4i{0, 0, 0, 0};
-        }
+        for (int l = 0; l < AHEAD; ++l)
+            w[l] = __builtin_nontemporal_load(&wp[l * 64]);
         __builtin_amdgcn_sched_barrier(0);
-    });
-    // The IL partial sums of each batch row: lane blocks q' with equal
-    // q' % MB.
-    if constexpr (MB == 1)
-        accf = sum_xor16(accf);
-    accf = sum_xor32(accf);
-    const uint32_t row = tile_id * 16 + j;
-    if (q < uint32_t(MB) && tile_id < a.n_tiles && q < a.m && row < a.n)
-        a.out[size_t(q) * a.n + row] = accf;
+
+        // 4. The prologue passes (the register prologue's arithmetic, per slot),
+        // then the scale block, into LDS.
+#pragma unroll
+        for (int pi = 0; pi < PER; ++pi) {
+            const uint32_t pass = wave + W * pi;
+            if (pass >= uint32_t(PASSES))
+                continue;
+            const uint32_t ps = pass * PASS_KS + (MB == 1 ? slot : slot & 1);
+            const bool inb = 64 * ps + 16 * q + 4 * p < a.k;
+            float v[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                v[t] = inb ? xv[pi][t] : 0.0f;
+            unsigned mb = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                mb = max(mb, __float_as_uint(v[t]) & 0x7FFFFFFFu);
+            mb = max(mb, quad_xor1(mb));
+            mb = max(mb, quad_xor2(mb));
+            mb = max(mb, half_mirror(mb));
+            mb = max_xor16(mb);
+            mb = max_xor32(mb);
+            const bool bad = mb >= 0x7F800000u;
+            int e = 0;
+            if (!bad && mb)
+                frexpf(__uint_as_float(mb), &e);  // |x| < 2^e
+            const float factor = bad ? __builtin_nanf("") : ldexpf(1.0f, e - 30);
+            long long corr = 0;
+            unsigned vp[4];
+            int u_prev = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                int val = bad ? 0 : int(rintf(ldexpf(v[t], 30 - e)));
+                // Field t of the nested masks (see the operand-field note).
+                const int u = t == 0 ? val : (val + (1 << (2 * t - 1))) >> (2 * t);
+                val = t == 0 ? u : u - u_prev;
+                u_prev = u;
+                corr += t < 3 ? (static_cast<long long>(u) << (2 * t))
+                              : -(static_cast<long long>(u) << 6);
+                vp[t] = unsigned(val + 0x808080);
+            }
+            unsigned d[4], wd[4];
+            byte_transpose<true>(vp, d);
+            quad_transpose(d, p);
+            byte_transpose<false>(d, wd);
+            const unsigned flip = p ? 0x80808080u : 0u;
+            frag[(ps * 4 + q) * RB + 4 * pb + p] =
+                v4i{int(wd[0] ^ flip), int(wd[1] ^ flip), int(wd[2] ^ flip), int(wd[3] ^ flip)};
+            corr += static_cast<long long>(quad_xor1(unsigned(corr))) |
+                    (static_cast<long long>(quad_xor1(unsigned(corr >> 32))) << 32);
+            corr += static_cast<long long>(quad_xor2(unsigned(corr))) |
+                    (static_cast<long long>(quad_xor2(unsigned(corr >> 32))) << 32);
+            corr += static_cast<long long>(half_mirror(unsigned(corr))) |
+                    (static_cast<long long>(half_mirror(unsigned(corr >> 32))) << 32);
+            corr = sum_xor16(corr);
+            corr = sum_xor32(corr);
+            // Split as hi * 2^16 + lo to match the epilogue's digit pairs.
+            const long long lo = ((corr + 32768) & 65535) - 32768;
+            const int hi = int((corr - lo) >> 16);
+            if (lane < 16 && p == 0 && (slot & 1) == 0)
+                rec[pb * G + ps / 2] = StreamRecord{int2{hi, int(lo)}, factor, 0.0f};
+        }
+        for (uint32_t i = threadIdx.x; i < uint32_t(KS * 4 * RB); i += 64 * W)
+            zeros[i] = v4i{0, 0, 0, 0};
+        if (lane < uint32_t(SLANES))
+            scale_lds[wave * SLANES + lane] = sv;
+        __syncthreads();
+
+        // 5. The tile's products.  Lane (q, i) supplies A row i: row block
+        // i / RB takes the groups g with g % IL == i / RB.
+        const uint32_t phase = j / RB;
+        const ST *scl = reinterpret_cast<const ST *>(scale_lds + wave * SLANES) + j;
+        // Per phase, the lane's fragment base: its own compact rows for its row
+        // block's phase, the zero region (same offsets) for the others.  Every
+        // read is then one unconditional 16-byte LDS load.
+        const v4i *abase[IL];
+#pragma unroll
+        for (int ph = 0; ph < IL; ++ph)
+            abase[ph] = (phase == uint32_t(ph) ? frag : zeros) + q * RB + j % RB;
+        v4i cur[2], next[2];
+        auto read_group = [&](auto g_tag, v4i (&av)[2]) {
+            constexpr int g = decltype(g_tag)::value;
+            av[0] = abase[g % IL][(2 * g) * 4 * RB];
+            av[1] = abase[g % IL][(2 * g + 1) * 4 * RB];
+        };
+        // Lane block q' of each accumulation holds group base + q' / MB, batch
+        // row q' % MB.
+        const uint32_t my_group = q / MB, my_batch = q % MB;
+        float accf = 0.0f;
+        v4i acci = v4i{0, 0, 0, 0};
+        read_group(std::integral_constant<int, 0>{}, cur);
+        unroll_groups<G>([&](auto g_tag) {
+            constexpr int g = decltype(g_tag)::value;
+            if constexpr (g % 2 == 0 && g / 2 + AHEAD < KL)
+                w[g / 2 + AHEAD] = __builtin_nontemporal_load(&wp[(g / 2 + AHEAD) * 64]);
+            if constexpr (g + 1 < G)
+                read_group(std::integral_constant<int, g + 1>{}, next);
+#pragma unroll
+            for (int kk = 0; kk < 2; ++kk) {
+                const int s = 2 * g + kk;
+                const unsigned word = w[s / 4][s % 4];
+                const v4i bw = v4i{int(word), int(word & 0xFCFCFCFCu), int(word & 0xF0F0F0F0u),
+                                   int(word & 0xC0C0C0C0u)};
+                acci = __builtin_amdgcn_mfma_i32_16x16x64_i8(cur[kk], bw, acci, 0, 0, 0);
+            }
+            cur[0] = next[0];
+            cur[1] = next[1];
+            if constexpr (g % IL == IL - 1) {
+                const uint32_t gg = uint32_t(g - (IL - 1)) + my_group;
+                const StreamRecord r = rec[my_batch * G + gg];
+                const float scale = to_f32<HALF>(scl[gg * 16]);
+                // |d.x| < 2^21, so the pairs combine exactly in int32.
+                const int hi = (acci.x << 8) + acci.y - r.corr.x;
+                const int lo = (acci.z << 8) + acci.w - r.corr.y;
+                const float gsum = float(hi) * 65536.0f + float(lo);
+                accf += gsum * (scale * r.xf);
+                // Keep the accumulation here: otherwise it sinks into the
+                // guarded store below and every group's MFMA results stay live.
+                asm volatile("" : "+v"(accf));
+                acci = v4i{0, 0, 0, 0};
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        });
+        // The IL partial sums of each batch row: lane blocks q' with equal
+        // q' % MB.
+        if constexpr (MB == 1)
+            accf = sum_xor16(accf);
+        accf = sum_xor32(accf);
+        const uint32_t row = tile_id * 16 + j;
+        if (q < uint32_t(MB) && tile_id < a.n_tiles && q < a.m && row < a.n)
+            a.out[size_t(q) * a.n + row] = accf;
+    };
+    if (wave < uint32_t(PASSES))
+        rest(std::integral_constant<int, kStreamTernaryAhead>{});
+    else
+        rest(std::integral_constant<int, kStreamTernaryIdleAhead>{});
 }
 
 // ---------------------------------------------------------------------------
