@@ -624,10 +624,12 @@ __device__ __forceinline__ void reduce_and_store(uint32_t m, const Target &tg,
 // buffered in registers: the next block's weights and activation fragments
 // are in flight while the current one is computed.
 // ---------------------------------------------------------------------------
-template <Format F, int T, int S, int NF, bool HALF>
+template <Format F, int T, int S, int NF, bool HALF, int LBO = Geo<F>::lb>
 struct I8Block {
-    static constexpr int LB = Geo<F>::lb;
-    static constexpr int LOADS = LB / Geo<F>::kpl;
+    // LBO: ksteps per loop block (Geo<F>::lb; 2 for the ternary 128-k
+    // pieces of wide_rows_kernel, whose own weight registers leave w unused).
+    static constexpr int LB = LBO;
+    static constexpr int LOADS = LB / Geo<F>::kpl > 0 ? LB / Geo<F>::kpl : 1;
     static constexpr int GPB = LB / 2;  // 128-groups per loop block
     using ST = typename ScaleT<HALF>::type;
     v4u w[S][T][LOADS];
@@ -867,11 +869,11 @@ __device__ __forceinline__ void reg_load_issued(RegX<LB> &rx, const float *xrow,
 }
 
 // Fragment f (batch rows 4f..4f+3) of a loop block from this lane's values.
-template <Format F, int T, int S, int NF, bool HALF>
-__device__ __forceinline__ void reg_digits(const RegX<Geo<F>::lb> &rx,
-                                           I8Block<F, T, S, NF, HALF> &blk, int f)
+template <Format F, int T, int S, int NF, bool HALF, int LBO>
+__device__ __forceinline__ void reg_digits(const RegX<LBO> &rx,
+                                           I8Block<F, T, S, NF, HALF, LBO> &blk, int f)
 {
-    using B = I8Block<F, T, S, NF, HALF>;
+    using B = I8Block<F, T, S, NF, HALF, LBO>;
     const uint32_t lane = threadIdx.x & 63;
     const uint32_t p = lane & 3, q = lane >> 4;
     const unsigned flip = p ? 0x80808080u : 0u;
@@ -2685,37 +2687,38 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 // accumulator.  Output lane block q holds batch 4f + q: the group sums,
 // scales and slice order are wide_row_kernel's, so each row's result is the
 // one-row kernel's bit for bit.  Rows at or beyond m read row 0 and are
-// zeroed.  FS = 2 splits a slice's two fragments over two waves (each forms
-// and multiplies one, both loading the slice's weights), halving the
-// digit prologue on each wave's path.  HS = 2 (INT8) splits each slice into
-// two 128-k pieces, one group each, on two waves (half the weight loads and
-// digits per wave, none duplicated); the block adds the two pieces of a
-// slice before adding the slices in order, the one-row kernel's sum.
-template <Format F, bool HALF, int P, int R, int NF, int W = 16, int FS = 1, int HS = 1>
+// zeroed.  HS = 2 splits each slice into two 128-k pieces, one group each,
+// on two waves (half the weight loads and digits per wave, none
+// duplicated; a ternary piece reads half of each 16-byte lane load); the
+// block adds the two pieces of a slice before adding the slices in order,
+// the one-row kernel's sum.
+template <Format F, bool HALF, int P, int R, int NF, int W = 16, int HS = 1>
 __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
 {
     static_assert(F != Format::Nf4, "integer formats");
-    static_assert(NF % FS == 0, "whole fragments per wave");
-    static_assert(HS == 1 || (HS == 2 && F == Format::Int8), "128-k pieces: INT8");
+    static_assert(HS == 1 || HS == 2, "whole or half slices");
     using ST = typename ScaleT<HALF>::type;
-    constexpr int NFL = NF / FS;                    // fragments this wave forms
-    using Blk = I8Block<F, 1, 1, NFL, HALF>;
+    constexpr int NFL = NF;                         // fragments this wave forms
+    // Ternary pieces read half of each 16-byte lane load (8 bytes: two
+    // ksteps, one 128-group).
+    constexpr bool HALFLOAD = F == Format::Ternary && HS == 2;
     constexpr int PW = P * HS;                      // slice pieces per tile
-    constexpr int TS = W / (PW * FS);               // tiles per round
+    constexpr int TS = W / PW;                      // tiles per round
     constexpr int LS = WideGeo<F>::loads;           // lane loads per (tile, slice)
-    constexpr int L = LS / HS;                      // ... per (tile, piece)
-    constexpr int KPL = WideGeo<F>::ksteps_per_load;
+    constexpr int L = HALFLOAD ? 1 : LS / HS;       // ... per (tile, piece)
+    constexpr int KPL = HALFLOAD ? 2 : WideGeo<F>::ksteps_per_load;
     constexpr int NL = R * L;                       // lane loads per wave
     constexpr int AH = NL < kWideAhead ? NL : kWideAhead;
     constexpr int G = 2 * P;                        // 128-groups per tile
     constexpr int GW = 2 / HS;                      // 128-groups per piece
-    constexpr int LB = Geo<F>::lb;                  // ksteps per digit block
-    constexpr int NB = 4 / LB / HS;                 // digit blocks per piece
+    constexpr int LB = Geo<F>::lb < 4 / HS ? Geo<F>::lb : 4 / HS;  // ksteps per digit block
+    constexpr int NB = 4 / HS / LB;                 // digit blocks per piece
+    using Blk = I8Block<F, 1, 1, NFL, HALF, LB>;
     constexpr int MB = 4 * NF;                      // batch rows held
     __shared__ float partial[TS * R * PW * MB * 16];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t part = wave % PW, fbase = NFL * ((wave / PW) % FS), tslot = wave / (PW * FS);
+    const uint32_t part = wave % PW, tslot = wave / PW;
     const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
     auto tile_of = [&](int i) {
         const uint32_t t = tile0 + uint32_t(TS * i);
@@ -2729,7 +2732,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     RegX<LB> rx[NFL][NB];
 #pragma unroll
     for (int f = 0; f < NFL; ++f) {
-        const uint32_t row = 4 * (fbase + f) + b;
+        const uint32_t row = 4 * f + b;
         const bool live = row < a.m;
         const float *xrow = a.x + size_t(live ? row : 0) * a.k + off;
 #pragma unroll
@@ -2753,9 +2756,19 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     v4u w[NL];
     auto issue = [&](auto n_tag) {
         constexpr int n = decltype(n_tag)::value;
-        const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
-                         (size_t(tile_of(n / L)) * (P * LS) + part * L + n % L) * 64 + lane;
-        w[n] = __builtin_nontemporal_load(src);
+        if constexpr (HALFLOAD) {
+            typedef unsigned v2u __attribute__((ext_vector_type(2)));
+            const v2u *src = reinterpret_cast<const v2u *>(
+                                 reinterpret_cast<const v4u *>(a.tiles) +
+                                 (size_t(tile_of(n)) * (P * LS) + (part / 2) * LS) * 64 + lane) +
+                             part % 2;
+            const v2u u = __builtin_nontemporal_load(src);
+            w[n] = v4u{u.x, u.y, 0u, 0u};
+        } else {
+            const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
+                             (size_t(tile_of(n / L)) * (P * LS) + part * L + n % L) * 64 + lane;
+            w[n] = __builtin_nontemporal_load(src);
+        }
     };
     unroll_groups<AH>(issue);
     __builtin_amdgcn_sched_barrier(0);
@@ -2819,7 +2832,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                 const float gsum = float(hi) * 65536.0f + float(lo);
                 g[gs] = gsum * (to_f32<HALF>(sc[i][gs]) * xf);
             }
-            partial[(((tslot + TS * i) * PW + part) * MB + 4 * (fbase + f) + q) * 16 + j] =
+            partial[(((tslot + TS * i) * PW + part) * MB + 4 * f + q) * 16 + j] =
                 GW == 2 ? g[0] + g[GW - 1] : g[0];
         }
     });
@@ -3603,15 +3616,6 @@ unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, 
 // telescoping), repeated by every wave of a slice, cost more than it saved
 // (65536 x 2048, B = 2 / 4 / 8: R = 8 8.9 / 9.3 / 14.2 us against 8.1 / 8.9
 // / 14.3).
-// Below the head size, ternary at five to eight rows: each slice's two
-// fragments on two waves (wide_rows_kernel FS = 2) when the one-wave launch
-// holds at most two waves per SIMD (tiles x slices <= 2048).  (INT8 takes
-// the 128-k pieces instead.)  Measured at B = 8 (us per
-// launch, A/B on one device): INT8 1024 x 1024 3.9 -> 3.4-3.7, ternary 4608
-// x 1024 5.4-5.5 -> 5.2-5.3, ternary 2048 x 2048 5.5 -> 5.4, INT8 2048 x
-// 2048 5.0-5.2 -> 5.0-5.1 (B = 5 5.0 -> 4.7); at four waves per SIMD the
-// duplicated weight loads cost more (INT8 8192 x 2048 7.1 -> 7.5).
-constexpr uint32_t kWideRowsSplitWaves = 2048;
 
 template <Format F, bool HALF, int P, int NF>
 void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
@@ -3625,25 +3629,18 @@ void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
     // / 6.22 / 8.16 -> 5.05 / 5.14 / 7.12 (1024 x 1024: 3.25 / 3.22 / 3.94 ->
     // 3.51 / 3.46 / 3.70).
     if (args.n_tiles < kHeadTiles) {
-        if constexpr (F == Format::Int8) {
-            // Two waves per slice, one 128-k piece each.  Measured at B = 2
-            // / 4 / 8 (us per launch, A/B on one device): 2048 x 2048 3.84
-            // / 3.96 / 4.84 -> 3.62 / 3.53 / 4.31, 4608 x 1024 - / 3.78 /
-            // 4.41 -> - / 3.48 / 4.15, 8192 x 2048 5.1 / 5.1 / 7.27 -> 5.1
-            // / 5.1 / 6.64, 1024 x 1024 the same; B = 5 at 2048 x 2048
-            // 4.81 -> 4.27-4.48.
-            wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 1, 2>
-                <<<args.n_tiles, 128 * P, 0, stream>>>(args);
-            return;
-        }
-        if constexpr (NF == 2) {
-            if (args.n_tiles * uint32_t(P) <= kWideRowsSplitWaves) {
-                wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 2>
-                    <<<args.n_tiles, 128 * P, 0, stream>>>(args);
-                return;
-            }
-        }
-        wide_rows_kernel<F, HALF, P, 1, NF, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
+        // Two waves per slice, one 128-k piece each.  Measured at B = 2 / 4
+        // / 8 (us per launch, A/B on one device) against one wave per
+        // slice: INT8 2048 x 2048 3.84 / 3.96 / 4.84 -> 3.62 / 3.53 / 4.31,
+        // 4608 x 1024 - / 3.78 / 4.41 -> - / 3.48 / 4.15, 8192 x 2048 5.1 /
+        // 5.1 / 7.27 -> 5.1 / 5.1 / 6.64, 1024 x 1024 the same (B = 5 at
+        // 2048 x 2048 4.81 -> 4.27-4.48); ternary (against the fragments of
+        // a slice split over two waves at five to eight rows) 1024 x 1024
+        // 3.73 / - / 3.93 -> 3.48 / - / 3.7-4.0, 4608 x 1024 3.95 / 3.98 /
+        // 5.27 -> 3.68 / 3.73 / 5.07, 2048 x 2048 3.93 / 4.04 / 5.45 -> 3.82
+        // / 3.91 / 5.24, 8192 x 2048 5.37 / 5.58 / 8.49 -> 5.40 / 5.46 /
+        // 8.20.
+        wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 2><<<args.n_tiles, 128 * P, 0, stream>>>(args);
         return;
     }
     constexpr int R = P;

@@ -208,10 +208,10 @@ def test_one_row_few_tiles(backend, path, scheme, n, k):
 @pytest.mark.parametrize("n", [65541, 2053])
 def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k, n):
     """Past 4096 row tiles (n = 65541) and at 129 row tiles (n = 2053, where
-    five to eight rows split each slice's two fragments over two waves), the
-    last tile five rows long: two, five and eight activation rows (dead batch
-    slots in the one- and two-fragment layouts) against the oracle, and for
-    INT8 every row of the batch equal bit for bit to the same row multiplied
+    each 256-k slice runs as two 128-k pieces on two waves), the last tile
+    five rows long: two, five and eight activation rows (dead batch slots in
+    the one- and two-fragment layouts) against the oracle, and for INT8
+    every row of the batch equal bit for bit to the same row multiplied
     alone (the multi-row wide kernel keeps the one-row kernel's group and
     slice order)."""
     say("wide rows", scheme, path, k, n)
