@@ -2692,22 +2692,23 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
 // duplicated; a ternary piece reads half of each 16-byte lane load); the
 // block adds the two pieces of a slice before adding the slices in order,
 // the one-row kernel's sum.
-template <Format F, bool HALF, int P, int R, int NF, int W = 16, int HS = 1>
+template <Format F, bool HALF, int P, int R, int NF, int W = 16, int HS = 1, int SPW = 1>
 __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
 {
     static_assert(F != Format::Nf4, "integer formats");
     static_assert(HS == 1 || HS == 2, "whole or half slices");
+    static_assert(SPW == 1 || (HS == 1 && R == 1), "several slices per wave: one tile, whole slices");
     using ST = typename ScaleT<HALF>::type;
     constexpr int NFL = NF;                         // fragments this wave forms
     // Ternary pieces read half of each 16-byte lane load (8 bytes: two
     // ksteps, one 128-group).
     constexpr bool HALFLOAD = F == Format::Ternary && HS == 2;
-    constexpr int PW = P * HS;                      // slice pieces per tile
+    constexpr int PW = P * HS / SPW;                // waves per tile
     constexpr int TS = W / PW;                      // tiles per round
     constexpr int LS = WideGeo<F>::loads;           // lane loads per (tile, slice)
     constexpr int L = HALFLOAD ? 1 : LS / HS;       // ... per (tile, piece)
     constexpr int KPL = HALFLOAD ? 2 : WideGeo<F>::ksteps_per_load;
-    constexpr int NL = R * L;                       // lane loads per wave
+    constexpr int NL = R * L * SPW;                 // lane loads per wave
     constexpr int AH = NL < kWideAhead ? NL : kWideAhead;
     constexpr int G = 2 * P;                        // 128-groups per tile
     constexpr int GW = 2 / HS;                      // 128-groups per piece
@@ -2718,7 +2719,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     __shared__ float partial[TS * R * PW * MB * 16];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
-    const uint32_t part = wave % PW, tslot = wave / PW;
+    const uint32_t wpart = wave % PW, tslot = wave / PW;
     const uint32_t tile0 = blockIdx.x * (TS * R) + tslot;
     auto tile_of = [&](int i) {
         const uint32_t t = tile0 + uint32_t(TS * i);
@@ -2726,64 +2727,80 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     };
 
     // 1. The piece's activations: one float4 per kstep and fragment (K is
-    // 256 P, so every address lies in the row).
+    // 256 P, so every address lies in the row).  With several slices per
+    // wave (slice wpart * SPW + sp), each slice's values are loaded one
+    // slice ahead of its digits.
     const uint32_t b = (lane >> 2) & 3;
-    const uint32_t off = (256 / HS) * part + 16 * q + 4 * (lane & 3);
     RegX<LB> rx[NFL][NB];
+    auto load_x = [&](uint32_t part) {
+        const uint32_t off = (256 / HS) * part + 16 * q + 4 * (lane & 3);
 #pragma unroll
-    for (int f = 0; f < NFL; ++f) {
-        const uint32_t row = 4 * f + b;
-        const bool live = row < a.m;
-        const float *xrow = a.x + size_t(live ? row : 0) * a.k + off;
+        for (int f = 0; f < NFL; ++f) {
+            const uint32_t row = 4 * f + b;
+            const bool live = row < a.m;
+            const float *xrow = a.x + size_t(live ? row : 0) * a.k + off;
 #pragma unroll
-        for (int bi = 0; bi < NB; ++bi)
+            for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-            for (int kk = 0; kk < LB; ++kk) {
-                const v4f v = *reinterpret_cast<const v4f *>(xrow + 64 * (bi * LB + kk));
-                rx[f][bi].v[kk] = live ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            }
-    }
-    // 2. The piece's group scales of every tile (this lane's row j), then
+                for (int kk = 0; kk < LB; ++kk) {
+                    const v4f v = *reinterpret_cast<const v4f *>(xrow + 64 * (bi * LB + kk));
+                    rx[f][bi].v[kk] = live ? v : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+        }
+    };
+    load_x(wpart * SPW);
+    // 2. The group scales of every tile and slice (this lane's row j), then
     // the first weight loads.
-    ST sc[R][GW];
+    ST sc[R * SPW][GW];
 #pragma unroll
-    for (int i = 0; i < R; ++i)
+    for (int i = 0; i < R * SPW; ++i)
 #pragma unroll
         for (int gs = 0; gs < GW; ++gs)
             sc[i][gs] = reinterpret_cast<const ST *>(
-                a.scales)[(size_t(tile_of(i)) * G + GW * part + gs) * 16 + j];
+                a.scales)[(size_t(tile_of(SPW == 1 ? i : 0)) * G +
+                           GW * (wpart * SPW + (SPW == 1 ? 0 : i)) + gs) *
+                              16 +
+                          j];
     __builtin_amdgcn_sched_barrier(0);
     v4u w[NL];
     auto issue = [&](auto n_tag) {
         constexpr int n = decltype(n_tag)::value;
+        // SPW > 1 (one tile): load n is load n % L of slice n / L.
+        const uint32_t part = SPW == 1 ? wpart : wpart * SPW + n / L;
+        constexpr int ti = SPW == 1 ? n / L : 0;
         if constexpr (HALFLOAD) {
             typedef unsigned v2u __attribute__((ext_vector_type(2)));
             const v2u *src = reinterpret_cast<const v2u *>(
                                  reinterpret_cast<const v4u *>(a.tiles) +
-                                 (size_t(tile_of(n)) * (P * LS) + (part / 2) * LS) * 64 + lane) +
+                                 (size_t(tile_of(ti)) * (P * LS) + (part / 2) * LS) * 64 + lane) +
                              part % 2;
             const v2u u = __builtin_nontemporal_load(src);
             w[n] = v4u{u.x, u.y, 0u, 0u};
         } else {
             const v4u *src = reinterpret_cast<const v4u *>(a.tiles) +
-                             (size_t(tile_of(n / L)) * (P * LS) + part * L + n % L) * 64 + lane;
+                             (size_t(tile_of(ti)) * (P * LS) + part * L + n % L) * 64 + lane;
             w[n] = __builtin_nontemporal_load(src);
         }
     };
     unroll_groups<AH>(issue);
     __builtin_amdgcn_sched_barrier(0);
 
-    // 3. Digits, group factors and corrections of the piece.
+    // 3. Digits, group factors and corrections of the piece (of each slice
+    // in turn), then 4. the tiles: products of the piece per group and the
+    // combine.  Several slices per wave add in slice order.
     Blk blk[NB];
+    float wave_sum[NFL];
+    unroll_groups<R * SPW>([&](auto i_tag) {
+        constexpr int i = decltype(i_tag)::value;  // tile (SPW == 1) or slice
+        if constexpr (SPW == 1 ? i == 0 : true) {
 #pragma unroll
-    for (int bi = 0; bi < NB; ++bi)
+            for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-        for (int f = 0; f < NFL; ++f)
-            reg_digits(rx[f][bi], blk[bi], f);
-
-    // 4. The tiles: products of the piece per group, then the combine.
-    unroll_groups<R>([&](auto i_tag) {
-        constexpr int i = decltype(i_tag)::value;
+                for (int f = 0; f < NFL; ++f)
+                    reg_digits(rx[f][bi], blk[bi], f);
+            if constexpr (SPW > 1 && i + 1 < SPW)
+                load_x(wpart * SPW + i + 1);  // the next slice's values
+        }
         v4i acc[GW][NFL];
 #pragma unroll
         for (int gs = 0; gs < GW; ++gs)
@@ -2832,10 +2849,18 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                 const float gsum = float(hi) * 65536.0f + float(lo);
                 g[gs] = gsum * (to_f32<HALF>(sc[i][gs]) * xf);
             }
-            partial[(((tslot + TS * i) * PW + part) * MB + 4 * f + q) * 16 + j] =
-                GW == 2 ? g[0] + g[GW - 1] : g[0];
+            const float value = GW == 2 ? g[0] + g[GW - 1] : g[0];
+            if constexpr (SPW == 1)
+                partial[(((tslot + TS * i) * PW + wpart) * MB + 4 * f + q) * 16 + j] = value;
+            else
+                wave_sum[f] = i == 0 ? value : wave_sum[f] + value;
         }
     });
+    if constexpr (SPW > 1) {
+#pragma unroll
+        for (int f = 0; f < NFL; ++f)
+            partial[((tslot * PW + wpart) * MB + 4 * f + q) * 16 + j] = wave_sum[f];
+    }
 
     // 5. The slices of each (tile, batch row), added in order (each slice
     // the sum of its pieces).
@@ -2848,7 +2873,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
         };
         float sum = slice(0);
 #pragma unroll
-        for (int pp = 1; pp < P; ++pp)
+        for (int pp = 1; pp < P / SPW; ++pp)
             sum += slice(pp);
         const uint32_t t = blockIdx.x * (TS * R) + (tl % TS) + TS * (tl / TS);
         const uint32_t row = t * 16 + r;
@@ -3673,9 +3698,16 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
                   t.head_dim == 0 || t.head_dim % 4 || call.k % t.head_dim))
         return false;
     const float *x = norm || merge ? t.a : call.x;
+    // INT8, K = 8192 at two to four rows below the head size: sixteen waves
+    // of two slices each (wide_rows_kernel SPW = 2).  Measured (us per
+    // launch, A/B on one device) against the K-split plans: 2048 x 8192 B =
+    // 2 / 4 8.43 / 8.89 -> 7.69 / 7.89, 8192 x 8192 B = 4 16.4 -> 15.9; at
+    // eight rows slower (9.8 -> 11.6), and slower for ternary at every row
+    // count (B = 2 7.45 -> 8.26, B = 8 8.65 -> 14.5).
+    const bool k8192 = F == Format::Int8 && call.k == 8192 && call.m > 1 && call.m <= 4 && !head;
     if (call.separate_prologue || (t.kind != XKind::Plain && !norm && !merge) || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > max_m ||
-        (call.k != 1024 && call.k != 2048) ||
+        (call.k != 1024 && call.k != 2048 && !k8192) ||
         (F == Format::Ternary && head && call.k != 1024) || !x || !aligned(x))
         return false;
     // wide_row_kernel addresses the repacked codes with 32-bit byte offsets.
@@ -3704,6 +3736,19 @@ bool try_wide_row(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
     args.n_tiles = n_tiles;
     const bool half = call.a.tiled_half;
     if constexpr (F != Format::Nf4) {
+        if (k8192) {
+            auto go = [&](auto nf_tag) {
+                constexpr int NF = decltype(nf_tag)::value;
+                if (half)
+                    wide_rows_kernel<F, true, 32, 1, NF, 16, 1, 2>
+                        <<<args.n_tiles, 1024, 0, stream>>>(args);
+                else
+                    wide_rows_kernel<F, false, 32, 1, NF, 16, 1, 2>
+                        <<<args.n_tiles, 1024, 0, stream>>>(args);
+            };
+            go(std::integral_constant<int, 1>{});
+            return true;
+        }
         if (call.m > 1) {
             auto rows = [&](auto p_tag, auto nf_tag) {
                 constexpr int P = decltype(p_tag)::value, NF = decltype(nf_tag)::value;

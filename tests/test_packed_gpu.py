@@ -237,6 +237,25 @@ def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k, n
                 assert np.array_equal(got[b], alone[b]), (m, b)
 
 
+def test_int8_k8192_rows_at_a_ragged_width(backend, path):
+    """INT8 at K = 8192, two to four rows, 129 row tiles (n = 2053, the last
+    tile five rows long; the multi-row wide kernel with sixteen waves of two
+    256-k slices each), against the oracle."""
+    say("int8 k8192 rows", path)
+    n, k = 2053, 8192
+    codes, scales = make_weights(n, k, "int8", 0x5EED0031)
+    cb, sb = upload_weights(backend, codes, scales)
+    x = convert.normal((4, k), 0xAC70031)
+    for m in (2, 3, 4):
+        xb = backend.upload_f32((m, k), x[:m])
+        out = backend.allocate_f32((m, n))
+        backend.packed_linear(out, xb, cb, sb)
+        got = backend.read(out)
+        want = cached_oracle(("int8 k8192", m, n, k), x[:m], codes, scales)
+        assert max_rel_err(got, want) <= 1e-3
+        assert_close(got, want, 1e-4, 1e-4)
+
+
 # The prefill GEMM configuration: M in {512, 2048} tokens against 8192 x 2048
 # and 2048 x 8192 weights.  M = 512 is checked on every row; M = 2048 on a
 # seeded subset of rows (all N columns), the oracle being a scalar CPU path.
