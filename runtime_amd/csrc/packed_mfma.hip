@@ -2699,7 +2699,6 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     static_assert(HS == 1 || HS == 2, "whole or half slices");
     static_assert(SPW == 1 || (HS == 1 && R == 1), "several slices per wave: one tile, whole slices");
     using ST = typename ScaleT<HALF>::type;
-    constexpr int NFL = NF;                         // fragments this wave forms
     // Ternary pieces read half of each 16-byte lane load (8 bytes: two
     // ksteps, one 128-group).
     constexpr bool HALFLOAD = F == Format::Ternary && HS == 2;
@@ -2714,7 +2713,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     constexpr int GW = 2 / HS;                      // 128-groups per piece
     constexpr int LB = Geo<F>::lb < 4 / HS ? Geo<F>::lb : 4 / HS;  // ksteps per digit block
     constexpr int NB = 4 / HS / LB;                 // digit blocks per piece
-    using Blk = I8Block<F, 1, 1, NFL, HALF, LB>;
+    using Blk = I8Block<F, 1, 1, NF, HALF, LB>;
     constexpr int MB = 4 * NF;                      // batch rows held
     __shared__ float partial[TS * R * PW * MB * 16];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -2731,11 +2730,11 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     // wave (slice wpart * SPW + sp), each slice's values are loaded one
     // slice ahead of its digits.
     const uint32_t b = (lane >> 2) & 3;
-    RegX<LB> rx[NFL][NB];
+    RegX<LB> rx[NF][NB];
     auto load_x = [&](uint32_t part) {
         const uint32_t off = (256 / HS) * part + 16 * q + 4 * (lane & 3);
 #pragma unroll
-        for (int f = 0; f < NFL; ++f) {
+        for (int f = 0; f < NF; ++f) {
             const uint32_t row = 4 * f + b;
             const bool live = row < a.m;
             const float *xrow = a.x + size_t(live ? row : 0) * a.k + off;
@@ -2789,23 +2788,23 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     // in turn), then 4. the tiles: products of the piece per group and the
     // combine.  Several slices per wave add in slice order.
     Blk blk[NB];
-    float wave_sum[NFL];
+    float wave_sum[NF];
     unroll_groups<R * SPW>([&](auto i_tag) {
         constexpr int i = decltype(i_tag)::value;  // tile (SPW == 1) or slice
         if constexpr (SPW == 1 ? i == 0 : true) {
 #pragma unroll
             for (int bi = 0; bi < NB; ++bi)
 #pragma unroll
-                for (int f = 0; f < NFL; ++f)
+                for (int f = 0; f < NF; ++f)
                     reg_digits(rx[f][bi], blk[bi], f);
             if constexpr (SPW > 1 && i + 1 < SPW)
                 load_x(wpart * SPW + i + 1);  // the next slice's values
         }
-        v4i acc[GW][NFL];
+        v4i acc[GW][NF];
 #pragma unroll
         for (int gs = 0; gs < GW; ++gs)
 #pragma unroll
-            for (int f = 0; f < NFL; ++f)
+            for (int f = 0; f < NF; ++f)
                 acc[gs][f] = v4i{0, 0, 0, 0};
         unroll_groups<L>([&](auto l_tag) {
             constexpr int l = decltype(l_tag)::value;
@@ -2825,14 +2824,14 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
                     bw = v4i{int(wv.x), int(wv.y), int(wv.z), int(wv.w)};
                 }
 #pragma unroll
-                for (int f = 0; f < NFL; ++f)
+                for (int f = 0; f < NF; ++f)
                     acc[s2 / 2][f] = __builtin_amdgcn_mfma_i32_16x16x64_i8(
                         blk[s2 / LB].af[s2 % LB][f], bw, acc[s2 / 2][f], 0, 0, 0);
             }
             __builtin_amdgcn_sched_barrier(0);
         });
 #pragma unroll
-        for (int f = 0; f < NFL; ++f) {
+        for (int f = 0; f < NF; ++f) {
             // Each group's product is rounded before the add (no fused
             // multiply-add), as the one-row kernel's cross-lane sum.
 #pragma clang fp contract(off)
@@ -2858,7 +2857,7 @@ __global__ __launch_bounds__(64 * W) void wide_rows_kernel(StreamArgs a)
     });
     if constexpr (SPW > 1) {
 #pragma unroll
-        for (int f = 0; f < NFL; ++f)
+        for (int f = 0; f < NF; ++f)
             partial[((tslot * PW + wpart) * MB + 4 * f + q) * 16 + j] = wave_sum[f];
     }
 
