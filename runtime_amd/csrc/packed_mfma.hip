@@ -3615,7 +3615,11 @@ unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, 
             wide_row_kernel<F, HALF, P, 1, P><<<args.n_tiles, 64 * P, 0, stream>>>(args);
         return 0;
     }
-    constexpr int R = F == Format::Nf4 && P == 8 ? 8 : 4;
+    // Tiles per wave at the head: eight at K = 2048, four at K = 1024 (one
+    // row, us per launch, A/B on one device: INT8 65536 x 2048 R = 4 / 8
+    // 21.1-21.2 / 20.9-21.0; 65536 x 1024 R = 2 / 4 / 8 12.0 / 11.6 / 13.5,
+    // ternary 6.5 / 5.7-5.8 / 7.4; R = 1 slower everywhere).
+    constexpr int R = P == 8 ? 8 : 4;
     constexpr int TS = 16 / P;
     const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
     // The norm comes with the argmax candidates (the LM head of the fused
