@@ -2059,6 +2059,22 @@ void gemv_nf4_kernel(MfmaArgs a)
 // order.
 // ---------------------------------------------------------------------------
 constexpr uint32_t kStreamLutCopies = 32;
+// The code-byte table with C copies of each entry (C = 32, 16 or 8): the
+// cells of one byte value lie 8 C bytes apart, and a lane's cell address is
+// (code byte) * 256 + 8 * spread * (lane % C), shifted right by `shift`
+// (one byte permute and one shift).  Kernels of one block per row tile
+// (below the head size) fill 8 copies: their blocks are short, and the
+// 64 KB fill of 32 copies sat on every block's path (1.2B-shape decode 2289
+// -> 2337 tok/s, NF4 4608 x 1024 at one row 4.48 -> 3.70 us, 8192 x 2048
+// 5.44 -> 4.88; the head, 13.8 us with 32, takes 17.1 with 8).
+template <uint32_t C>
+struct LutLayout {
+    static_assert(C == 32 || C == 16 || C == 8, "table copies");
+    static constexpr uint32_t copies = C;
+    static constexpr uint32_t shift = C == 32 ? 0 : C == 16 ? 1 : 2;
+    static constexpr uint32_t spread = 1u << shift;
+};
+constexpr uint32_t kSmallLutCopies = 8;
 
 template <int G, bool HALF>
 __global__ __launch_bounds__(64 * kStreamWaves) void stream_nf4_kernel(StreamArgs a)
@@ -2387,7 +2403,9 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
     constexpr int G = 2 * P;                        // 128-groups per tile
     constexpr bool NF4 = F == Format::Nf4;
     __shared__ float partial[TS * R * P * 16];
-    __shared__ unsigned lut[NF4 ? 256 * 2 * kStreamLutCopies : 1];
+    // One block per tile below the head size: the small table.
+    using LUT = LutLayout<R == 1 ? kSmallLutCopies : kStreamLutCopies>;
+    __shared__ unsigned lut[NF4 ? 256 * 2 * LUT::copies : 1];
     __shared__ uint2 entries[NF4 ? 256 : 1];
     const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
@@ -2443,8 +2461,8 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
         if (threadIdx.x < 256)
             entries[threadIdx.x] = nf4_lut_entry(threadIdx.x);
         __syncthreads();
-        for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
-            const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
+        for (uint32_t v = threadIdx.x; v < 256 * 2 * LUT::copies / 4; v += blockDim.x) {
+            const uint2 e = entries[v / (2 * LUT::copies / 4)];
             reinterpret_cast<v4u *>(lut)[v] = v4u{e.x, e.y, e.x, e.y};
         }
     }
@@ -2532,7 +2550,7 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
     }
     if constexpr (NF4)
         __syncthreads();  // the table
-    const unsigned copy_byte = 8 * (lane % kStreamLutCopies);
+    const unsigned copy_byte = 8 * LUT::spread * (lane % LUT::copies);
     const char *cells = reinterpret_cast<const char *>(lut);
 
     // NF4 B operands of one kstep's code word: the table entries (hi pair,
@@ -2544,7 +2562,8 @@ __global__ __launch_bounds__(64 * W) void wide_row_kernel(StreamArgs a)
         for (int b = 0; b < 4; ++b) {
             // (code byte b) * 256 + copy_byte.
             const unsigned at =
-                __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + b) << 8));
+                __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + b) << 8)) >>
+                LUT::shift;
             ent[b] = *reinterpret_cast<const uint2 *>(cells + at);
         }
         b0 = v4u{ent[0].x, ent[0].y, ent[1].x, ent[1].y};
@@ -2914,7 +2933,8 @@ __global__ __launch_bounds__(64 * P) void wide_one_kernel(WideArgs a)
     constexpr int G = 2 * P * SPW;                   // 128-groups per tile
     __shared__ float partial[S * P * 16];
     __shared__ float squares_part[P];
-    __shared__ unsigned lut[NF4 ? 256 * 2 * kStreamLutCopies : 1];
+    using LUT = LutLayout<kSmallLutCopies>;  // one block per tile
+    __shared__ unsigned lut[NF4 ? 256 * 2 * LUT::copies : 1];
     __shared__ uint2 entries[NF4 ? 256 : 1];
     const uint32_t lane = threadIdx.x & 63, part = threadIdx.x >> 6;
     const uint32_t q = lane >> 4, j = lane & 15;
@@ -2968,8 +2988,8 @@ __global__ __launch_bounds__(64 * P) void wide_one_kernel(WideArgs a)
         if (threadIdx.x < 256)
             entries[threadIdx.x] = nf4_lut_entry(threadIdx.x);
         __syncthreads();
-        for (uint32_t v = threadIdx.x; v < 256 * 2 * kStreamLutCopies / 4; v += blockDim.x) {
-            const uint2 e = entries[v / (2 * kStreamLutCopies / 4)];
+        for (uint32_t v = threadIdx.x; v < 256 * 2 * LUT::copies / 4; v += blockDim.x) {
+            const uint2 e = entries[v / (2 * LUT::copies / 4)];
             reinterpret_cast<v4u *>(lut)[v] = v4u{e.x, e.y, e.x, e.y};
         }
     }
@@ -3059,14 +3079,15 @@ __global__ __launch_bounds__(64 * P) void wide_one_kernel(WideArgs a)
     };
     if constexpr (NF4)
         __syncthreads();  // the table
-    const unsigned copy_byte = 8 * (lane % kStreamLutCopies);
+    const unsigned copy_byte = 8 * LUT::spread * (lane % LUT::copies);
     const char *cells = reinterpret_cast<const char *>(lut);
     auto nf4_entries = [&](unsigned word, v4u &b0, v4u &b1) {
         uint2 ent[4];
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const unsigned at =
-                __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + b) << 8));
+                __builtin_amdgcn_perm(word, copy_byte, 0x0C0C0000u | ((4u + b) << 8)) >>
+                LUT::shift;
             ent[b] = *reinterpret_cast<const uint2 *>(cells + at);
         }
         b0 = v4u{ent[0].x, ent[0].y, ent[1].x, ent[1].y};
