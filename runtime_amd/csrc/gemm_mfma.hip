@@ -617,16 +617,23 @@ uint32_t tiles_of(const PackedCall &call, uint32_t *tiles_n, uint32_t bm)
 
 // Rows per block tile: 64 where 128-row tiles would not fill the grid
 // without a K split (fewer than kHalfRowsBelow tiles), so the product
-// needs fewer K chunks (none at M = 512 x 8192) and their reduction.
-// Measured (us per call, A/B on one device): M = 512 x 8192 x 2048 ternary
-// 58.4 -> 50.0, INT8 61.3 -> 50.0-50.9, NF4 70-73 -> 62.6-63.5; M = 128
-// 35.6 -> 30.1; M = 256 41.8 -> 39.0; M = 512 x 2048 x 8192 (still split)
-// 2-7 % faster.
+// needs fewer K chunks (none at M = 512 x 8192) and their reduction --
+// except for ternary and NF4 at long K past 512 rows, where the 128-row
+// tiles and their split measured faster.  Measured (us per call, A/B on one device): M = 512 x
+// 8192 x 2048 ternary 58.4 -> 50.0, INT8 61.3 -> 50.0-50.9, NF4 70-73 ->
+// 62.6-63.5; M = 2048 x 2048 x 2048 ternary 63.5 -> 58.3-59.2, NF4 76.3 ->
+// 69.6; M = 128 35.6 -> 30.1; M = 256 41.8 -> 39.0; M = 512 x 2048 x 8192
+// 2-7 % faster; but M = 2048 x 2048 x 8192 ternary 156.1-156.6 with the
+// split against 159.8-160.1, NF4 209.2-209.5 against 213.5-214.5, M = 1024
+// ternary 95.8 against 98.7-100 (INT8 164.8-166.5 against 169.3-169.8: it
+// keeps the 64-row tiles).
 constexpr uint32_t kHalfRowsBelow = 512;
 uint32_t block_rows(const PackedCall &call)
 {
     uint32_t tiles_n;
-    return tiles_of(call, &tiles_n, kBM) < kHalfRowsBelow ? kBM / 2 : kBM;
+    const bool split = tiles_of(call, &tiles_n, kBM) < kHalfRowsBelow;
+    return split && (call.k <= 4096 || call.m <= 512 || call.format == Format::Int8) ? kBM / 2
+                                                                                     : kBM;
 }
 
 }  // namespace
