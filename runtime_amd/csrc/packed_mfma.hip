@@ -1222,9 +1222,12 @@ constexpr int kStreamTernaryAhead = 3;
 // 7.70-7.82 with eight (interleaved runs on one device).
 constexpr int kStreamTernaryIdleAhead = 6;
 constexpr int kStreamNf4Ahead = 2;
-// Widest grids only: below this many tiles the K-split plans keep more
-// waves busy.
-constexpr uint32_t kStreamMinTiles = 1024;
+// Widest grids only: below this many tiles the one-tile-per-block plans
+// keep more waves busy.  At 512 tiles (8192 x 2048, us per launch, A/B on
+// one device) the streaming kernels measured 4.1 -> 4.3 at one row, 5.6 ->
+// 6.0 at four, 8.6 -> 9.0 at eight; at 768 (12288 x 2048) 4.9 -> 4.4 at
+// one, 7.5 -> 6.1 at four.
+constexpr uint32_t kStreamMinTiles = 768;
 // Fewest blocks a streaming launch spreads its tiles over.
 constexpr uint32_t kStreamMinBlocks = 256;
 
@@ -3525,12 +3528,10 @@ void launch_stream_ternary(hipStream_t stream, const StreamArgs &args, bool half
         else
             stream_ternary_kernel<NF, KL, false, W><<<blocks, 64 * W, 0, stream>>>(args);
     };
-    // (n_tiles >= kStreamMinTiles = 4 * kStreamMinBlocks.)  Measured at
-    // 16384 x 1024, one row: 16 waves per block 5.3 us, 4 waves 4.6-4.8 us.
-    // Smaller matrices stay on the K-split kernels: streamed with 1-4 waves
-    // per block they measured slower (8192 x 2048 5.5-8.1 against 5.8 us,
-    // 2048 x 2048 8.0-12.5 against 4.3 us).
-    static_assert(kStreamMinTiles >= 4 * kStreamMinBlocks, "at least four waves per block");
+    // (n_tiles >= kStreamMinTiles, so at least 192 blocks of four waves.)
+    // Measured at 16384 x 1024, one row: 16 waves per block 5.3 us, 4 waves
+    // 4.6-4.8 us.
+    static_assert(kStreamMinTiles >= 3 * kStreamMinBlocks, "at least 192 blocks");
     if (args.n_tiles >= 16 * kStreamMinBlocks)
         go(std::integral_constant<int, 16>{});
     else if (args.n_tiles >= 8 * kStreamMinBlocks)
@@ -4017,6 +4018,17 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
+    // Ternary from kStreamMinTiles row tiles to below the head size: the
+    // streaming kernels before the one-tile-per-block plans.  Measured (us
+    // per launch, A/B on one device), one / two / four / eight rows: 16384 x
+    // 2048 5.6 / 9.1 / 9.3 / 14.8 -> 4.5 / 5.3 / 6.2 / 9.5, 32768 x 2048
+    // 8.7 / 16.2 / 16.8 / 27.3 -> 5.3 / 6.0 / 6.6 / 9.5, 12288 x 2048 at
+    // one / four rows 4.9 / 7.5 -> 4.4 / 6.1; two rows at K = 1024, 16384 /
+    // 32768 rows 5.4 / 8.9 -> 3.9 / 4.3.
+    if constexpr (F == Format::Ternary) {
+        if (n_tiles < kHeadTiles && try_stream_ternary(stream, call, n_tiles))
+            return;
+    }
     if (try_wide_row<F>(stream, call, n_tiles))
         return;
     if (try_wide_one<F>(stream, call, n_tiles))
