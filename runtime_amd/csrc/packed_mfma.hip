@@ -3319,6 +3319,7 @@ constexpr uint32_t kSplitMaxBlocks = 128;
 // Row tiles from which an INT8 product at one or two rows is an LM head
 // (65536 rows: 4096 tiles) and streams one tile per block.
 constexpr uint32_t kHeadTiles = 4096;
+constexpr uint32_t kNf4MidTiles = 1024;
 
 // Whether float ranges [a, a + na) and [b, b + nb) share memory.
 bool overlaps(const float *a, size_t na, const float *b, size_t nb)
@@ -3629,6 +3630,30 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
 template <Format F, bool HALF, int P>
 unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, bool merge)
 {
+    constexpr int TS = 16 / P;
+    // NF4 from kNf4MidTiles tiles to below the head size: blocks of 16
+    // waves, R tiles per wave with R the largest of 4, 2, 1 that leaves at
+    // least 256 blocks (the 32-copy table filled once per R rounds).
+    // Measured at one row (us per launch, A/B on one device) against one
+    // block per tile: 16384 x 2048 7.1 -> 5.9, 32768 x 2048 12.0 -> 8.5,
+    // 49152 x 2048 16.4-18.5 -> 14.6-15.3, 32768 x 1024 7.5 -> 6.0, 16384 x
+    // 1024 the same; INT8 measured the same or slower (32768 x 1024 6.9 ->
+    // 7.2, 49152 x 2048 16.4 -> 17.8) and keeps one block per tile.
+    if constexpr (F == Format::Nf4) {
+        if (args.n_tiles < kHeadTiles && args.n_tiles >= kNf4MidTiles && !merge) {
+            auto mid = [&](auto r_tag) {
+                constexpr int RM = decltype(r_tag)::value;
+                const unsigned blocks = (args.n_tiles + TS * RM - 1) / (TS * RM);
+                wide_row_kernel<F, HALF, P, RM><<<blocks, 1024, 0, stream>>>(args);
+                return args.argmax ? 0u : blocks;
+            };
+            if (args.n_tiles >= 4 * TS * 256)
+                return mid(std::integral_constant<int, 4>{});
+            if (args.n_tiles >= 2 * TS * 256)
+                return mid(std::integral_constant<int, 2>{});
+            return mid(std::integral_constant<int, 1>{});
+        }
+    }
     if (args.n_tiles < kHeadTiles) {
         if (merge)
             wide_row_kernel<F, HALF, P, 1, P, false, false, true><<<args.n_tiles, 64 * P, 0,
@@ -3642,7 +3667,6 @@ unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, 
     // 21.1-21.2 / 20.9-21.0; 65536 x 1024 R = 2 / 4 / 8 12.0 / 11.6 / 13.5,
     // ternary 6.5 / 5.7-5.8 / 7.4; R = 1 slower everywhere).
     constexpr int R = P == 8 ? 8 : 4;
-    constexpr int TS = 16 / P;
     const unsigned blocks = (args.n_tiles + TS * R - 1) / (TS * R);
     // The norm comes with the argmax candidates (the LM head of the fused
     // decode step); NF4 heads keep the separate norm and selection (folded,
