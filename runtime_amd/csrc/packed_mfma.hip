@@ -3714,7 +3714,36 @@ void launch_wide_rows(hipStream_t stream, const StreamArgs &args)
         // 5.27 -> 3.68 / 3.73 / 5.07, 2048 x 2048 3.93 / 4.04 / 5.45 -> 3.82
         // / 3.91 / 5.24, 8192 x 2048 5.37 / 5.58 / 8.49 -> 5.40 / 5.46 /
         // 8.20.
-        wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 2><<<args.n_tiles, 128 * P, 0, stream>>>(args);
+        // INT8 from 512 blocks' worth of tiles at two tiles per wave (1024
+        // tiles at K = 2048, 2048 at K = 1024) to below the head size:
+        // blocks of 16 waves, two tiles per wave up to 256 blocks, four
+        // beyond.  Measured at B = 2 / 4-5 / 8 (us per launch, A/B on one
+        // device) against one block per tile: 16384 x 2048 8.5 / 8.6 / 11.4
+        // -> 7.7 / 7.8 / 8.8, 20480 x 2048 10.1 / 13.2 (B = 5) / - -> 9.3 /
+        // 10.5 / -, 24576 x 2048 11.5 / 16.2 (B = 5) / - -> 10.2 / 11.1 / -,
+        // 32768 x 2048 14.6 / - / 21.2-23.6 -> 12.2 / - / 13.2, 40960 x
+        // 2048 - / 18.4-19.6 / 26.5-29.3 -> - / 18.3 / 21.1, 32768 x 1024
+        // at B = 8 11.2 -> 8.8, 49152 x 1024 at B = 4 11.1 -> 10.4; one
+        // tile per wave at 16384 x 1024 measured slower (B = 2 / 4 / 8 4.9
+        // / 5.0 / 6.5 -> 5.4 / 5.4 / 7.5), and 320 blocks of two tiles per
+        // wave slower than 160 of four (20480 x 2048, B = 5 10.5 -> 14.2).
+        constexpr int TS = 16 / P;
+        if (F != Format::Int8 || args.n_tiles < 2 * TS * 256) {
+            wide_rows_kernel<F, HALF, P, 1, NF, 2 * P, 2><<<args.n_tiles, 128 * P, 0, stream>>>(
+                args);
+            return;
+        }
+        if constexpr (F == Format::Int8) {
+            auto mid = [&](auto r_tag) {
+                constexpr int RM = decltype(r_tag)::value;
+                const unsigned blocks = (args.n_tiles + TS * RM - 1) / (TS * RM);
+                wide_rows_kernel<F, HALF, P, RM, NF><<<blocks, 1024, 0, stream>>>(args);
+            };
+            if (args.n_tiles <= 2 * TS * 256)
+                mid(std::integral_constant<int, 2>{});
+            else
+                mid(std::integral_constant<int, 4>{});
+        }
         return;
     }
     constexpr int R = P;

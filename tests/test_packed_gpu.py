@@ -172,8 +172,8 @@ def test_lm_head_shape(backend, path, scheme, m):
 
 @pytest.mark.parametrize("scheme", SCHEMES)
 @pytest.mark.parametrize("m", [1, 2, 3, 8])
-@pytest.mark.parametrize("n,k", [(12293, 2048), (16384, 1024), (16421, 1024), (16421, 2048),
-                                 (32805, 2048), (65536, 1024)])
+@pytest.mark.parametrize("n,k", [(12293, 2048), (16384, 1024), (16384, 2048), (16421, 1024),
+                                 (16421, 2048), (32773, 1024), (32805, 2048), (65536, 1024)])
 def test_wide_matrix_shapes(backend, path, scheme, m, n, k):
     """At least 768 row tiles at K = 1024 and 2048: the streaming ternary
     kernels (one and two rows, three to eight rows) at 4, 8 and 16 waves per
@@ -205,11 +205,12 @@ def test_one_row_few_tiles(backend, path, scheme, n, k):
 
 @pytest.mark.parametrize("scheme", ["ternary", "int8"])
 @pytest.mark.parametrize("k", [1024, 2048])
-@pytest.mark.parametrize("n", [65541, 2053])
+@pytest.mark.parametrize("n", [65541, 16421, 2053])
 def test_wide_rows_partial_tile_and_row_independence(backend, path, scheme, k, n):
-    """Past 4096 row tiles (n = 65541) and at 129 row tiles (n = 2053, where
-    each 256-k slice runs as two 128-k pieces on two waves), the last tile
-    five rows long: two, five and eight activation rows (dead batch slots in
+    """Past 4096 row tiles (n = 65541), at 1027 (n = 16421: INT8 on blocks of
+    16 waves with several tiles per wave, ternary on the streaming kernels)
+    and at 129 row tiles (n = 2053, where each 256-k slice runs as two 128-k
+    pieces on two waves), the last tile five rows long: two, five and eight activation rows (dead batch slots in
     the one- and two-fragment layouts) against the oracle, and for INT8
     every row of the batch equal bit for bit to the same row multiplied
     alone (the multi-row wide kernel keeps the one-row kernel's group and
