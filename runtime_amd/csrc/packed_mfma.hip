@@ -4253,12 +4253,20 @@ void launch_stream_nf4(hipStream_t stream, const StreamArgs &args, bool half)
 
 // As try_stream_ternary: K of 8 or 16 groups (one prologue group per wave),
 // and grids of at least kStreamMinBlocks full 16-wave blocks.
+// From 2048 row tiles (128 blocks) the streaming kernel serves what the wide
+// kernels do not (two to eight rows).  Measured (us per launch, A/B on one
+// device) against the K-split plans: 32768 x 2048 at B = 2 / 4 / 8 15.9 /
+// 15.9 / 16.1 -> 14.8 / 15.2 / 14.8, 49152 x 2048 at B = 4 21.8 -> 16.6,
+// 32768 x 1024 at B = 2 / 8 10.6 / 11.1 -> 9.5 / 9.6; at 1024 tiles slower
+// (16384 x 2048 at B = 2 / 8 11.3 / 11.4 -> 14.1 / 13.8).
+constexpr uint32_t kStreamNf4MinTiles = 2048;
+
 bool try_stream_nf4(hipStream_t stream, const PackedCall &call, uint32_t n_tiles)
 {
     const uint32_t groups = pad_to(call.k, 128) / 128;
     if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > 8 ||
-        n_tiles < kStreamWaves * kStreamMinBlocks || (groups != 8 && groups != 16) ||
+        n_tiles < kStreamNf4MinTiles || (groups != 8 && groups != 16) ||
         reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
         return false;
     StreamArgs args{};
