@@ -1228,6 +1228,9 @@ constexpr int kStreamNf4Ahead = 2;
 // 6.0 at four, 8.6 -> 9.0 at eight; at 768 (12288 x 2048) 4.9 -> 4.4 at
 // one, 7.5 -> 6.1 at four.
 constexpr uint32_t kStreamMinTiles = 768;
+// Two rows from 512 tiles: 8192 x 2048 5.5 -> 5.1 us, 8192 x 1024 3.8 -> 3.7
+// (one, four and eight rows measured slower there).
+constexpr uint32_t kStreamTwoRowMinTiles = 512;
 // Fewest blocks a streaming launch spreads its tiles over.
 constexpr uint32_t kStreamMinBlocks = 256;
 
@@ -3532,7 +3535,8 @@ void launch_stream_ternary(hipStream_t stream, const StreamArgs &args, bool half
     // (n_tiles >= kStreamMinTiles, so at least 192 blocks of four waves.)
     // Measured at 16384 x 1024, one row: 16 waves per block 5.3 us, 4 waves
     // 4.6-4.8 us.
-    static_assert(kStreamMinTiles >= 3 * kStreamMinBlocks, "at least 192 blocks");
+    static_assert(kStreamMinTiles >= 3 * kStreamMinBlocks && kStreamTwoRowMinTiles >= 512,
+                  "at least 192 blocks (128 at two rows)");
     if (args.n_tiles >= 16 * kStreamMinBlocks)
         go(std::integral_constant<int, 16>{});
     else if (args.n_tiles >= 8 * kStreamMinBlocks)
@@ -3569,7 +3573,7 @@ bool try_stream_ternary(hipStream_t stream, const PackedCall &call, uint32_t n_t
     const uint32_t kl = k_pad / 256;
     if (call.separate_prologue || call.xform.kind != XKind::Plain || call.segments ||
         call.epilogue != Epilogue::Single || call.m == 0 || call.m > 8 ||
-        n_tiles < kStreamMinTiles || (kl != 4 && kl != 8) ||
+        n_tiles < (call.m == 2 ? kStreamTwoRowMinTiles : kStreamMinTiles) || (kl != 4 && kl != 8) ||
         reinterpret_cast<uintptr_t>(call.x) % 16 != 0)
         return false;
     StreamArgs args{};
@@ -4071,8 +4075,9 @@ void gemv_i8_format(hipStream_t stream, const PackedCall &call, void *scratch)
     const uint32_t k_pad = pad_to(call.k, Geo<F>::align);
     const uint32_t groups = k_pad / 128;
     const uint32_t n_tiles = call_tiles(call);
-    // Ternary from kStreamMinTiles row tiles to below the head size: the
-    // streaming kernels before the one-tile-per-block plans.  Measured (us
+    // Ternary from kStreamMinTiles row tiles (two rows from
+    // kStreamTwoRowMinTiles) to below the head size: the streaming kernels
+    // before the one-tile-per-block plans.  Measured (us
     // per launch, A/B on one device), one / two / four / eight rows: 16384 x
     // 2048 5.6 / 9.1 / 9.3 / 14.8 -> 4.5 / 5.3 / 6.2 / 9.5, 32768 x 2048
     // 8.7 / 16.2 / 16.8 / 27.3 -> 5.3 / 6.0 / 6.6 / 9.5, 12288 x 2048 at
