@@ -3642,7 +3642,9 @@ unsigned launch_wide_row(hipStream_t stream, const StreamArgs &args, bool norm, 
     // block per tile: 16384 x 2048 7.1 -> 5.9, 32768 x 2048 12.0 -> 8.5,
     // 49152 x 2048 16.4-18.5 -> 14.6-15.3, 32768 x 1024 7.5 -> 6.0, 16384 x
     // 1024 the same; INT8 measured the same or slower (32768 x 1024 6.9 ->
-    // 7.2, 49152 x 2048 16.4 -> 17.8) and keeps one block per tile.
+    // 7.2, 49152 x 2048 16.4 -> 17.8) and keeps one block per tile, and so
+    // does NF4 below 1024 tiles (R = 1 on 16-wave blocks: 12288 x 2048 6.1
+    // -> 7.2, 10240 x 2048 6.0 -> 7.0, 8192 x 1024 3.9 -> 4.6).
     if constexpr (F == Format::Nf4) {
         if (args.n_tiles < kHeadTiles && args.n_tiles >= kNf4MidTiles && !merge) {
             auto mid = [&](auto r_tag) {
